@@ -1,0 +1,264 @@
+"""Benchmark of the gfx950 GGUF matvec path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-suite]
+
+Headline workload: Q4_K GEMV, W 3584 x 18944 (out x in; the Qwen2.5-7B
+ffn_down shape), batch 1, fp32 x and y. One step = one fused dequant + matvec
+launch over one weight copy. The raw blocks are resident in HBM before the
+timed region, and steps rotate over >= 1 GiB of distinct weight copies so no
+step is served from the 256 MB Infinity Cache.
+
+Printed: ONE JSON line with
+  value      effective GB/s over the whole timed region (K launches,
+             back-to-back on one stream, bracketed by device syncs);
+             effective bytes per step = raw blocks + 4k (x) + 4n (y);
+  roofline   the GEMV kernel against 8 TB/s HBM: achieved = effective bytes
+             per launch / mean kernel duration, timed with HIP events around
+             each launch on the launching stream;
+  cpu_baseline  the reference's native scalar matmul (its own _C module built
+             from its sources, 1 thread) on the same bytes, timed on the host
+             for a bounded number of full-shape repetitions; plus the NumPy path;
+  configs    every other benchmark workload (GB/s, mean kernel us, fraction of
+             HBM peak) and the Llama-3-8B decode-step weight sweep (ms/step).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from flatrun_amd import _lib, device, synth  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+ROTATE_BYTES = 1 << 30         # >= 1 GiB of distinct copies per workload
+
+
+def effective_bytes(q: str, n: int, k: int, batch: int = 1) -> int:
+    return synth.nbytes(q, n, k) + 4 * k * batch + 4 * n * batch
+
+
+class GemvWorkload:
+    """Rotating device copies of one seeded weight, x and y resident in HBM."""
+
+    def __init__(self, q: str, n: int, k: int, seed: int, stream, rotate_bytes: int = ROTATE_BYTES):
+        self.q, self.n, self.k = q, n, k
+        self.raw = synth.make_blocks(q, n, k, seed=seed)
+        self.ncopies = max(2, math.ceil(rotate_bytes / self.raw.nbytes))
+        self.w = [device.DeviceBuffer.from_host(self.raw) for _ in range(self.ncopies)]
+        self.x_host = synth.make_x(k, seed=seed + 1)
+        self.x = device.DeviceBuffer.from_host(self.x_host)
+        self.y = device.DeviceBuffer(4 * n)
+        self.stream = stream
+        self.bytes = effective_bytes(q, n, k)
+
+    def launch(self, i: int) -> None:
+        device.gemv(self.q, self.w[i % self.ncopies], self.x, self.y, self.n, self.k, stream=self.stream,
+                    w_bytes=self.raw.nbytes)
+
+    def result(self) -> np.ndarray:
+        device.synchronize()
+        return self.y.to_host(np.float32)
+
+    def time_throughput(self, steps: int, warmup: int) -> float:
+        """Seconds for `steps` back-to-back launches after `warmup` untimed ones."""
+        for i in range(warmup):
+            self.launch(i)
+        device.synchronize()
+        e0, e1 = device.Event(), device.Event()
+        e0.record(self.stream)
+        for i in range(steps):
+            self.launch(i)
+        e1.record(self.stream)
+        e1.synchronize()
+        device.synchronize()
+        return e0.elapsed_ms(e1) / 1e3
+
+    def time_kernel(self, launches: int) -> float:
+        """Mean per-launch kernel time (s): an event pair around every launch."""
+        evs = [(device.Event(), device.Event()) for _ in range(launches)]
+        for i, (a, b) in enumerate(evs):
+            a.record(self.stream)
+            self.launch(i)
+            b.record(self.stream)
+        device.synchronize()
+        ms = [a.elapsed_ms(b) for a, b in evs]
+        return float(np.mean(ms)) / 1e3
+
+    def free(self) -> None:
+        for b in self.w:
+            b.free()
+        self.x.free()
+        self.y.free()
+
+
+def cpu_baseline(work: GemvWorkload, y_gpu: np.ndarray, seconds: float) -> dict:
+    """The reference's native matmul on the host (oracle/_ref, 1 thread) or, if
+    that build is absent, the C restatement; plus the NumPy path (BLAS)."""
+    from oracle import gguf_np as G
+    from oracle.loader import c_oracle, ref_C
+
+    q, n, k, raw, x = work.q, work.n, work.k, work.raw, work.x_host
+    R = ref_C()
+    if R is not None:
+        fn = getattr(R, f"matmul_{q.lower()}")
+        kind, what = "reference", f"reference _C.matmul_{q.lower()} (src/flatrun_native, scalar x86, 1 thread)"
+        run = lambda: fn(x, raw, n, k)  # noqa: E731
+    else:
+        kind, what = "port", f"C restatement of the reference scalar matmul_{q.lower()} (1 thread)"
+        run = lambda: c_oracle().matmul(q, x, raw, n, k, threads=1)  # noqa: E731
+    y_ref = run()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 200:
+            break
+    gbs = work.bytes * reps / el / 1e9
+    # NumPy path of the reference (dequant + BLAS matvec), all host cores
+    t0 = time.perf_counter()
+    y_np = G.matmul_numpy(q, x, raw, n, k)
+    t_np = time.perf_counter() - t0
+    err = float(np.max(np.abs(y_gpu - y_ref)) / np.max(np.abs(y_ref)))
+    err_np = float(np.max(np.abs(y_gpu - y_np)) / np.max(np.abs(y_np)))
+    return {
+        "value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+        "sample": f"{q} GEMV {n}x{k} b1, full shape x {reps} reps ({el:.1f} s): {what}",
+        "ms_per_step": round(el / reps * 1e3, 3),
+        "numpy_path": {"value": round(work.bytes / t_np / 1e9, 4), "unit": "GB/s", "ms_per_step": round(t_np * 1e3, 2),
+                       "cores": os.cpu_count(), "what": "dequant_q4_k restatement + numpy BLAS matvec"},
+        "gpu_vs_cpu_max_rel_err": err, "gpu_vs_numpy_max_rel_err": err_np,
+    }
+
+
+SUITE = [
+    ("q8_0_4864x896", "Q8_0", 4864, 896),
+    ("q4_k_18944x3584", "Q4_K", 18944, 3584),
+    ("q4_k_3584x18944", "Q4_K", 3584, 18944),
+    ("q6_k_152064x3584", "Q6_K", 152064, 3584),
+    ("q1_0_4096x4096", "Q1_0", 4096, 4096),
+]
+
+# Llama-3-8B Q4_K_M projection mix: (name, quant, out, in)
+LLAMA_LAYER = [
+    ("q", "Q4_K", 4096, 4096), ("k", "Q4_K", 1024, 4096), ("v", "Q6_K", 1024, 4096), ("o", "Q4_K", 4096, 4096),
+    ("gate", "Q4_K", 14336, 4096), ("up", "Q4_K", 14336, 4096), ("down", "Q6_K", 4096, 14336),
+]
+
+
+def run_suite(stream, steps: int) -> dict:
+    out = {}
+    for idx, (name, q, n, k) in enumerate(SUITE):
+        w = GemvWorkload(q, n, k, seed=100 + idx, stream=stream)
+        t = w.time_throughput(steps, warmup=10)
+        tk = w.time_kernel(min(steps, 100))
+        out[name] = {"gbs": round(w.bytes * steps / t / 1e9, 1), "kernel_us": round(tk * 1e6, 2),
+                     "kernel_gbs": round(w.bytes / tk / 1e9, 1), "frac_hbm": round(w.bytes / tk / 1e9 / HBM_PEAK_GBS, 4),
+                     "effective_bytes": w.bytes}
+        w.free()
+    out["llama3_8b_decode_resident"] = decode_sweep_resident(stream, steps=max(3, min(steps // 50, 20)))
+    return out
+
+
+def decode_sweep_resident(stream, steps: int, layers: int = 32) -> dict:
+    """All 32 layers' raw blocks resident in HBM; one step = 224 GEMVs."""
+    host = {name: synth.make_blocks(q, n, k, seed=i) for i, (name, q, n, k) in enumerate(LLAMA_LAYER)}
+    dev = [{name: device.DeviceBuffer.from_host(host[name]) for name, *_ in LLAMA_LAYER} for _ in range(layers)]
+    kmax = max(k for *_, k in LLAMA_LAYER)
+    nmax = max(n for _, _, n, _ in LLAMA_LAYER)
+    x = device.DeviceBuffer.from_host(synth.make_x(kmax, seed=5))
+    y = device.DeviceBuffer(4 * nmax)
+    total = sum(synth.nbytes(q, n, k) for _, q, n, k in LLAMA_LAYER) * layers
+
+    def step():
+        for L in range(layers):
+            for name, q, n, k in LLAMA_LAYER:
+                device.gemv(q, dev[L][name], x, y, n, k, stream=stream, w_bytes=host[name].nbytes)
+
+    step()
+    device.synchronize()
+    e0, e1 = device.Event(), device.Event()
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    for d in dev:
+        for b in d.values():
+            b.free()
+    return {"ms_per_step": round(ms, 4), "weight_bytes_per_step": total, "gemvs_per_step": layers * len(LLAMA_LAYER),
+            "gbs": round(total / (ms / 1e3) / 1e9, 1), "floor_ms_at_8TBs": round(total / 8e12 * 1e3, 4)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-suite", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU (the matvec path is single-device); "
+              f"--gpus {a.gpus} is not supported", file=sys.stderr)
+        return 2
+    _lib.lib()
+    if _lib.device_count() <= 0:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    _lib.check(_lib.lib().frq_set_device(0))
+    stream = device.Stream()
+
+    q, n, k = "Q4_K", 3584, 18944
+    work = GemvWorkload(q, n, k, seed=2024, stream=stream)
+    work.launch(0)
+    y_gpu = work.result()
+    t = work.time_throughput(a.steps, a.warmup)
+    t_kernel = work.time_kernel(min(a.steps, 200))
+    value = work.bytes * a.steps / t / 1e9
+    achieved = work.bytes / t_kernel / 1e9
+    rec = {
+        "metric": "Q4_K GEMV GB/s (% HBM peak) @3584x18944 b1; ms per 8B decode step",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(t / a.steps * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 (Q4_K weights)",
+        "data": "synthetic: seeded GGUF Q4_K blocks (d, dmin ~ U[1e-4, 5e-3], 6-bit scales/mins U[0,63], "
+                "q U[0,15]), x ~ N(0,1)",
+        "config": {"workload": "Q4_K GEMV W[3584 x 18944] (out x in) . x[18944], batch 1",
+                   "effective_bytes_per_step": work.bytes, "weight_copies_rotated": work.ncopies,
+                   "rotation_bytes": work.ncopies * work.raw.nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel_us": round(t_kernel * 1e6, 3)},
+    }
+    if not a.no_suite:
+        rec["configs"] = run_suite(stream, steps=min(a.steps, 500))
+        rec["decode_step_ms_resident"] = rec["configs"]["llama3_8b_decode_resident"]["ms_per_step"]
+    if not a.no_cpu:
+        rec["cpu_baseline"] = cpu_baseline(work, y_gpu, a.cpu_seconds)
+    work.free()
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,189 @@
+"""Drop-in for the reference's pybind11 module ``flatrun_native._C``.
+
+Same function names, argument order, argument conversion and return shapes as
+``src/flatrun_native/_C.cpp:455-488``; each function calls the matching
+``frq_*`` entry point of libfrq_hip.so (include/frq.h), which runs the HIP
+kernels. Arguments are converted the way ``py::array_t<T, c_style |
+forcecast>`` converts them (any ndim, cast to the element type, made
+contiguous). Errors the reference raises as ``std::runtime_error`` arrive as
+:class:`flatrun_amd._lib.FrqError`, a ``RuntimeError``.
+
+Additions beyond the reference module, for the formats it lacks:
+``dequant_q5_k``, ``dequant_q1_0``, ``matmul_q5_k``, ``matmul_q1_0`` and
+their ``_batched`` forms, plus ``dequant(qtype, weight, shape)`` with the NumPy
+decoders' ragged-size rule.
+"""
+
+from __future__ import annotations
+
+import operator
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib, ptr
+
+
+def _size_t(v, what: str) -> int:
+    v = operator.index(v)
+    if v < 0:
+        raise TypeError(f"{what} must be a non-negative integer, got {v}")
+    return v
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def _u8(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint8))
+
+
+def _shape2(shape) -> tuple[int, int]:
+    o, i = shape
+    return int(o), int(i)
+
+
+# ------------------------------------------------------------------ dequant
+
+def dequant_q4_k(weight, shape):
+    """dequant_q4_k(weight_uint8, (out, in)) -> float32 (out, in). _C.cpp:47-86."""
+    w = _u8(weight)
+    o, i = _shape2(shape)
+    out = np.empty((max(o, 0), max(i, 0)), dtype=np.float32)
+    check(lib().frq_dequant_q4_k(ptr(w), w.size, o, i, ptr(out)))
+    return out
+
+
+def dequant_q8_0(weight, shape):
+    """dequant_q8_0(weight_uint8, (out, in)). _C.cpp:285-320."""
+    w = _u8(weight)
+    o, i = _shape2(shape)
+    out = np.empty((max(o, 0), max(i, 0)), dtype=np.float32)
+    check(lib().frq_dequant_q8_0(ptr(w), w.size, o, i, ptr(out)))
+    return out
+
+
+def dequant_q6_k(weight, shape):
+    """dequant_q6_k(weight_uint8, (out, in)). _C.cpp:363-398."""
+    w = _u8(weight)
+    o, i = _shape2(shape)
+    out = np.empty((max(o, 0), max(i, 0)), dtype=np.float32)
+    check(lib().frq_dequant_q6_k(ptr(w), w.size, o, i, ptr(out)))
+    return out
+
+
+def dequant(qtype, weight, shape):
+    """Any supported type, NumPy-decoder size rule (ceil-div blocks, tail
+    trimmed; gguf.py:61-73). Returns float32 of ``shape``."""
+    q = _lib.QTYPES[qtype.upper()] if isinstance(qtype, str) else int(qtype)
+    w = _u8(weight)
+    shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+    n = int(np.prod(shape)) if shape else 1
+    out = np.empty(n, dtype=np.float32)
+    check(lib().frq_dequant(q, ptr(w), w.size, n, ptr(out)))
+    return out.reshape(shape)
+
+
+def dequant_q5_k(weight, shape):
+    return dequant(_lib.Q5_K, weight, shape)
+
+
+def dequant_q1_0(weight, shape):
+    return dequant(_lib.Q1_0, weight, shape)
+
+
+# ------------------------------------------------------------------ matmul
+
+def _matmul_1d(entry, x, weight, n, k):
+    xc, w = _f32(x), _u8(weight)
+    n, k = _size_t(n, "n"), _size_t(k, "k")
+    out = np.empty(n, dtype=np.float32)
+    check(entry(ptr(xc), xc.size, ptr(w), w.size, n, k, ptr(out)))
+    return out
+
+
+def _matmul_2d(entry, x, weight, n, k):
+    xc, w = _f32(x), _u8(weight)
+    n, k = _size_t(n, "n"), _size_t(k, "k")
+    seq = xc.shape[0] if xc.ndim == 2 else 0
+    cols = xc.shape[1] if xc.ndim == 2 else 0
+    out = np.empty((seq, n), dtype=np.float32)
+    check(entry(ptr(xc), xc.ndim, seq, cols, ptr(w), w.size, n, k, ptr(out)))
+    return out
+
+
+def matmul_q4_k(x, weight, n, k):
+    """out[n] = W . x; x has k elements. _C.cpp:99-132."""
+    return _matmul_1d(lib().frq_matmul_q4_k, x, weight, n, k)
+
+
+def matmul_q4_k_batched(x, weight, n, k):
+    """out[seq, n] for x of shape (seq, k). _C.cpp:154-197."""
+    return _matmul_2d(lib().frq_matmul_q4_k_batched, x, weight, n, k)
+
+
+def matmul_q8_0(x, weight, n, k):
+    """_C.cpp:326-357."""
+    return _matmul_1d(lib().frq_matmul_q8_0, x, weight, n, k)
+
+
+def matmul_q8_0_batched(x, weight, n, k):
+    """_C.cpp:199-242."""
+    return _matmul_2d(lib().frq_matmul_q8_0_batched, x, weight, n, k)
+
+
+def matmul_q6_k(x, weight, n, k):
+    """_C.cpp:404-435."""
+    return _matmul_1d(lib().frq_matmul_q6_k, x, weight, n, k)
+
+
+def matmul_q6_k_batched(x, weight, n, k):
+    """_C.cpp:244-283."""
+    return _matmul_2d(lib().frq_matmul_q6_k_batched, x, weight, n, k)
+
+
+def _generic_1d(q: int, name: str):
+    def f(x, weight, n, k):
+        xc, w = _f32(x), _u8(weight)
+        n, k = _size_t(n, "n"), _size_t(k, "k")
+        if xc.size != k:
+            raise _lib.FrqError(_lib.ERR_SHAPE, f"{name} matmul: x.size() != k")
+        out = np.empty(n, dtype=np.float32)
+        check(lib().frq_matmul(q, ptr(xc), 1, ptr(w), w.size, n, k, ptr(out)))
+        return out
+    f.__name__ = f"matmul_{name.lower()}"
+    return f
+
+
+def _generic_2d(q: int, name: str):
+    def f(x, weight, n, k):
+        xc, w = _f32(x), _u8(weight)
+        n, k = _size_t(n, "n"), _size_t(k, "k")
+        if xc.ndim != 2:
+            raise _lib.FrqError(_lib.ERR_SHAPE, f"{name} matmul (batched): x must be 2-D (seq, k)")
+        if xc.shape[1] != k:
+            raise _lib.FrqError(_lib.ERR_SHAPE, f"{name} matmul (batched): x.shape[1] != k")
+        out = np.empty((xc.shape[0], n), dtype=np.float32)
+        check(lib().frq_matmul(q, ptr(xc), xc.shape[0], ptr(w), w.size, n, k, ptr(out)))
+        return out
+    f.__name__ = f"matmul_{name.lower()}_batched"
+    return f
+
+
+matmul_q5_k = _generic_1d(_lib.Q5_K, "Q5_K")
+matmul_q5_k_batched = _generic_2d(_lib.Q5_K, "Q5_K")
+matmul_q1_0 = _generic_1d(_lib.Q1_0, "Q1_0")
+matmul_q1_0_batched = _generic_2d(_lib.Q1_0, "Q1_0")
+
+
+# ------------------------------------------------------------------ diagnostics
+
+def is_neon() -> bool:
+    """Always False (no NEON path). _C.cpp:441-447."""
+    return bool(lib().frq_is_neon())
+
+
+def version() -> str:
+    """Build identifier. _C.cpp:449-451."""
+    return _lib.version()

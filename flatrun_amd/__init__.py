@@ -1,0 +1,202 @@
+"""flatrun_amd -- MI355X (gfx950) GGUF dequant + quantized matvec.
+
+Drop-in for the reference's native accelerator package ``flatrun_native``
+(``src/flatrun_native/python/__init__.py``): the same public names
+(``NativeBackend``, ``Q4K_GEMM_BLOCK``, ``is_available``, ``is_neon``,
+``version``), the same method signatures and dispatch (1-D ``x`` -> matvec,
+2-D ``x`` -> batched), the same exception types (``ValueError`` for a bad
+``x`` shape, ``RuntimeError`` when unavailable or when the kernel rejects a
+layout). The kernels are hand-written HIP for gfx950 reached through ctypes
+(``flatrun_amd._lib``); there is no CPU fallback inside this package --
+``--backend python`` stays the reference's own NumPy path.
+
+Typical use::
+
+    from flatrun_amd import NativeBackend
+    b = NativeBackend()
+    y = b.matmul_q4k(x, raw_q4k_bytes, n, k)          # host buffers
+    w = b.upload(raw_q4k_bytes)                       # resident in HBM
+    y = b.matmul_q4k(x, w, n, k)                      # no weight copy
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from . import _C, _lib
+from ._lib import FrqError, LibraryMissing
+
+__all__ = [
+    "NativeBackend",
+    "DeviceWeight",
+    "Q4K_GEMM_BLOCK",
+    "is_available",
+    "is_neon",
+    "version",
+    "FrqError",
+    "LibraryMissing",
+]
+
+# Block size of the Q4_K format (python/__init__.py:37-38).
+Q4K_GEMM_BLOCK = 256
+
+
+def is_available() -> bool:
+    """True when libfrq_hip.so loads and a HIP device is visible."""
+    try:
+        return _lib.device_count() > 0
+    except (LibraryMissing, FrqError):
+        return False
+
+
+def version() -> str:
+    """Build identifier, or the reason the library is unavailable."""
+    err = _lib.load_error()
+    if err is not None:
+        return f"flatrun_amd (unavailable: {err})"
+    return _C.version()
+
+
+def is_neon() -> bool:
+    """Always False: this build targets gfx950, not ARM NEON."""
+    return False
+
+
+class DeviceWeight:
+    """Raw GGUF block bytes resident in device memory (uploaded once)."""
+
+    def __init__(self, raw: np.ndarray):
+        from .device import DeviceBuffer
+        raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
+        self.nbytes = int(raw.size)
+        self.buffer = DeviceBuffer.from_host(raw)
+
+    def data_ptr(self) -> int:
+        return self.buffer.ptr
+
+
+def _raw_bytes(weight) -> np.ndarray:
+    if hasattr(weight, "as_numpy"):          # reference tensor handle (core/tensor.py)
+        weight = weight.as_numpy()
+    return np.ascontiguousarray(weight, dtype=np.uint8)
+
+
+class NativeBackend:
+    """Facade over the gfx950 kernels; mirrors python/__init__.py:85-227.
+
+    Stateless apart from a device scratch buffer for resident-weight calls;
+    safe to share across threads (host-buffer calls serialise inside the
+    library).
+
+    Attributes
+    ----------
+    available : bool
+        True if the library loaded and a device is visible. Methods on an
+        unavailable backend raise RuntimeError.
+    """
+
+    def __init__(self) -> None:
+        self.available = is_available()
+        self._neon = False
+        self._scratch = None
+
+    # ------------------------------------------------------------ helpers
+    def _require(self) -> None:
+        if not self.available:
+            raise RuntimeError(
+                "flatrun_amd is not available: " + version()
+                + " (build with `python -m flatrun_amd.build` on a host with ROCm; a HIP device is required)")
+
+    def _matmul(self, qname: str, x, weight, n: int, k: int):
+        self._require()
+        x_c = np.ascontiguousarray(x, dtype=np.float32)
+        if isinstance(weight, DeviceWeight):
+            return self._matmul_resident(qname, x_c, weight, n, k)
+        w_c = _raw_bytes(weight)
+        fn1 = getattr(_C, f"matmul_{qname.lower()}")
+        fn2 = getattr(_C, f"matmul_{qname.lower()}_batched")
+        if x_c.ndim == 1:
+            if x_c.shape[0] != k:
+                raise ValueError(f"x.shape[0]={x_c.shape[0]} != k={k}")
+            return fn1(x_c, w_c, int(n), int(k))
+        if x_c.ndim == 2:
+            return fn2(x_c, w_c, int(n), int(k))
+        raise ValueError(f"x must be 1-D or 2-D, got shape {x_c.shape}")
+
+    def _matmul_resident(self, qname: str, x_c: np.ndarray, weight: DeviceWeight, n: int, k: int):
+        from . import device
+        if x_c.ndim == 1:
+            if x_c.shape[0] != k:
+                raise ValueError(f"x.shape[0]={x_c.shape[0]} != k={k}")
+            seq = 1
+        elif x_c.ndim == 2:
+            if x_c.shape[1] != k:
+                raise FrqError(_lib.ERR_SHAPE, f"{qname} matmul (batched): x.shape[1] != k")
+            seq = x_c.shape[0]
+        else:
+            raise ValueError(f"x must be 1-D or 2-D, got shape {x_c.shape}")
+        n, k = int(n), int(k)
+        out = np.empty((seq, n), dtype=np.float32)
+        if seq and n:
+            xb = (seq * k * 4 + 255) // 256 * 256
+            need = xb + seq * n * 4
+            if self._scratch is None or self._scratch.nbytes < need:
+                self._scratch = device.DeviceBuffer(need)
+            base = self._scratch.ptr
+            if x_c.size:
+                _lib.check(_lib.lib().frq_memcpy_h2d(base, x_c.ctypes.data, x_c.nbytes))
+            device.gemv(qname, weight.buffer, base, base + xb, n, k, batch=seq, w_bytes=weight.nbytes)
+            _lib.check(_lib.lib().frq_memcpy_d2h(out.ctypes.data, base + xb, out.nbytes))
+        return out[0] if x_c.ndim == 1 else out
+
+    def upload(self, weight) -> DeviceWeight:
+        """Copy raw block bytes to device memory once; pass the result as
+        ``weight`` to any matmul to skip the per-call weight copy."""
+        self._require()
+        return DeviceWeight(_raw_bytes(weight))
+
+    # ------------------------------------------------------------ matmuls
+    def matmul_q4k(self, x, weight, n: int, k: int):
+        """Fused Q4_K dequant + matvec. x (k,) -> (n,), x (seq, k) -> (seq, n)."""
+        return self._matmul("Q4_K", x, weight, n, k)
+
+    def matmul_q8_0(self, x, weight, n: int, k: int):
+        """Fused Q8_0 dequant + matvec (python/__init__.py:155-182)."""
+        return self._matmul("Q8_0", x, weight, n, k)
+
+    def matmul_q6_k(self, x, weight, n: int, k: int):
+        """Fused Q6_K dequant + matvec (python/__init__.py:184-209)."""
+        return self._matmul("Q6_K", x, weight, n, k)
+
+    # the runtime backend's spelling (runtime/backend.py:111, 273)
+    matmul_q6k = matmul_q6_k
+
+    def matmul_q5_k(self, x, weight, n: int, k: int):
+        """Fused Q5_K dequant + matvec (no native counterpart in the reference)."""
+        return self._matmul("Q5_K", x, weight, n, k)
+
+    def matmul_q1_0(self, x, weight, n: int, k: int):
+        """Fused Q1_0 dequant + matvec (no native counterpart in the reference)."""
+        return self._matmul("Q1_0", x, weight, n, k)
+
+    # ------------------------------------------------------------ dequant
+    def dequant_q4k(self, weight, shape: tuple[int, int]):
+        """Pure Q4_K dequant to f32 (out, in) (python/__init__.py:211-227)."""
+        self._require()
+        return _C.dequant_q4_k(_raw_bytes(weight), shape)
+
+    def dequant_q8_0(self, weight, shape: tuple[int, int]):
+        self._require()
+        return _C.dequant_q8_0(_raw_bytes(weight), shape)
+
+    def dequant_q6_k(self, weight, shape: tuple[int, int]):
+        self._require()
+        return _C.dequant_q6_k(_raw_bytes(weight), shape)
+
+    def dequant_q5_k(self, weight, shape):
+        self._require()
+        return _C.dequant_q5_k(_raw_bytes(weight), shape)
+
+    def dequant_q1_0(self, weight, shape):
+        self._require()
+        return _C.dequant_q1_0(_raw_bytes(weight), shape)

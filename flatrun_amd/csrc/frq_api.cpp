@@ -1,0 +1,412 @@
+// C-ABI layer of libfrq_hip.so (declared in include/frq.h).
+//
+// Validation mirrors the reference's pybind11 module (src/flatrun_native/
+// _C.cpp): the same checks in the same order with the same messages, so a
+// caller that maps FRQ_ERR_SHAPE / FRQ_ERR_SIZE to RuntimeError sees the
+// errors the reference raises. Host-buffer calls stage through one
+// grow-only device workspace per device, serialised by a mutex (the
+// reference holds the GIL for the whole call, so it is serial too).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/frq.h"
+#include "frq_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(FRQ_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+#define FRQ_HIP(call)                                   \
+    do {                                                \
+        hipError_t e_ = (call);                         \
+        if (e_ != hipSuccess) return hip_fail(e_, #call); \
+    } while (0)
+
+struct Fmt {
+    const char* name;
+    int64_t bbytes, belems;
+};
+
+bool fmt_of(int qtype, Fmt* f) {
+    switch (qtype) {
+        case FRQ_Q8_0: *f = {"Q8_0", 34, 32}; return true;
+        case FRQ_Q4_K: *f = {"Q4_K", 144, 256}; return true;
+        case FRQ_Q5_K: *f = {"Q5_K", 176, 256}; return true;
+        case FRQ_Q6_K: *f = {"Q6_K", 210, 256}; return true;
+        case FRQ_Q1_0: *f = {"Q1_0", 18, 128}; return true;
+        default: return false;
+    }
+}
+
+int have_device() {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        return fail(FRQ_ERR_NO_DEVICE, "no HIP device available");
+    }
+    return FRQ_OK;
+}
+
+// Grow-only staging buffer on the current device.
+struct Workspace {
+    std::mutex mu;
+    std::vector<void*> ptr;
+    std::vector<size_t> cap;
+};
+Workspace g_ws;
+
+// Returns a device buffer of >= bytes on the current device; caller holds g_ws.mu.
+int workspace(size_t bytes, void** out) {
+    int dev = 0;
+    FRQ_HIP(hipGetDevice(&dev));
+    if ((size_t)dev >= g_ws.ptr.size()) {
+        g_ws.ptr.resize(dev + 1, nullptr);
+        g_ws.cap.resize(dev + 1, 0);
+    }
+    if (g_ws.cap[dev] < bytes) {
+        if (g_ws.ptr[dev]) FRQ_HIP(hipFree(g_ws.ptr[dev]));
+        g_ws.ptr[dev] = nullptr;
+        g_ws.cap[dev] = 0;
+        size_t want = bytes < (size_t)1 << 20 ? (size_t)1 << 20 : bytes;
+        FRQ_HIP(hipMalloc(&g_ws.ptr[dev], want));
+        g_ws.cap[dev] = want;
+    }
+    *out = g_ws.ptr[dev];
+    return FRQ_OK;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Host dequant: stage weight, decode, copy back. n_elems may be ragged.
+int host_dequant(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, float* out) {
+    if (n_elems == 0) return FRQ_OK;
+    if (int rc = have_device()) return rc;
+    std::lock_guard<std::mutex> lk(g_ws.mu);
+    const size_t wb = align256(weight_bytes), yb = align256((size_t)n_elems * 4);
+    void* base = nullptr;
+    if (int rc = workspace(wb + yb, &base)) return rc;
+    uint8_t* dw = static_cast<uint8_t*>(base);
+    float* dy = reinterpret_cast<float*>(dw + wb);
+    FRQ_HIP(hipMemcpy(dw, weight, weight_bytes, hipMemcpyHostToDevice));
+    FRQ_HIP(frq::launch_dequant(qtype, dw, dy, n_elems, nullptr));
+    FRQ_HIP(hipMemcpy(out, dy, (size_t)n_elems * 4, hipMemcpyDeviceToHost));
+    return FRQ_OK;
+}
+
+// Host matmul over seq rows of x (already validated).
+int host_matmul(int qtype, const float* x, size_t seq, const uint8_t* weight, size_t weight_bytes, size_t n,
+                size_t k, float* out) {
+    if (seq == 0 || n == 0) return FRQ_OK;
+    if (k == 0) {   // empty dot products: the reference's accumulators stay 0
+        std::memset(out, 0, seq * n * sizeof(float));
+        return FRQ_OK;
+    }
+    if (int rc = have_device()) return rc;
+    if (!frq::gemv_supported(qtype, (int64_t)n, (int64_t)k))
+        return fail(FRQ_ERR_UNSUPPORTED, "matmul: k=%zu is beyond the single-workgroup row limit of this build", k);
+    std::lock_guard<std::mutex> lk(g_ws.mu);
+    const size_t wb = align256(weight_bytes), xb = align256(seq * k * 4), yb = align256(seq * n * 4);
+    void* base = nullptr;
+    if (int rc = workspace(wb + xb + yb, &base)) return rc;
+    uint8_t* dw = static_cast<uint8_t*>(base);
+    float* dx = reinterpret_cast<float*>(dw + wb);
+    float* dy = reinterpret_cast<float*>(dw + wb + xb);
+    FRQ_HIP(hipMemcpy(dw, weight, weight_bytes, hipMemcpyHostToDevice));
+    FRQ_HIP(hipMemcpy(dx, x, seq * k * 4, hipMemcpyHostToDevice));
+    for (size_t s = 0; s < seq; ++s)
+        FRQ_HIP(frq::launch_gemv(qtype, dw, dx + s * k, dy + s * n, (int64_t)n, (int64_t)k, nullptr, nullptr));
+    FRQ_HIP(hipMemcpy(out, dy, seq * n * 4, hipMemcpyDeviceToHost));
+    return FRQ_OK;
+}
+
+// _C.cpp dequant_<q>_py checks (e.g. :54-67).
+int check_dequant_2d(const Fmt& f, size_t weight_bytes, int64_t out_dim, int64_t in_dim) {
+    if (out_dim < 0 || in_dim < 0) return fail(FRQ_ERR_SHAPE, "%s: negative shape", f.name);
+    const int64_t total = out_dim * in_dim;
+    if (total % f.belems != 0)
+        return fail(FRQ_ERR_SHAPE, "%s tensor element count must be a multiple of %lld", f.name, (long long)f.belems);
+    const int64_t nblk = total / f.belems;
+    if ((int64_t)weight_bytes != nblk * f.bbytes)
+        return fail(FRQ_ERR_SIZE, "%s weight byte size mismatch: expected %lld bytes, got %zu", f.name,
+                    (long long)(nblk * f.bbytes), weight_bytes);
+    return FRQ_OK;
+}
+
+// _C.cpp matmul_<q>_py checks (e.g. :105-120).
+int check_matmul(const Fmt& f, size_t x_len, size_t weight_bytes, size_t n, size_t k) {
+    if (k % (size_t)f.belems != 0)
+        return fail(FRQ_ERR_SHAPE, "%s matmul: in_features must be a multiple of %lld", f.name, (long long)f.belems);
+    if (x_len != k) return fail(FRQ_ERR_SHAPE, "%s matmul: x.size() != k", f.name);
+    if (weight_bytes != n * (k / (size_t)f.belems) * (size_t)f.bbytes)
+        return fail(FRQ_ERR_SIZE, "%s matmul: weight byte size mismatch", f.name);
+    return FRQ_OK;
+}
+
+// _C.cpp matmul_<q>_batched_py checks (e.g. :160-182).
+int check_batched(const Fmt& f, int x_ndim, size_t x_cols, size_t weight_bytes, size_t n, size_t k) {
+    if (k % (size_t)f.belems != 0)
+        return fail(FRQ_ERR_SHAPE, "%s matmul (batched): in_features must be a multiple of %lld", f.name,
+                    (long long)f.belems);
+    if (x_ndim != 2) return fail(FRQ_ERR_SHAPE, "%s matmul (batched): x must be 2-D (seq, k)", f.name);
+    if (x_cols != k) return fail(FRQ_ERR_SHAPE, "%s matmul (batched): x.shape[1] != k", f.name);
+    if (weight_bytes != n * (k / (size_t)f.belems) * (size_t)f.bbytes)
+        return fail(FRQ_ERR_SIZE, "%s matmul (batched): weight byte size mismatch", f.name);
+    return FRQ_OK;
+}
+
+int dequant_2d(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t out_dim, int64_t in_dim, float* out) {
+    Fmt f;
+    fmt_of(qtype, &f);
+    if (int rc = check_dequant_2d(f, weight_bytes, out_dim, in_dim)) return rc;
+    if ((!weight && weight_bytes) || (!out && out_dim * in_dim)) return fail(FRQ_ERR_INVALID, "null buffer");
+    return host_dequant(qtype, weight, weight_bytes, out_dim * in_dim, out);
+}
+
+int matmul_1d(int qtype, const float* x, size_t x_len, const uint8_t* weight, size_t weight_bytes, size_t n, size_t k,
+              float* out) {
+    Fmt f;
+    fmt_of(qtype, &f);
+    if (int rc = check_matmul(f, x_len, weight_bytes, n, k)) return rc;
+    if ((!x && k) || (!weight && weight_bytes) || (!out && n)) return fail(FRQ_ERR_INVALID, "null buffer");
+    return host_matmul(qtype, x, 1, weight, weight_bytes, n, k, out);
+}
+
+int matmul_2d(int qtype, const float* x, int x_ndim, size_t seq, size_t x_cols, const uint8_t* weight,
+              size_t weight_bytes, size_t n, size_t k, float* out) {
+    Fmt f;
+    fmt_of(qtype, &f);
+    if (int rc = check_batched(f, x_ndim, x_cols, weight_bytes, n, k)) return rc;
+    if ((!x && seq * k) || (!weight && weight_bytes) || (!out && seq * n)) return fail(FRQ_ERR_INVALID, "null buffer");
+    return host_matmul(qtype, x, seq, weight, weight_bytes, n, k, out);
+}
+
+int check_dev_ptrs(int qtype, const void* w, const float* x, const float* y) {
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
+    const bool k_quant16 = qtype == FRQ_Q4_K || qtype == FRQ_Q5_K;
+    if (k_quant16 ? (wa & 15) : (wa & 1)) return fail(FRQ_ERR_ALIGN, "weight pointer misaligned for its format");
+    if (x && (reinterpret_cast<uintptr_t>(x) & 15)) return fail(FRQ_ERR_ALIGN, "x must be 16-byte aligned");
+    if (y && (reinterpret_cast<uintptr_t>(y) & 3)) return fail(FRQ_ERR_ALIGN, "y must be 4-byte aligned");
+    return FRQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* frq_version(void) { return "flatrun_amd 0.1.0 (gfx950 HIP: Q8_0, Q4_K, Q5_K, Q6_K, Q1_0)"; }
+int frq_is_neon(void) { return 0; }
+const char* frq_last_error(void) { return g_err.c_str(); }
+
+int frq_device_count(int* count) {
+    if (!count) return fail(FRQ_ERR_INVALID, "null count");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        n = 0;
+    }
+    *count = n;
+    return FRQ_OK;
+}
+
+int frq_block_info(int qtype, int64_t* block_bytes, int64_t* block_elems) {
+    Fmt f;
+    if (!fmt_of(qtype, &f)) return fail(FRQ_ERR_INVALID, "unknown quant type %d", qtype);
+    if (block_bytes) *block_bytes = f.bbytes;
+    if (block_elems) *block_elems = f.belems;
+    return FRQ_OK;
+}
+
+int frq_dequant_q4_k(const uint8_t* w, size_t wb, int64_t o, int64_t i, float* out) { return dequant_2d(FRQ_Q4_K, w, wb, o, i, out); }
+int frq_dequant_q8_0(const uint8_t* w, size_t wb, int64_t o, int64_t i, float* out) { return dequant_2d(FRQ_Q8_0, w, wb, o, i, out); }
+int frq_dequant_q6_k(const uint8_t* w, size_t wb, int64_t o, int64_t i, float* out) { return dequant_2d(FRQ_Q6_K, w, wb, o, i, out); }
+
+int frq_dequant(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, float* out) {
+    Fmt f;
+    if (!fmt_of(qtype, &f)) return fail(FRQ_ERR_INVALID, "unknown quant type %d", qtype);
+    if (n_elems < 0) return fail(FRQ_ERR_SHAPE, "%s: negative element count", f.name);
+    const int64_t nblk = (n_elems + f.belems - 1) / f.belems;
+    if ((int64_t)weight_bytes != nblk * f.bbytes)
+        return fail(FRQ_ERR_SIZE, "%s weight byte size mismatch: expected %lld bytes, got %zu", f.name,
+                    (long long)(nblk * f.bbytes), weight_bytes);
+    if ((!weight && weight_bytes) || (!out && n_elems)) return fail(FRQ_ERR_INVALID, "null buffer");
+    return host_dequant(qtype, weight, weight_bytes, n_elems, out);
+}
+
+int frq_matmul_q4_k(const float* x, size_t xl, const uint8_t* w, size_t wb, size_t n, size_t k, float* out) { return matmul_1d(FRQ_Q4_K, x, xl, w, wb, n, k, out); }
+int frq_matmul_q8_0(const float* x, size_t xl, const uint8_t* w, size_t wb, size_t n, size_t k, float* out) { return matmul_1d(FRQ_Q8_0, x, xl, w, wb, n, k, out); }
+int frq_matmul_q6_k(const float* x, size_t xl, const uint8_t* w, size_t wb, size_t n, size_t k, float* out) { return matmul_1d(FRQ_Q6_K, x, xl, w, wb, n, k, out); }
+
+int frq_matmul_q4_k_batched(const float* x, int nd, size_t seq, size_t xc, const uint8_t* w, size_t wb, size_t n, size_t k, float* out) {
+    return matmul_2d(FRQ_Q4_K, x, nd, seq, xc, w, wb, n, k, out);
+}
+int frq_matmul_q8_0_batched(const float* x, int nd, size_t seq, size_t xc, const uint8_t* w, size_t wb, size_t n, size_t k, float* out) {
+    return matmul_2d(FRQ_Q8_0, x, nd, seq, xc, w, wb, n, k, out);
+}
+int frq_matmul_q6_k_batched(const float* x, int nd, size_t seq, size_t xc, const uint8_t* w, size_t wb, size_t n, size_t k, float* out) {
+    return matmul_2d(FRQ_Q6_K, x, nd, seq, xc, w, wb, n, k, out);
+}
+
+int frq_matmul(int qtype, const float* x, size_t seq, const uint8_t* weight, size_t weight_bytes, size_t n, size_t k,
+               float* out) {
+    Fmt f;
+    if (!fmt_of(qtype, &f)) return fail(FRQ_ERR_INVALID, "unknown quant type %d", qtype);
+    return matmul_2d(qtype, x, 2, seq, k, weight, weight_bytes, n, k, out);
+}
+
+int frq_dev_dequant(int qtype, const void* w, size_t w_bytes, int64_t n_elems, float* y, void* stream) {
+    Fmt f;
+    if (!fmt_of(qtype, &f)) return fail(FRQ_ERR_INVALID, "unknown quant type %d", qtype);
+    if (n_elems < 0) return fail(FRQ_ERR_SHAPE, "%s: negative element count", f.name);
+    const int64_t nblk = (n_elems + f.belems - 1) / f.belems;
+    if ((int64_t)w_bytes != nblk * f.bbytes)
+        return fail(FRQ_ERR_SIZE, "%s weight byte size mismatch: expected %lld bytes, got %zu", f.name,
+                    (long long)(nblk * f.bbytes), w_bytes);
+    if (n_elems == 0) return FRQ_OK;
+    if (!w || !y) return fail(FRQ_ERR_INVALID, "null buffer");
+    if (int rc = check_dev_ptrs(qtype, w, nullptr, y)) return rc;
+    FRQ_HIP(frq::launch_dequant(qtype, static_cast<const uint8_t*>(w), y, n_elems, static_cast<hipStream_t>(stream)));
+    return FRQ_OK;
+}
+
+static int dev_gemv_checks(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
+                           int64_t batch, Fmt* f) {
+    if (!fmt_of(qtype, f)) return fail(FRQ_ERR_INVALID, "unknown quant type %d", qtype);
+    if (n < 0 || k < 0 || batch < 0) return fail(FRQ_ERR_SHAPE, "%s: negative shape", f->name);
+    if (k % f->belems) return fail(FRQ_ERR_SHAPE, "%s matmul: in_features must be a multiple of %lld", f->name, (long long)f->belems);
+    if ((int64_t)w_bytes != n * (k / f->belems) * f->bbytes)
+        return fail(FRQ_ERR_SIZE, "%s matmul: weight byte size mismatch", f->name);
+    if (n == 0 || batch == 0) return FRQ_OK;
+    if (!w || !x || !y) return fail(FRQ_ERR_INVALID, "null buffer");
+    if (int rc = check_dev_ptrs(qtype, w, x, y)) return rc;
+    if (k > 0 && !frq::gemv_supported(qtype, n, k))
+        return fail(FRQ_ERR_UNSUPPORTED, "%s matmul: k=%lld is beyond the single-workgroup row limit of this build",
+                    f->name, (long long)k);
+    return FRQ_OK;
+}
+
+int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
+                 int64_t batch, void* stream) {
+    Fmt f;
+    if (int rc = dev_gemv_checks(qtype, w, w_bytes, x, y, n, k, batch, &f)) return rc;
+    if (n == 0 || batch == 0) return FRQ_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (k == 0) {   // empty dot products are 0; a kernel fill keeps the call graph-capturable
+        FRQ_HIP(frq::launch_fill(y, 0.0f, batch * n, s));
+        return FRQ_OK;
+    }
+    for (int64_t b = 0; b < batch; ++b)
+        FRQ_HIP(frq::launch_gemv(qtype, static_cast<const uint8_t*>(w), x + b * k, y + b * n, n, k, nullptr, s));
+    return FRQ_OK;
+}
+
+int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
+                       int* cpl, int* rows_per_wg, int* unroll, int* waves, void* stream) {
+    Fmt f;
+    if (int rc = dev_gemv_checks(qtype, w, w_bytes, x, y, n, k, 1, &f)) return rc;
+    if (n == 0 || k == 0) return fail(FRQ_ERR_SHAPE, "tuned gemv needs n > 0 and k > 0");
+    frq::GemvPlan p;
+    p.cpl = cpl ? *cpl : 0;
+    p.rows_per_wg = rows_per_wg ? *rows_per_wg : 0;
+    p.unroll = unroll ? *unroll : 0;
+    hipError_t e = frq::launch_gemv(qtype, static_cast<const uint8_t*>(w), x, y, n, k, &p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "launch_gemv");
+    if (cpl) *cpl = p.cpl;
+    if (rows_per_wg) *rows_per_wg = p.rows_per_wg;
+    if (unroll) *unroll = p.unroll;
+    if (waves) *waves = p.waves;
+    return FRQ_OK;
+}
+
+int frq_dev_copy(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes % 16) return fail(FRQ_ERR_INVALID, "copy size must be a multiple of 16 bytes");
+    if (((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15) != 0)
+        return fail(FRQ_ERR_ALIGN, "copy buffers must be 16-byte aligned");
+    if (bytes == 0) return FRQ_OK;
+    if (!dst || !src) return fail(FRQ_ERR_INVALID, "null buffer");
+    FRQ_HIP(frq::launch_copy(dst, src, (int64_t)bytes, static_cast<hipStream_t>(stream)));
+    return FRQ_OK;
+}
+
+int frq_set_device(int device) { FRQ_HIP(hipSetDevice(device)); return FRQ_OK; }
+int frq_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(FRQ_ERR_INVALID, "null ptr");
+    FRQ_HIP(hipMalloc(ptr, bytes ? bytes : 1));
+    return FRQ_OK;
+}
+int frq_free(void* ptr) { FRQ_HIP(hipFree(ptr)); return FRQ_OK; }
+int frq_host_alloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(FRQ_ERR_INVALID, "null ptr");
+    FRQ_HIP(hipHostMalloc(ptr, bytes ? bytes : 1, hipHostMallocDefault));
+    return FRQ_OK;
+}
+int frq_host_free(void* ptr) { FRQ_HIP(hipHostFree(ptr)); return FRQ_OK; }
+int frq_memcpy_h2d(void* d, const void* s, size_t b) { FRQ_HIP(hipMemcpy(d, s, b, hipMemcpyHostToDevice)); return FRQ_OK; }
+int frq_memcpy_d2h(void* d, const void* s, size_t b) { FRQ_HIP(hipMemcpy(d, s, b, hipMemcpyDeviceToHost)); return FRQ_OK; }
+int frq_memcpy_h2d_async(void* d, const void* s, size_t b, void* st) {
+    FRQ_HIP(hipMemcpyAsync(d, s, b, hipMemcpyHostToDevice, static_cast<hipStream_t>(st)));
+    return FRQ_OK;
+}
+int frq_memcpy_d2h_async(void* d, const void* s, size_t b, void* st) {
+    FRQ_HIP(hipMemcpyAsync(d, s, b, hipMemcpyDeviceToHost, static_cast<hipStream_t>(st)));
+    return FRQ_OK;
+}
+int frq_memset_async(void* d, int v, size_t b, void* st) {
+    FRQ_HIP(hipMemsetAsync(d, v, b, static_cast<hipStream_t>(st)));
+    return FRQ_OK;
+}
+int frq_stream_create(void** s) {
+    if (!s) return fail(FRQ_ERR_INVALID, "null stream");
+    hipStream_t st = nullptr;
+    FRQ_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    *s = st;
+    return FRQ_OK;
+}
+int frq_stream_destroy(void* s) { FRQ_HIP(hipStreamDestroy(static_cast<hipStream_t>(s))); return FRQ_OK; }
+int frq_stream_synchronize(void* s) { FRQ_HIP(hipStreamSynchronize(static_cast<hipStream_t>(s))); return FRQ_OK; }
+int frq_stream_wait_event(void* s, void* e) {
+    FRQ_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(s), static_cast<hipEvent_t>(e), 0));
+    return FRQ_OK;
+}
+int frq_event_create(void** e) {
+    if (!e) return fail(FRQ_ERR_INVALID, "null event");
+    hipEvent_t ev = nullptr;
+    FRQ_HIP(hipEventCreate(&ev));
+    *e = ev;
+    return FRQ_OK;
+}
+int frq_event_destroy(void* e) { FRQ_HIP(hipEventDestroy(static_cast<hipEvent_t>(e))); return FRQ_OK; }
+int frq_event_record(void* e, void* s) {
+    FRQ_HIP(hipEventRecord(static_cast<hipEvent_t>(e), static_cast<hipStream_t>(s)));
+    return FRQ_OK;
+}
+int frq_event_synchronize(void* e) { FRQ_HIP(hipEventSynchronize(static_cast<hipEvent_t>(e))); return FRQ_OK; }
+int frq_event_elapsed_ms(float* ms, void* a, void* b) {
+    if (!ms) return fail(FRQ_ERR_INVALID, "null ms");
+    FRQ_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(a), static_cast<hipEvent_t>(b)));
+    return FRQ_OK;
+}
+int frq_device_synchronize(void) { FRQ_HIP(hipDeviceSynchronize()); return FRQ_OK; }
+
+}  // extern "C"

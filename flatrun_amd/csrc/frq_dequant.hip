@@ -1,0 +1,172 @@
+// GGUF block dequant kernels for gfx950: raw blocks in HBM -> fp32.
+//
+// Bit-exact contract with the reference NumPy decoders
+// (src/flatrun/dequant/gguf.py), which fixes the rounding sequence:
+//   Q8_0  fl32(q * d)                                     gguf.py:112-127
+//   Q4_K  fl32(fl32(fl32(d*sc) * q) - fl32(dmin*m))       gguf.py:166-220
+//   Q5_K  fl32(fl64(fl32(d*sc) * v) - fl32(dmin*m))       gguf.py:223-263
+//   Q6_K  fl32(fl32(d*sc) * (q - 32))                     gguf.py:365-420
+//   Q1_0  +d / -d by bit, LSB first                       gguf.py:266-299
+// This translation unit is built with -ffp-contract=off, so none of the
+// products above is fused into the following add.
+//
+// Work mapping: one thread writes four consecutive outputs (one dwordx4
+// store), so a wavefront writes 1 KiB of contiguous fp32 and the stores are
+// fully coalesced; the kernel is bound by the 4 B/element write stream. The
+// four outputs always share one scale, so each thread decodes one scale pair.
+// A ragged last block (element count not a multiple of the block) is decoded
+// and the tail trimmed, as the reference's _finish does (gguf.py:61-73).
+#include "frq_common.h"
+#include "frq_kernels.h"
+
+namespace frq {
+
+__device__ __forceinline__ void store4(float* __restrict__ y, int64_t e0, int64_t n, float v0, float v1,
+                                       float v2, float v3) {
+    if (e0 + 3 < n && ((reinterpret_cast<uintptr_t>(y + e0) & 15) == 0)) {
+        *reinterpret_cast<float4*>(y + e0) = make_float4(v0, v1, v2, v3);
+    } else {
+        if (e0 + 0 < n) y[e0 + 0] = v0;
+        if (e0 + 1 < n) y[e0 + 1] = v1;
+        if (e0 + 2 < n) y[e0 + 2] = v2;
+        if (e0 + 3 < n) y[e0 + 3] = v3;
+    }
+}
+
+__device__ __forceinline__ float ub(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
+
+__global__ void __launch_bounds__(256) dequant_q4_k_kernel(const uint8_t* __restrict__ w,
+                                                           float* __restrict__ y, int64_t n) {
+    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (e0 >= n) return;
+    const int64_t b = e0 / kQKElems;
+    const int o = (int)(e0 % kQKElems);
+    const int j = o >> 5, i = o & 31, g = j >> 1;
+    const uint8_t* blk = w + b * kQ4KBytes;
+    const uint4 hd = *reinterpret_cast<const uint4*>(blk);
+    uint32_t sc, m;
+    k4_scale_min(hd.y, hd.z, hd.w, j, sc, m);
+    const float s = f16_bits_to_f32(hd.x) * (float)sc;
+    const float t = f16_bits_to_f32(hd.x >> 16) * (float)m;
+    uint32_t q = *reinterpret_cast<const uint32_t*>(blk + 16 + 32 * g + i);
+    q = (j & 1) ? (q >> 4) : q;
+    q &= 0x0F0F0F0Fu;
+    store4(y, e0, n, s * ub(q, 0) - t, s * ub(q, 1) - t, s * ub(q, 2) - t, s * ub(q, 3) - t);
+}
+
+__global__ void __launch_bounds__(256) dequant_q5_k_kernel(const uint8_t* __restrict__ w,
+                                                           float* __restrict__ y, int64_t n) {
+    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (e0 >= n) return;
+    const int64_t b = e0 / kQKElems;
+    const int o = (int)(e0 % kQKElems);
+    const int j = o >> 5, i = o & 31, g = j >> 1;
+    const uint8_t* blk = w + b * kQ5KBytes;
+    const uint4 hd = *reinterpret_cast<const uint4*>(blk);
+    uint32_t sc, m;
+    k4_scale_min(hd.y, hd.z, hd.w, j, sc, m);
+    const double s = (double)(f16_bits_to_f32(hd.x) * (float)sc);   // fl32(d*sc), widened exactly
+    const double t = (double)(f16_bits_to_f32(hd.x >> 16) * (float)m);
+    uint32_t q = *reinterpret_cast<const uint32_t*>(blk + 48 + 32 * g + i);
+    q = ((j & 1) ? (q >> 4) : q) & 0x0F0F0F0Fu;
+    const uint32_t h = (*reinterpret_cast<const uint32_t*>(blk + 16 + i) >> j) & 0x01010101u;
+    q |= h << 4;                                                         // v = q4 + 16*bit, exact
+    float v[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = (float)(s * (double)((q >> (8 * c)) & 0xFFu) - t);
+    store4(y, e0, n, v[0], v[1], v[2], v[3]);
+}
+
+__global__ void __launch_bounds__(256) dequant_q6_k_kernel(const uint8_t* __restrict__ w,
+                                                           float* __restrict__ y, int64_t n) {
+    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (e0 >= n) return;
+    const int64_t b = e0 / kQKElems;
+    const int o = (int)(e0 % kQKElems);
+    const int h = o >> 7, k = (o >> 5) & 3, l = o & 31;   // element 128h + 32k + l
+    const uint8_t* blk = w + b * kQ6KBytes;
+    uint32_t nib = ld_u32_a2(blk + 64 * h + 32 * (k & 1) + l);
+    nib = ((k >= 2) ? (nib >> 4) : nib) & 0x0F0F0F0Fu;
+    const uint32_t hb = (ld_u32_a2(blk + 128 + 32 * h + l) >> (2 * k)) & 0x03030303u;
+    const uint32_t q = nib | (hb << 4);
+    const int sc = (int)(int8_t)blk[192 + 8 * h + (l >> 4) + 2 * k];
+    const float s = f16_bits_to_f32(ld_u16(blk + 208)) * (float)sc;
+    store4(y, e0, n, s * (ub(q, 0) - 32.0f), s * (ub(q, 1) - 32.0f), s * (ub(q, 2) - 32.0f),
+           s * (ub(q, 3) - 32.0f));
+}
+
+__global__ void __launch_bounds__(256) dequant_q8_0_kernel(const uint8_t* __restrict__ w,
+                                                           float* __restrict__ y, int64_t n) {
+    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (e0 >= n) return;
+    const int64_t b = e0 / kQ80Elems;
+    const int o = (int)(e0 % kQ80Elems);
+    const uint8_t* blk = w + b * kQ80Bytes;
+    const float d = f16_bits_to_f32(ld_u16(blk));
+    const uint32_t q = ld_u32_a2(blk + 2 + o);
+    float v[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = (float)(int)(int8_t)((q >> (8 * c)) & 0xFFu) * d;
+    store4(y, e0, n, v[0], v[1], v[2], v[3]);
+}
+
+__global__ void __launch_bounds__(256) dequant_q1_0_kernel(const uint8_t* __restrict__ w,
+                                                           float* __restrict__ y, int64_t n) {
+    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (e0 >= n) return;
+    const int64_t b = e0 / kQ10Elems;
+    const int o = (int)(e0 % kQ10Elems);
+    const uint8_t* blk = w + b * kQ10Bytes;
+    const float d = f16_bits_to_f32(ld_u16(blk));
+    const uint32_t bits = (uint32_t)blk[2 + (o >> 3)] >> (o & 7);
+    float v[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = ((bits >> c) & 1u) ? d : -d;
+    store4(y, e0, n, v[0], v[1], v[2], v[3]);
+}
+
+__global__ void __launch_bounds__(256) fill_kernel(float* __restrict__ y, float v, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = v;
+}
+
+hipError_t launch_fill(float* y, float value, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    fill_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream>>>(y, value, n);
+    return hipGetLastError();
+}
+
+// Plain streaming copy (16 B per lane, grid-stride). Used to calibrate the
+// HBM traffic counters against a kernel whose traffic is known exactly.
+__global__ void __launch_bounds__(256) copy16_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src,
+                                                     int64_t n16) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+hipError_t launch_copy(void* dst, const void* src, int64_t bytes, hipStream_t stream) {
+    if (bytes <= 0) return hipSuccess;
+    const int64_t n16 = bytes / 16;
+    const int64_t blocks = (n16 + 255) / 256;
+    copy16_kernel<<<dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256), 0, stream>>>(
+        static_cast<uint4*>(dst), static_cast<const uint4*>(src), n16);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant(int qtype, const uint8_t* w, float* y, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int64_t threads = (n + 3) / 4;
+    const dim3 block(256);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    switch (qtype) {
+        case kTypeQ4K: dequant_q4_k_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
+        case kTypeQ5K: dequant_q5_k_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
+        case kTypeQ6K: dequant_q6_k_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
+        case kTypeQ80: dequant_q8_0_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
+        case kTypeQ10: dequant_q1_0_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace frq

@@ -1,0 +1,648 @@
+// Fused dequant + matvec (GEMV) kernels for gfx950: y[n] = W[n, k] . x[k].
+//
+// Semantics follow the reference's native matmuls (fp32 in, fp32 out,
+// y[i] = sum_j w[i, j] * x[j]): matmul_q4_k q4_k.h:427-449,
+// matmul_q6_k q6_k.h:180-201, matmul_q8_0 q8_0.h:187-208; Q5_K and Q1_0
+// have no native matmul in the reference and follow its NumPy path
+// (dequant @ x, runtime/backend.py:203-213). Accumulation is fp32; the
+// order differs from the reference's sequential loop (tolerance contract,
+// not bit-exact).
+//
+// Layout and mapping (all formats):
+//   * W is row-major raw GGUF blocks: row i is k/B_elems blocks, contiguous.
+//   * A workgroup owns `rows_per_wg` consecutive rows and spans all of k:
+//     lane t of the workgroup owns one fixed slice of the k axis (a "work
+//     unit" inside block t / LPB) for every row it visits. Its slice of x is
+//     loaded once into VGPRs and reused for every row, so x costs no LDS or
+//     L1 bandwidth in the row loop; only W streams from HBM.
+//   * For each row the lanes of a block read adjacent bytes, so one wave
+//     load instruction covers a contiguous span of the row.
+//   * Loads for `U` rows are issued before any of them is consumed, to keep
+//     enough bytes in flight per wave to cover HBM latency.
+//   * Per-row partials are reduced across the wave with DPP, then across the
+//     workgroup's waves through LDS in a fixed order (deterministic output).
+//   * Scale algebra: sum_i (s*q_i - t) x_i = s * sum_i q_i x_i - t * sum_i x_i;
+//     the per-lane sums of x are computed once with x.
+#include "frq_common.h"
+#include "frq_kernels.h"
+
+namespace frq {
+
+__device__ __forceinline__ uint32_t vxor(uint32_t a, uint32_t mask) {
+    uint32_t r;
+    asm("v_xor_b32 %0, %1, %2" : "=v"(r) : "s"(mask), "v"(a));
+    return r;
+}
+__device__ __forceinline__ float sbf(uint32_t w, int b) { return (float)(int)(int8_t)((w >> (8 * b)) & 0xFFu); }
+
+// Writes the U row partials of one row batch: wave-reduce each, then either
+// store directly (one wave per row) or park the wave's share in LDS.
+template <int U>
+__device__ __forceinline__ void row_partials_out(const float (&part)[U], int64_t rb, int64_t row0,
+                                                 int64_t row_end, float* __restrict__ y,
+                                                 float* __restrict__ red, int nwaves, int wave,
+                                                 int lane) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const float v = wave_sum(part[u]);
+        if (lane == 0 && rb + u < row_end) {
+            if (nwaves == 1)
+                y[rb + u] = v;
+            else
+                red[(rb - row0 + u) * nwaves + wave] = v;
+        }
+    }
+}
+
+__device__ __forceinline__ void finish_rows(int64_t row0, int64_t row_end, float* __restrict__ y,
+                                            const float* __restrict__ red, int nwaves) {
+    if (nwaves == 1) return;
+    __syncthreads();
+    for (int r = threadIdx.x; r < row_end - row0; r += blockDim.x) {
+        float s = 0.0f;
+        for (int w = 0; w < nwaves; ++w) s += red[r * nwaves + w];
+        y[row0 + r] = s;
+    }
+}
+
+// ------------------------------------------------------------------ Q4_K
+// Work unit: CPL=2 -> one 32-byte qs group g of a block (64 elements,
+// 4 lanes per block); CPL=1 -> half a group (16 qs bytes, 32 elements,
+// 8 lanes per block). qs byte i of the unit holds element base+i in its low
+// nibble and base+32+i in its high nibble (gguf.py:209-219).
+template <int CPL, int U>
+__global__ void __launch_bounds__(512) gemv_q4_k_kernel(const uint8_t* __restrict__ w,
+                                                         const float* __restrict__ x,
+                                                         float* __restrict__ y, int64_t n, int nb,
+                                                         int rows_per_wg) {
+    extern __shared__ float red[];
+    constexpr int LPB = 8 / CPL;
+    constexpr int NE = 16 * CPL;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const int blk = tid / LPB, sub = tid % LPB;
+    const bool active = blk < nb;
+    const int g = (CPL == 2) ? sub : (sub >> 1);
+    const int hh = (CPL == 2) ? 0 : (sub & 1);
+
+    float xl[NE], xh[NE];
+    float sxl = 0.0f, sxh = 0.0f;
+    if (active) {
+        const float* xb = x + (int64_t)blk * kQKElems + 64 * g + 16 * hh;
+#pragma unroll
+        for (int i = 0; i < NE; i += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(xb + i);
+            const float4 c = *reinterpret_cast<const float4*>(xb + 32 + i);
+            xl[i] = a.x; xl[i + 1] = a.y; xl[i + 2] = a.z; xl[i + 3] = a.w;
+            xh[i] = c.x; xh[i + 1] = c.y; xh[i + 2] = c.z; xh[i + 3] = c.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NE; ++i) { xl[i] = 0.0f; xh[i] = 0.0f; }
+    }
+#pragma unroll
+    for (int i = 0; i < NE; ++i) { sxl += xl[i]; sxh += xh[i]; }
+
+    const int64_t row0 = (int64_t)blockIdx.x * rows_per_wg;
+    const int64_t row_end = row0 + rows_per_wg < n ? row0 + rows_per_wg : n;
+    const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
+    const uint8_t* wb = w + row0 * row_bytes + (int64_t)blk * kQ4KBytes;
+    const int qoff = 16 + 32 * g + 16 * hh;
+
+    for (int64_t rb = row0; rb < row_end; rb += U) {
+        uint4 hd[U];
+        uint4 q[U][CPL];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (active && rb + u < row_end) {
+                const uint8_t* p = wb + (rb - row0 + u) * row_bytes;
+                hd[u] = *reinterpret_cast<const uint4*>(p);
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) q[u][c] = *reinterpret_cast<const uint4*>(p + qoff + 16 * c);
+            } else {
+                hd[u] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) q[u][c] = make_uint4(0, 0, 0, 0);
+            }
+        }
+        float part[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            uint32_t sc0, m0, sc1, m1;
+            k4_scale_min(hd[u].y, hd[u].z, hd[u].w, 2 * g, sc0, m0);
+            k4_scale_min(hd[u].y, hd[u].z, hd[u].w, 2 * g + 1, sc1, m1);
+            const float d = f16_bits_to_f32(hd[u].x), dm = f16_bits_to_f32(hd[u].x >> 16);
+            float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const uint32_t qw[4] = {q[u][c].x, q[u][c].y, q[u][c].z, q[u][c].w};
+#pragma unroll
+                for (int wd = 0; wd < 4; ++wd) {
+                    const uint32_t lo = vand(qw[wd], 0x0F0F0F0Fu);
+                    const uint32_t hi = vand(qw[wd], 0xF0F0F0F0u);   // 16 * high nibble
+                    const int e = 16 * c + 4 * wd;
+                    a0 = __builtin_fmaf(byte_f(lo, 0), xl[e + 0], a0);
+                    a1 = __builtin_fmaf(byte_f(lo, 1), xl[e + 1], a1);
+                    a0 = __builtin_fmaf(byte_f(lo, 2), xl[e + 2], a0);
+                    a1 = __builtin_fmaf(byte_f(lo, 3), xl[e + 3], a1);
+                    b0 = __builtin_fmaf(byte_f(hi, 0), xh[e + 0], b0);
+                    b1 = __builtin_fmaf(byte_f(hi, 1), xh[e + 1], b1);
+                    b0 = __builtin_fmaf(byte_f(hi, 2), xh[e + 2], b0);
+                    b1 = __builtin_fmaf(byte_f(hi, 3), xh[e + 3], b1);
+                }
+            }
+            const float s0 = d * (float)sc0, t0 = dm * (float)m0;
+            const float s1 = d * (float)sc1 * 0.0625f, t1 = dm * (float)m1;
+            float pu = s0 * (a0 + a1);
+            pu = __builtin_fmaf(-t0, sxl, pu);
+            pu = __builtin_fmaf(s1, b0 + b1, pu);
+            part[u] = __builtin_fmaf(-t1, sxh, pu);
+        }
+        row_partials_out<U>(part, rb, row0, row_end, y, red, nwaves, wave, lane);
+    }
+    finish_rows(row0, row_end, y, red, nwaves);
+}
+
+// ------------------------------------------------------------------ Q5_K
+// Work unit: one 32-byte qs group g (64 elements, 4 lanes per block). The
+// 5th bit of element base+i is bit 2g (low nibble) / 2g+1 (high nibble) of
+// qh byte i (gguf.py:252-262).
+template <int U>
+__global__ void __launch_bounds__(512) gemv_q5_k_kernel(const uint8_t* __restrict__ w,
+                                                         const float* __restrict__ x,
+                                                         float* __restrict__ y, int64_t n, int nb,
+                                                         int rows_per_wg) {
+    extern __shared__ float red[];
+    constexpr int NE = 32;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const int blk = tid >> 2, g = tid & 3;
+    const bool active = blk < nb;
+
+    float xl[NE], xh[NE];
+    float sxl = 0.0f, sxh = 0.0f;
+    if (active) {
+        const float* xb = x + (int64_t)blk * kQKElems + 64 * g;
+#pragma unroll
+        for (int i = 0; i < NE; i += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(xb + i);
+            const float4 c = *reinterpret_cast<const float4*>(xb + 32 + i);
+            xl[i] = a.x; xl[i + 1] = a.y; xl[i + 2] = a.z; xl[i + 3] = a.w;
+            xh[i] = c.x; xh[i + 1] = c.y; xh[i + 2] = c.z; xh[i + 3] = c.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NE; ++i) { xl[i] = 0.0f; xh[i] = 0.0f; }
+    }
+#pragma unroll
+    for (int i = 0; i < NE; ++i) { sxl += xl[i]; sxh += xh[i]; }
+
+    const int64_t row0 = (int64_t)blockIdx.x * rows_per_wg;
+    const int64_t row_end = row0 + rows_per_wg < n ? row0 + rows_per_wg : n;
+    const int64_t row_bytes = (int64_t)nb * kQ5KBytes;
+    const uint8_t* wb = w + row0 * row_bytes + (int64_t)blk * kQ5KBytes;
+
+    for (int64_t rb = row0; rb < row_end; rb += U) {
+        uint4 hd[U], qh[U][2], qs[U][2];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (active && rb + u < row_end) {
+                const uint8_t* p = wb + (rb - row0 + u) * row_bytes;
+                hd[u] = *reinterpret_cast<const uint4*>(p);
+                qh[u][0] = *reinterpret_cast<const uint4*>(p + 16);
+                qh[u][1] = *reinterpret_cast<const uint4*>(p + 32);
+                qs[u][0] = *reinterpret_cast<const uint4*>(p + 48 + 32 * g);
+                qs[u][1] = *reinterpret_cast<const uint4*>(p + 64 + 32 * g);
+            } else {
+                hd[u] = qh[u][0] = qh[u][1] = qs[u][0] = qs[u][1] = make_uint4(0, 0, 0, 0);
+            }
+        }
+        float part[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            uint32_t sc0, m0, sc1, m1;
+            k4_scale_min(hd[u].y, hd[u].z, hd[u].w, 2 * g, sc0, m0);
+            k4_scale_min(hd[u].y, hd[u].z, hd[u].w, 2 * g + 1, sc1, m1);
+            const float d = f16_bits_to_f32(hd[u].x), dm = f16_bits_to_f32(hd[u].x >> 16);
+            float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const uint32_t sw[4] = {qs[u][c].x, qs[u][c].y, qs[u][c].z, qs[u][c].w};
+                const uint32_t hw[4] = {qh[u][c].x, qh[u][c].y, qh[u][c].z, qh[u][c].w};
+#pragma unroll
+                for (int wd = 0; wd < 4; ++wd) {
+                    // 5th bit of the low / high nibble moved to bit 4 of each byte
+                    const uint32_t h4 = hw[wd] << 4;
+                    const uint32_t lo = vand_or(sw[wd], 0x0F0F0F0Fu, vand(h4 >> (2 * g), 0x10101010u));
+                    const uint32_t hi = vand_or(sw[wd] >> 4, 0x0F0F0F0Fu, vand(h4 >> (2 * g + 1), 0x10101010u));
+                    const int e = 16 * c + 4 * wd;
+                    a0 = __builtin_fmaf(byte_f(lo, 0), xl[e + 0], a0);
+                    a1 = __builtin_fmaf(byte_f(lo, 1), xl[e + 1], a1);
+                    a0 = __builtin_fmaf(byte_f(lo, 2), xl[e + 2], a0);
+                    a1 = __builtin_fmaf(byte_f(lo, 3), xl[e + 3], a1);
+                    b0 = __builtin_fmaf(byte_f(hi, 0), xh[e + 0], b0);
+                    b1 = __builtin_fmaf(byte_f(hi, 1), xh[e + 1], b1);
+                    b0 = __builtin_fmaf(byte_f(hi, 2), xh[e + 2], b0);
+                    b1 = __builtin_fmaf(byte_f(hi, 3), xh[e + 3], b1);
+                }
+            }
+            const float s0 = d * (float)sc0, t0 = dm * (float)m0;
+            const float s1 = d * (float)sc1, t1 = dm * (float)m1;
+            float pu = s0 * (a0 + a1);
+            pu = __builtin_fmaf(-t0, sxl, pu);
+            pu = __builtin_fmaf(s1, b0 + b1, pu);
+            part[u] = __builtin_fmaf(-t1, sxh, pu);
+        }
+        row_partials_out<U>(part, rb, row0, row_end, y, red, nwaves, wave, lane);
+    }
+    finish_rows(row0, row_end, y, red, nwaves);
+}
+
+// ------------------------------------------------------------------ Q6_K
+// Work unit: half h of a block and LQ = 4*CPL consecutive l (l0 = LQ*p),
+// which covers elements 128h + 32k + l0 + [0, LQ) for k = 0..3. They need
+// ql[64h + l0 ..], ql[64h + 32 + l0 ..], qh[32h + l0 ..] (LQ bytes each) and
+// scales sc[8h + l0/16 + 2k] (gguf.py:401-419). Blocks are 210 B, so fields
+// are only 2-byte aligned: 4-byte reads go through ld_u32_a2.
+template <int CPL, int U>
+__global__ void __launch_bounds__(512) gemv_q6_k_kernel(const uint8_t* __restrict__ w,
+                                                         const float* __restrict__ x,
+                                                         float* __restrict__ y, int64_t n, int nb,
+                                                         int rows_per_wg) {
+    extern __shared__ float red[];
+    constexpr int LQ = 4 * CPL;          // l values per lane
+    constexpr int PPH = 32 / LQ;         // lanes per half
+    constexpr int LPB = 2 * PPH;         // lanes per block
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const int blk = tid / LPB, sub = tid % LPB;
+    const int h = sub / PPH, l0 = LQ * (sub % PPH);
+    const bool active = blk < nb;
+
+    float xv[4][LQ];
+    float xs[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        xs[k] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < LQ; i += 4) {
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (active) a = *reinterpret_cast<const float4*>(x + (int64_t)blk * kQKElems + 128 * h + 32 * k + l0 + i);
+            xv[k][i] = a.x; xv[k][i + 1] = a.y; xv[k][i + 2] = a.z; xv[k][i + 3] = a.w;
+        }
+#pragma unroll
+        for (int i = 0; i < LQ; ++i) xs[k] += xv[k][i];
+    }
+
+    const int64_t row0 = (int64_t)blockIdx.x * rows_per_wg;
+    const int64_t row_end = row0 + rows_per_wg < n ? row0 + rows_per_wg : n;
+    const int64_t row_bytes = (int64_t)nb * kQ6KBytes;
+    const uint8_t* wb = w + row0 * row_bytes + (int64_t)blk * kQ6KBytes;
+    const int sidx = l0 >> 4;   // l/16 for this lane's l range
+
+    for (int64_t rb = row0; rb < row_end; rb += U) {
+        uint32_t ql0[U][CPL], ql1[U][CPL], qh[U][CPL], sca[U], scb[U], dd[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (active && rb + u < row_end) {
+                const uint8_t* p = wb + (rb - row0 + u) * row_bytes;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    ql0[u][c] = ld_u32_a2(p + 64 * h + l0 + 4 * c);
+                    ql1[u][c] = ld_u32_a2(p + 64 * h + 32 + l0 + 4 * c);
+                    qh[u][c] = ld_u32_a2(p + 128 + 32 * h + l0 + 4 * c);
+                }
+                sca[u] = ld_u32_a2(p + 192 + 8 * h);
+                scb[u] = ld_u32_a2(p + 196 + 8 * h);
+                dd[u] = ld_u16(p + 208);
+            } else {
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) ql0[u][c] = ql1[u][c] = qh[u][c] = 0;
+                sca[u] = scb[u] = dd[u] = 0;
+            }
+        }
+        float part[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float d = f16_bits_to_f32(dd[u]);
+            const float sk[4] = {sbf(sca[u], sidx), sbf(sca[u], sidx + 2), sbf(scb[u], sidx), sbf(scb[u], sidx + 2)};
+            float pu = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    const uint32_t src = (k & 1) ? ql1[u][c] : ql0[u][c];
+                    // bits 2k, 2k+1 of each qh byte -> bits 4, 5
+                    const uint32_t hsh = (k == 0) ? (qh[u][c] << 4) : (k == 1) ? (qh[u][c] << 2)
+                                       : (k == 2) ? qh[u][c] : (qh[u][c] >> 2);
+                    const uint32_t q = vand_or((k >= 2) ? (src >> 4) : src, 0x0F0F0F0Fu, vand(hsh, 0x30303030u));
+                    a0 = __builtin_fmaf(byte_f(q, 0), xv[k][4 * c + 0], a0);
+                    a1 = __builtin_fmaf(byte_f(q, 1), xv[k][4 * c + 1], a1);
+                    a0 = __builtin_fmaf(byte_f(q, 2), xv[k][4 * c + 2], a0);
+                    a1 = __builtin_fmaf(byte_f(q, 3), xv[k][4 * c + 3], a1);
+                }
+                // sum_l (q - 32) x = sum_l q x - 32 sum_l x
+                const float dotk = __builtin_fmaf(-32.0f, xs[k], a0 + a1);
+                pu = __builtin_fmaf(d * sk[k], dotk, pu);
+            }
+            part[u] = pu;
+        }
+        row_partials_out<U>(part, rb, row0, row_end, y, red, nwaves, wave, lane);
+    }
+    finish_rows(row0, row_end, y, red, nwaves);
+}
+
+// ------------------------------------------------------------------ Q8_0
+// Work unit: 8*CPL consecutive int8 of one 34-byte block (32/(8*CPL) lanes
+// per block); y = sum_b d_b * sum_i q_i x_i.
+template <int CPL, int U>
+__global__ void __launch_bounds__(512) gemv_q8_0_kernel(const uint8_t* __restrict__ w,
+                                                         const float* __restrict__ x,
+                                                         float* __restrict__ y, int64_t n, int nb,
+                                                         int rows_per_wg) {
+    extern __shared__ float red[];
+    constexpr int NE = 8 * CPL;
+    constexpr int LPB = 32 / NE;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const int blk = tid / LPB, o = NE * (tid % LPB);
+    const bool active = blk < nb;
+
+    float xv[NE];
+    float sx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NE; i += 4) {
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (active) a = *reinterpret_cast<const float4*>(x + (int64_t)blk * kQ80Elems + o + i);
+        xv[i] = a.x; xv[i + 1] = a.y; xv[i + 2] = a.z; xv[i + 3] = a.w;
+    }
+#pragma unroll
+    for (int i = 0; i < NE; ++i) sx += xv[i];
+
+    const int64_t row0 = (int64_t)blockIdx.x * rows_per_wg;
+    const int64_t row_end = row0 + rows_per_wg < n ? row0 + rows_per_wg : n;
+    const int64_t row_bytes = (int64_t)nb * kQ80Bytes;
+    const uint8_t* wb = w + row0 * row_bytes + (int64_t)blk * kQ80Bytes;
+
+    for (int64_t rb = row0; rb < row_end; rb += U) {
+        uint32_t qv[U][NE / 4], dd[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (active && rb + u < row_end) {
+                const uint8_t* p = wb + (rb - row0 + u) * row_bytes;
+                dd[u] = ld_u16(p);
+#pragma unroll
+                for (int c = 0; c < NE / 4; ++c) qv[u][c] = ld_u32_a2(p + 2 + o + 4 * c);
+            } else {
+                dd[u] = 0;
+#pragma unroll
+                for (int c = 0; c < NE / 4; ++c) qv[u][c] = 0;
+            }
+        }
+        float part[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            // int8 q = (q ^ 0x80) - 128 with q ^ 0x80 read as an unsigned byte:
+            // sum q x = sum (q ^ 0x80) x - 128 sum x
+            float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NE / 4; ++c) {
+                const uint32_t v = vxor(qv[u][c], 0x80808080u);
+                a0 = __builtin_fmaf(byte_f(v, 0), xv[4 * c + 0], a0);
+                a1 = __builtin_fmaf(byte_f(v, 1), xv[4 * c + 1], a1);
+                a0 = __builtin_fmaf(byte_f(v, 2), xv[4 * c + 2], a0);
+                a1 = __builtin_fmaf(byte_f(v, 3), xv[4 * c + 3], a1);
+            }
+            part[u] = f16_bits_to_f32(dd[u]) * __builtin_fmaf(-128.0f, sx, a0 + a1);
+        }
+        row_partials_out<U>(part, rb, row0, row_end, y, red, nwaves, wave, lane);
+    }
+    finish_rows(row0, row_end, y, red, nwaves);
+}
+
+// ------------------------------------------------------------------ Q1_0
+// Work unit: 4*CPL bytes of sign bits (32*CPL elements, 4/CPL lanes per
+// block): sum_i (+-d) x_i = d * (2 * sum_{bit set} x_i - sum_i x_i).
+template <int CPL, int U>
+__global__ void __launch_bounds__(512) gemv_q1_0_kernel(const uint8_t* __restrict__ w,
+                                                        const float* __restrict__ x,
+                                                        float* __restrict__ y, int64_t n, int nb,
+                                                        int rows_per_wg) {
+    extern __shared__ float red[];
+    constexpr int NE = 32 * CPL;
+    constexpr int LPB = 4 / CPL;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const int blk = tid / LPB, o = NE * (tid % LPB);
+    const bool active = blk < nb;
+
+    // Element 8b + j of a 4-byte bit word is bit j of byte b. `bits & (0x01010101 << j)`
+    // leaves 2^j * bit in byte b, so x is stored pre-scaled by 2^-j (exact
+    // power-of-two scaling) and one v_cvt_f32_ubyte<b> + one FMA handles
+    // each element.
+    float xv[NE];
+    float sx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NE; i += 4) {
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (active) a = *reinterpret_cast<const float4*>(x + (int64_t)blk * kQ10Elems + o + i);
+        xv[i] = a.x; xv[i + 1] = a.y; xv[i + 2] = a.z; xv[i + 3] = a.w;
+    }
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        sx += xv[i];
+        xv[i] *= 1.0f / (float)(1u << (i & 7));
+    }
+
+    const int64_t row0 = (int64_t)blockIdx.x * rows_per_wg;
+    const int64_t row_end = row0 + rows_per_wg < n ? row0 + rows_per_wg : n;
+    const int64_t row_bytes = (int64_t)nb * kQ10Bytes;
+    const uint8_t* wb = w + row0 * row_bytes + (int64_t)blk * kQ10Bytes;
+
+    for (int64_t rb = row0; rb < row_end; rb += U) {
+        uint32_t bits[U][CPL], dd[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (active && rb + u < row_end) {
+                const uint8_t* p = wb + (rb - row0 + u) * row_bytes;
+                dd[u] = ld_u16(p);
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) bits[u][c] = ld_u32_a2(p + 2 + (o >> 3) + 4 * c);
+            } else {
+                dd[u] = 0;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) bits[u][c] = 0;
+            }
+        }
+        float part[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t t = vand(bits[u][c], 0x01010101u << j);
+                    a0 = __builtin_fmaf(byte_f(t, 0), xv[32 * c + j], a0);
+                    a1 = __builtin_fmaf(byte_f(t, 1), xv[32 * c + 8 + j], a1);
+                    a0 = __builtin_fmaf(byte_f(t, 2), xv[32 * c + 16 + j], a0);
+                    a1 = __builtin_fmaf(byte_f(t, 3), xv[32 * c + 24 + j], a1);
+                }
+            }
+            part[u] = f16_bits_to_f32(dd[u]) * __builtin_fmaf(2.0f, a0 + a1, -sx);
+        }
+        row_partials_out<U>(part, rb, row0, row_end, y, red, nwaves, wave, lane);
+    }
+    finish_rows(row0, row_end, y, red, nwaves);
+}
+
+// ------------------------------------------------------------------ planner
+
+namespace {
+
+struct Fmt {
+    int bbytes, belems;
+};
+
+Fmt fmt_of(int qtype) {
+    switch (qtype) {
+        case kTypeQ4K: return {kQ4KBytes, kQKElems};
+        case kTypeQ5K: return {kQ5KBytes, kQKElems};
+        case kTypeQ6K: return {kQ6KBytes, kQKElems};
+        case kTypeQ80: return {kQ80Bytes, kQ80Elems};
+        case kTypeQ10: return {kQ10Bytes, kQ10Elems};
+        default: return {0, 0};
+    }
+}
+
+// Lanes one block of this format needs with work unit `cpl`.
+int lanes_per_block(int qtype, int cpl) {
+    switch (qtype) {
+        case kTypeQ4K: return 8 / cpl;
+        case kTypeQ5K: return 4;
+        case kTypeQ6K: return 16 / cpl;
+        case kTypeQ80: return 4 / cpl;
+        case kTypeQ10: return 4 / cpl;
+        default: return 0;
+    }
+}
+
+bool cpl_valid(int qtype, int cpl) {
+    switch (qtype) {
+        case kTypeQ4K: return cpl == 1 || cpl == 2;
+        case kTypeQ6K: return cpl == 1 || cpl == 2 || cpl == 4;
+        case kTypeQ80: return cpl == 1 || cpl == 2 || cpl == 4;
+        case kTypeQ10: return cpl == 1 || cpl == 2;
+        case kTypeQ5K: return cpl == 1;
+        default: return false;
+    }
+}
+
+constexpr int64_t kMaxLanes = 512;   // matches __launch_bounds__(512)
+
+// Smallest-waste work unit whose row fits in one workgroup.
+int pick_cpl(int qtype, int64_t nb) {
+    int best = 0;
+    double best_waste = 2.0;
+    for (int cpl = 1; cpl <= 4; cpl *= 2) {
+        if (!cpl_valid(qtype, cpl)) continue;
+        const int64_t lanes = nb * lanes_per_block(qtype, cpl);
+        if (lanes > kMaxLanes) continue;
+        const int64_t padded = (lanes + 63) / 64 * 64;
+        const double waste = (double)(padded - lanes) / (double)padded;
+        // prefer larger units on ties: fewer scale decodes per element
+        if (waste < best_waste - 1e-9 || (waste <= best_waste + 1e-9 && cpl > best)) {
+            best = cpl;
+            best_waste = waste;
+        }
+    }
+    return best;
+}
+
+// Rows per workgroup: enough rows to amortise the x load into VGPRs, few
+// enough that the grid fills 256 CUs evenly.
+int pick_rows(int64_t n, int waves) {
+    const int64_t kCUs = 256;
+    int best_r = 1;
+    double best_score = -1.0;
+    for (int r = 2; r <= 32; ++r) {
+        const int64_t grid = (n + r - 1) / r;
+        // waves resident per CU if every workgroup ran at once
+        const double per_cu = (double)(grid * waves) / (double)kCUs;
+        const double rounds = (double)((grid + kCUs - 1) / kCUs);
+        const double balance = (double)grid / (rounds * kCUs);        // 1.0 = even spread
+        const double occ = per_cu >= 8.0 ? 1.0 : per_cu / 8.0;       // want >= 8 waves per CU
+        const double amort = r >= 8 ? 1.0 : 0.85 + 0.02 * r;         // x reload cost
+        const double score = balance * occ * amort;
+        if (score > best_score + 1e-9) {
+            best_score = score;
+            best_r = r;
+        }
+    }
+    return best_r;
+}
+
+// Variants whose 8-row batch exceeds the VGPR budget (they would spill to
+// scratch) run 4-row batches only.
+bool unroll8_ok(int qtype, int cpl) {
+    return !((qtype == kTypeQ4K && cpl == 2) || (qtype == kTypeQ6K && cpl == 4) || qtype == kTypeQ5K);
+}
+
+template <int U>
+hipError_t launch_u(int qtype, int cpl, const uint8_t* w, const float* x, float* y, int64_t n, int nb,
+                    int rows, int waves, int64_t grid, hipStream_t s) {
+    const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
+    const size_t lds = waves > 1 ? sizeof(float) * (size_t)rows * waves : 0;
+    switch (qtype) {
+        case kTypeQ4K:
+            if (cpl == 2) gemv_q4_k_kernel<2, 4><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
+            else gemv_q4_k_kernel<1, U><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
+            break;
+        case kTypeQ5K: gemv_q5_k_kernel<4><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows); break;
+        case kTypeQ6K:
+            if (cpl == 4) gemv_q6_k_kernel<4, 4><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
+            else if (cpl == 2) gemv_q6_k_kernel<2, U><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
+            else gemv_q6_k_kernel<1, U><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
+            break;
+        case kTypeQ80:
+            if (cpl == 4) gemv_q8_0_kernel<4, U><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
+            else if (cpl == 2) gemv_q8_0_kernel<2, U><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
+            else gemv_q8_0_kernel<1, U><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
+            break;
+        case kTypeQ10:
+            if (cpl == 2) gemv_q1_0_kernel<2, U><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
+            else gemv_q1_0_kernel<1, U><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemv_supported(int qtype, int64_t n, int64_t k) {
+    const Fmt f = fmt_of(qtype);
+    if (f.belems == 0 || n <= 0 || k <= 0 || k % f.belems) return false;
+    return pick_cpl(qtype, k / f.belems) != 0;
+}
+
+hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k,
+                       GemvPlan* plan, hipStream_t stream) {
+    const Fmt f = fmt_of(qtype);
+    if (f.belems == 0 || k % f.belems) return hipErrorInvalidValue;
+    if (n <= 0) return hipSuccess;
+    const int64_t nb = k / f.belems;
+    GemvPlan p = plan ? *plan : GemvPlan{};
+    if (p.cpl <= 0) p.cpl = pick_cpl(qtype, nb);
+    if (!cpl_valid(qtype, p.cpl)) return hipErrorInvalidValue;
+    const int64_t lanes = nb * lanes_per_block(qtype, p.cpl);
+    if (lanes > kMaxLanes) return hipErrorInvalidConfiguration;
+    p.waves = (int)((lanes + 63) / 64);
+    if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows(n, p.waves);
+    if (p.unroll != 4 && p.unroll != 8) p.unroll = p.rows_per_wg >= 8 ? 8 : 4;
+    if (!unroll8_ok(qtype, p.cpl)) p.unroll = 4;
+    p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
+    if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    if (plan) *plan = p;
+    if (p.unroll == 8)
+        return launch_u<8>(qtype, p.cpl, w, x, y, n, (int)nb, p.rows_per_wg, p.waves, p.grid, stream);
+    return launch_u<4>(qtype, p.cpl, w, x, y, n, (int)nb, p.rows_per_wg, p.waves, p.grid, stream);
+}
+
+}  // namespace frq

@@ -1,0 +1,43 @@
+// Launchers shared between the kernel translation units and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace frq {
+
+// GGML type ids (src/flatrun/backend/gguf.py:59-86).
+constexpr int kTypeQ80 = 8;
+constexpr int kTypeQ4K = 12;
+constexpr int kTypeQ5K = 13;
+constexpr int kTypeQ6K = 14;
+constexpr int kTypeQ10 = 41;
+
+// Launch geometry of one GEMV: lanes per row, waves per workgroup, rows per
+// workgroup and the per-format work unit chosen for it.
+struct GemvPlan {
+    int cpl = 0;            // format-specific work unit per lane (see frq_gemv.hip)
+    int waves = 0;          // wavefronts per workgroup
+    int rows_per_wg = 0;    // output rows owned by one workgroup
+    int unroll = 0;         // rows whose loads are issued together
+    int64_t grid = 0;       // workgroups
+};
+
+// y[0, n) = value, by kernel (no hipMemset node if the caller captures a graph).
+hipError_t launch_fill(float* y, float value, int64_t n, hipStream_t stream);
+
+// dst[0, bytes) = src[0, bytes); bytes a multiple of 16, both 16-byte aligned.
+hipError_t launch_copy(void* dst, const void* src, int64_t bytes, hipStream_t stream);
+
+hipError_t launch_dequant(int qtype, const uint8_t* w, float* y, int64_t n_elems, hipStream_t stream);
+
+// y[n] = W[n, k] . x[k] with fp32 accumulation. `plan` may be pre-filled
+// (cpl/rows_per_wg/unroll > 0) to override the heuristic; on return it holds
+// the geometry that was launched.
+hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k,
+                       GemvPlan* plan, hipStream_t stream);
+
+// Checks that a GEMV of this shape can be planned; returns false with no launch otherwise.
+bool gemv_supported(int qtype, int64_t n, int64_t k);
+
+}  // namespace frq

@@ -1,0 +1,216 @@
+"""Device-resident buffers, streams and the device-pointer entry points.
+
+This is the decode-time path: raw GGUF blocks are uploaded once
+(:meth:`DeviceBuffer.from_host`) and every matvec reads them straight from
+HBM through ``frq_dev_gemv``. Any object exposing ``data_ptr()`` (a torch
+CUDA tensor) can be passed where a device buffer is expected, so callers that
+keep activations in torch tensors need no copies.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib
+
+
+def _addr(obj) -> int:
+    if obj is None:
+        return 0
+    if isinstance(obj, DeviceBuffer):
+        return obj.ptr
+    if hasattr(obj, "data_ptr"):
+        return int(obj.data_ptr())
+    if isinstance(obj, int):
+        return obj
+    raise TypeError(f"expected a device buffer, got {type(obj).__name__}")
+
+
+def _nbytes(obj) -> int:
+    if isinstance(obj, DeviceBuffer):
+        return obj.nbytes
+    if hasattr(obj, "untyped_storage"):
+        return int(obj.numel() * obj.element_size())
+    raise TypeError(f"cannot size {type(obj).__name__}")
+
+
+def _stream(s) -> int:
+    if s is None:
+        return 0
+    if isinstance(s, Stream):
+        return s.handle
+    if hasattr(s, "cuda_stream"):
+        return int(s.cuda_stream)
+    return int(s)
+
+
+class DeviceBuffer:
+    """An allocation in device memory (hipMalloc), freed with the object."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        check(lib().frq_malloc(ctypes.byref(p), self.nbytes))
+        self.ptr = int(p.value or 0)
+
+    @classmethod
+    def from_host(cls, arr: np.ndarray, stream=None) -> "DeviceBuffer":
+        a = np.ascontiguousarray(arr)
+        buf = cls(a.nbytes)
+        if a.nbytes:
+            if stream is None:
+                check(lib().frq_memcpy_h2d(buf.ptr, a.ctypes.data, a.nbytes))
+            else:
+                check(lib().frq_memcpy_h2d_async(buf.ptr, a.ctypes.data, a.nbytes, _stream(stream)))
+        return buf
+
+    def to_host(self, dtype=np.uint8, count: int | None = None) -> np.ndarray:
+        dt = np.dtype(dtype)
+        n = self.nbytes // dt.itemsize if count is None else int(count)
+        out = np.empty(n, dtype=dt)
+        if out.nbytes:
+            check(lib().frq_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if getattr(self, "ptr", 0):
+            try:
+                lib().frq_free(self.ptr)
+            finally:
+                self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def data_ptr(self) -> int:
+        return self.ptr
+
+
+class PinnedBuffer:
+    """Page-locked host memory (hipHostMalloc) viewed as a numpy array."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        check(lib().frq_host_alloc(ctypes.byref(p), self.nbytes))
+        self.ptr = int(p.value or 0)
+        self.array = np.ctypeslib.as_array((ctypes.c_uint8 * max(self.nbytes, 1)).from_address(self.ptr))[: self.nbytes]
+
+    def free(self) -> None:
+        if getattr(self, "ptr", 0):
+            self.array = None
+            try:
+                lib().frq_host_free(self.ptr)
+            finally:
+                self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Stream:
+    """A HIP stream at the default priority (non-blocking w.r.t. the null stream)."""
+
+    def __init__(self):
+        p = ctypes.c_void_p()
+        check(lib().frq_stream_create(ctypes.byref(p)))
+        self.handle = int(p.value or 0)
+
+    def synchronize(self) -> None:
+        check(lib().frq_stream_synchronize(self.handle))
+
+    def wait(self, event: "Event") -> None:
+        check(lib().frq_stream_wait_event(self.handle, event.handle))
+
+    def destroy(self) -> None:
+        if getattr(self, "handle", 0):
+            try:
+                lib().frq_stream_destroy(self.handle)
+            finally:
+                self.handle = 0
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        p = ctypes.c_void_p()
+        check(lib().frq_event_create(ctypes.byref(p)))
+        self.handle = int(p.value or 0)
+
+    def record(self, stream=None) -> None:
+        check(lib().frq_event_record(self.handle, _stream(stream)))
+
+    def synchronize(self) -> None:
+        check(lib().frq_event_synchronize(self.handle))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        check(lib().frq_event_elapsed_ms(ctypes.byref(ms), self.handle, end.handle))
+        return float(ms.value)
+
+    def destroy(self) -> None:
+        if getattr(self, "handle", 0):
+            try:
+                lib().frq_event_destroy(self.handle)
+            finally:
+                self.handle = 0
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+def synchronize() -> None:
+    check(lib().frq_device_synchronize())
+
+
+def qtype_id(q) -> int:
+    if isinstance(q, str):
+        return _lib.QTYPES[q.upper()]
+    return int(q)
+
+
+def gemv(qtype, w, x, y, n: int, k: int, batch: int = 1, stream=None, w_bytes: int | None = None) -> None:
+    """y[b, :n] = W[n, k] . x[b, :k] on device buffers (enqueued, not synchronised)."""
+    q = qtype_id(qtype)
+    wb = _nbytes(w) if w_bytes is None else int(w_bytes)
+    check(lib().frq_dev_gemv(q, _addr(w), wb, _addr(x), _addr(y), int(n), int(k), int(batch), _stream(stream)))
+
+
+def gemv_tuned(qtype, w, x, y, n: int, k: int, cpl: int = 0, rows_per_wg: int = 0, unroll: int = 0,
+               stream=None, w_bytes: int | None = None) -> dict:
+    """One GEMV with an explicit launch geometry; returns the geometry used."""
+    q = qtype_id(qtype)
+    wb = _nbytes(w) if w_bytes is None else int(w_bytes)
+    c, r, u, wv = ctypes.c_int(cpl), ctypes.c_int(rows_per_wg), ctypes.c_int(unroll), ctypes.c_int(0)
+    check(lib().frq_dev_gemv_tuned(q, _addr(w), wb, _addr(x), _addr(y), int(n), int(k), ctypes.byref(c),
+                                   ctypes.byref(r), ctypes.byref(u), ctypes.byref(wv), _stream(stream)))
+    return {"cpl": c.value, "rows_per_wg": r.value, "unroll": u.value, "waves": wv.value}
+
+
+def copy(dst, src, nbytes: int, stream=None) -> None:
+    """dst[:nbytes] = src[:nbytes] with the library's streaming copy kernel (enqueued)."""
+    check(lib().frq_dev_copy(_addr(dst), _addr(src), int(nbytes), _stream(stream)))
+
+
+def dequant(qtype, w, y, n_elems: int, stream=None, w_bytes: int | None = None) -> None:
+    """y[:n_elems] = dequant(w) on device buffers (enqueued)."""
+    q = qtype_id(qtype)
+    wb = _nbytes(w) if w_bytes is None else int(w_bytes)
+    check(lib().frq_dev_dequant(q, _addr(w), wb, int(n_elems), _addr(y), _stream(stream)))

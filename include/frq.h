@@ -1,0 +1,172 @@
+/*
+ * frq.h -- C ABI of libfrq_hip.so, the gfx950 GGUF dequant + matvec library.
+ *
+ * Plain pointers and sizes only; no exceptions cross this boundary. Every
+ * entry point returns an frq_status; on failure frq_last_error() returns a
+ * thread-local message. Python reaches the library through ctypes
+ * (flatrun_amd/_lib.py); the binding a reference maintainer would add is in
+ * INTEGRATION.md.
+ *
+ * Two families:
+ *
+ *  1. Host-buffer entry points, one per function of the reference's pybind11
+ *     module flatrun_native._C (src/flatrun_native/_C.cpp:455-488). Inputs
+ *     and outputs are host memory; the library stages them through device
+ *     memory, runs the HIP kernels and copies the result back before
+ *     returning. Validation and messages follow _C.cpp; a failure the
+ *     reference reports as std::runtime_error is returned as
+ *     FRQ_ERR_SHAPE / FRQ_ERR_SIZE so the facade can raise RuntimeError,
+ *     the exception the reference runtime falls back on
+ *     (src/flatrun/runtime/backend.py:259-268).
+ *
+ *  2. Device entry points (frq_dev_*): raw GGUF blocks, x and y already in
+ *     device memory, work enqueued on a caller-given hipStream_t (NULL = the
+ *     null stream), nothing copied. This is the decode-time hot path.
+ *
+ * Quant types are GGML type ids (src/flatrun/backend/gguf.py:59-86):
+ *   FRQ_Q8_0 = 8 (34 B / 32), FRQ_Q4_K = 12 (144 B / 256),
+ *   FRQ_Q5_K = 13 (176 B / 256), FRQ_Q6_K = 14 (210 B / 256),
+ *   FRQ_Q1_0 = 41 (18 B / 128).
+ *
+ * Numerics: dequant is bit-exact with the reference NumPy decoders
+ * (src/flatrun/dequant/gguf.py); matmul accumulates in fp32 and is held to
+ * 1e-5 relative error (normwise and componentwise) against the reference
+ * NumPy / native matvec.
+ */
+#ifndef FRQ_H
+#define FRQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    FRQ_OK = 0,
+    FRQ_ERR_INVALID = 1,      /* bad argument (null pointer, unknown type, ...) */
+    FRQ_ERR_SHAPE = 2,        /* shape / ndim rule of _C.cpp violated          */
+    FRQ_ERR_SIZE = 3,         /* weight byte count does not match (n, k)       */
+    FRQ_ERR_UNSUPPORTED = 4,  /* valid request this build does not plan         */
+    FRQ_ERR_NO_DEVICE = 5,    /* no HIP device visible                          */
+    FRQ_ERR_HIP = 6,          /* HIP runtime error                              */
+    FRQ_ERR_ALIGN = 7         /* device pointer misaligned for its format       */
+} frq_status;
+
+enum { FRQ_Q8_0 = 8, FRQ_Q4_K = 12, FRQ_Q5_K = 13, FRQ_Q6_K = 14, FRQ_Q1_0 = 41 };
+
+/* ---------------------------------------------------------------- general */
+
+/* Build identifier. Replaces _C.version (_C.cpp:449-451). */
+const char* frq_version(void);
+
+/* Always 0: this build has no NEON path. Replaces _C.is_neon (_C.cpp:441-447). */
+int frq_is_neon(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* frq_last_error(void);
+
+/* Number of visible HIP devices (0 on a machine without a GPU). */
+int frq_device_count(int* count);
+
+/* Bytes and elements per block of a GGML type id
+ * (src/flatrun/backend/gguf.py:59-103). */
+int frq_block_info(int qtype, int64_t* block_bytes, int64_t* block_elems);
+
+/* ---------------------------------------------- host-buffer entry points
+ * weight: raw GGUF block bytes, weight_bytes long (host memory).
+ * out:    caller-allocated float32 host buffer of the result size.        */
+
+/* dequant_q4_k(weight, (out, in)) -> f32 (out, in). _C.cpp:47-86. */
+int frq_dequant_q4_k(const uint8_t* weight, size_t weight_bytes, int64_t out_dim, int64_t in_dim, float* out);
+/* dequant_q8_0(weight, (out, in)). _C.cpp:285-320. */
+int frq_dequant_q8_0(const uint8_t* weight, size_t weight_bytes, int64_t out_dim, int64_t in_dim, float* out);
+/* dequant_q6_k(weight, (out, in)). _C.cpp:363-398. */
+int frq_dequant_q6_k(const uint8_t* weight, size_t weight_bytes, int64_t out_dim, int64_t in_dim, float* out);
+
+/* Generic dequant of any supported type with the NumPy decoders' size rule
+ * (ceil-div blocks, tail trimmed): replaces dequant_q8_0 / q4_k / q5_k /
+ * q6_k / q1_0 of src/flatrun/dequant/gguf.py:112,166,223,266,365 for the
+ * Q5_K and Q1_0 formats the native module lacks. */
+int frq_dequant(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, float* out);
+
+/* matmul_q4_k(x[k], weight, n, k) -> out[n]. _C.cpp:99-132. */
+int frq_matmul_q4_k(const float* x, size_t x_len, const uint8_t* weight, size_t weight_bytes, size_t n, size_t k,
+                    float* out);
+/* matmul_q4_k_batched(x[seq, k], weight, n, k) -> out[seq, n]. _C.cpp:154-197.
+ * x_ndim is the ndim of the caller's array (must be 2), x_cols its shape[1]. */
+int frq_matmul_q4_k_batched(const float* x, int x_ndim, size_t seq, size_t x_cols, const uint8_t* weight,
+                            size_t weight_bytes, size_t n, size_t k, float* out);
+/* matmul_q8_0. _C.cpp:326-357. */
+int frq_matmul_q8_0(const float* x, size_t x_len, const uint8_t* weight, size_t weight_bytes, size_t n, size_t k,
+                    float* out);
+/* matmul_q8_0_batched. _C.cpp:199-242. */
+int frq_matmul_q8_0_batched(const float* x, int x_ndim, size_t seq, size_t x_cols, const uint8_t* weight,
+                            size_t weight_bytes, size_t n, size_t k, float* out);
+/* matmul_q6_k. _C.cpp:404-435. */
+int frq_matmul_q6_k(const float* x, size_t x_len, const uint8_t* weight, size_t weight_bytes, size_t n, size_t k,
+                    float* out);
+/* matmul_q6_k_batched. _C.cpp:244-283. */
+int frq_matmul_q6_k_batched(const float* x, int x_ndim, size_t seq, size_t x_cols, const uint8_t* weight,
+                            size_t weight_bytes, size_t n, size_t k, float* out);
+
+/* Generic host matmul for every supported type (adds Q5_K and Q1_0, whose
+ * reference path is dequant + `w @ x`, runtime/backend.py:203-213):
+ * x is seq rows of k floats, out is seq rows of n floats. */
+int frq_matmul(int qtype, const float* x, size_t seq, const uint8_t* weight, size_t weight_bytes, size_t n, size_t k,
+               float* out);
+
+/* ---------------------------------------------------- device entry points
+ * All pointers are device pointers; stream is a hipStream_t (NULL = null
+ * stream). Q4_K / Q5_K weights must be 16-byte aligned, the others 2-byte
+ * aligned; x and y 16-byte / 4-byte aligned.                              */
+
+/* y[n_elems] = dequant(w). Same numerics as frq_dequant. */
+int frq_dev_dequant(int qtype, const void* w, size_t w_bytes, int64_t n_elems, float* y, void* stream);
+
+/* y[b, n] = W[n, k] . x[b, k] for b < batch: the decode matvec of
+ * matmul_<q> / matmul_<q>_batched (_C.cpp:99-283) on device buffers. */
+int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
+                 int64_t batch, void* stream);
+
+/* frq_dev_gemv with an explicit launch geometry (cpl = work unit per lane,
+ * rows_per_wg, unroll 4|8; 0 = library choice). Reports the geometry used
+ * through the same pointers. For tuning sweeps and profiling. */
+int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
+                       int* cpl, int* rows_per_wg, int* unroll, int* waves, void* stream);
+
+/* dst = src on the device with a plain 16-byte-per-lane streaming kernel:
+ * the reference point for calibrating HBM traffic counters (bytes a
+ * multiple of 16, both pointers 16-byte aligned). No reference counterpart. */
+int frq_dev_copy(void* dst, const void* src, size_t bytes, void* stream);
+
+/* ------------------------------------------- memory, streams and events
+ * Thin wrappers so a ctypes caller needs no other HIP binding. Streams are
+ * created at the default priority.                                         */
+int frq_set_device(int device);
+int frq_malloc(void** ptr, size_t bytes);
+int frq_free(void* ptr);
+int frq_host_alloc(void** ptr, size_t bytes);      /* pinned host memory */
+int frq_host_free(void* ptr);
+int frq_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int frq_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int frq_memcpy_h2d_async(void* dst, const void* src, size_t bytes, void* stream);
+int frq_memcpy_d2h_async(void* dst, const void* src, size_t bytes, void* stream);
+int frq_memset_async(void* dst, int value, size_t bytes, void* stream);
+int frq_stream_create(void** stream);
+int frq_stream_destroy(void* stream);
+int frq_stream_synchronize(void* stream);
+int frq_stream_wait_event(void* stream, void* event);
+int frq_event_create(void** event);
+int frq_event_destroy(void* event);
+int frq_event_record(void* event, void* stream);
+int frq_event_synchronize(void* event);
+int frq_event_elapsed_ms(float* ms, void* start, void* stop);
+int frq_device_synchronize(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FRQ_H */
