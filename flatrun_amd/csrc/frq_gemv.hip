@@ -176,6 +176,7 @@ __global__ void __launch_bounds__(512) gemv_q5_k_kernel(const uint8_t* __restric
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
     const int blk = tid >> 2, g = tid & 3;
     const bool active = blk < nb;
+    const uint32_t rot_lo = (uint32_t)(2 * g + 28) & 31u, rot_hi = (uint32_t)(2 * g + 29) & 31u;
 
     float xl[NE], xh[NE];
     float sxl = 0.0f, sxh = 0.0f;
@@ -229,10 +230,14 @@ __global__ void __launch_bounds__(512) gemv_q5_k_kernel(const uint8_t* __restric
                 const uint32_t hw[4] = {qh[u][c].x, qh[u][c].y, qh[u][c].z, qh[u][c].w};
 #pragma unroll
                 for (int wd = 0; wd < 4; ++wd) {
-                    // 5th bit of the low / high nibble moved to bit 4 of each byte
-                    const uint32_t h4 = hw[wd] << 4;
-                    const uint32_t lo = vand_or(sw[wd], 0x0F0F0F0Fu, vand(h4 >> (2 * g), 0x10101010u));
-                    const uint32_t hi = vand_or(sw[wd] >> 4, 0x0F0F0F0Fu, vand(h4 >> (2 * g + 1), 0x10101010u));
+                    // 5th bit (bit j of each qh byte) moved to bit 4 of its byte by a
+                    // 32-bit rotate right by (j - 4) mod 32: bits that wrap land
+                    // outside bit 4 of every byte, so the mask removes them (a plain
+                    // shift would push byte 3's high bits out of the dword).
+                    const uint32_t hl = __builtin_amdgcn_alignbit(hw[wd], hw[wd], rot_lo);
+                    const uint32_t hh = __builtin_amdgcn_alignbit(hw[wd], hw[wd], rot_hi);
+                    const uint32_t lo = vand_or(sw[wd], 0x0F0F0F0Fu, vand(hl, 0x10101010u));
+                    const uint32_t hi = vand_or(sw[wd] >> 4, 0x0F0F0F0Fu, vand(hh, 0x10101010u));
                     const int e = 16 * c + 4 * wd;
                     a0 = __builtin_fmaf(byte_f(lo, 0), xl[e + 0], a0);
                     a1 = __builtin_fmaf(byte_f(lo, 1), xl[e + 1], a1);
