@@ -9,17 +9,20 @@ timed region, and steps rotate over >= 1 GiB of distinct weight copies so no
 step is served from the 256 MB Infinity Cache.
 
 Printed: ONE JSON line with
-  value      effective GB/s over the whole timed region (K launches,
-             back-to-back on one stream, bracketed by device syncs);
+  value      effective GB/s over the whole timed region: K launches recorded
+             once as a HIP graph and replayed back-to-back on one stream,
+             bracketed by device syncs and HIP events on that stream;
              effective bytes per step = raw blocks + 4k (x) + 4n (y);
   roofline   the GEMV kernel against 8 TB/s HBM: achieved = effective bytes
-             per launch / mean kernel duration, timed with HIP events around
-             each launch on the launching stream;
+             per launch / mean launch duration over the same timed region;
+  eager_launch_us  mean time per launch when each launch is issued from
+             Python one by one (host-bound for kernels this short);
   cpu_baseline  the reference's native scalar matmul (its own _C module built
              from its sources, 1 thread) on the same bytes, timed on the host
              for a bounded number of full-shape repetitions; plus the NumPy path;
   configs    every other benchmark workload (GB/s, mean kernel us, fraction of
-             HBM peak) and the Llama-3-8B decode-step weight sweep (ms/step).
+             HBM peak) and the Llama-3-8B decode-step weight sweep (ms/step,
+             graph replay and eager).
 """
 
 from __future__ import annotations
@@ -69,10 +72,32 @@ class GemvWorkload:
         device.synchronize()
         return self.y.to_host(np.float32)
 
+    def graph(self, launches: int, start: int = 0) -> "device.Graph":
+        """`launches` consecutive steps recorded as one HIP graph."""
+        with device.Graph.capture(self.stream) as cap:
+            for i in range(launches):
+                self.launch(start + i)
+        return cap.graph
+
     def time_throughput(self, steps: int, warmup: int) -> float:
-        """Seconds for `steps` back-to-back launches after `warmup` untimed ones."""
-        for i in range(warmup):
-            self.launch(i)
+        """Seconds for `steps` launches replayed back-to-back from one HIP
+        graph, after `warmup` untimed ones; events on the launching stream."""
+        g_warm, g = self.graph(max(warmup, 1)), self.graph(steps, start=warmup)
+        g_warm.launch(self.stream)
+        device.synchronize()
+        e0, e1 = device.Event(), device.Event()
+        e0.record(self.stream)
+        g.launch(self.stream)
+        e1.record(self.stream)
+        e1.synchronize()
+        device.synchronize()
+        g.destroy()
+        g_warm.destroy()
+        return e0.elapsed_ms(e1) / 1e3
+
+    def time_eager(self, steps: int) -> float:
+        """Seconds for `steps` launches issued one by one from Python."""
+        self.launch(0)
         device.synchronize()
         e0, e1 = device.Event(), device.Event()
         e0.record(self.stream)
@@ -80,19 +105,7 @@ class GemvWorkload:
             self.launch(i)
         e1.record(self.stream)
         e1.synchronize()
-        device.synchronize()
         return e0.elapsed_ms(e1) / 1e3
-
-    def time_kernel(self, launches: int) -> float:
-        """Mean per-launch kernel time (s): an event pair around every launch."""
-        evs = [(device.Event(), device.Event()) for _ in range(launches)]
-        for i, (a, b) in enumerate(evs):
-            a.record(self.stream)
-            self.launch(i)
-            b.record(self.stream)
-        device.synchronize()
-        ms = [a.elapsed_ms(b) for a, b in evs]
-        return float(np.mean(ms)) / 1e3
 
     def free(self) -> None:
         for b in self.w:
@@ -161,10 +174,11 @@ def run_suite(stream, steps: int) -> dict:
     for idx, (name, q, n, k) in enumerate(SUITE):
         w = GemvWorkload(q, n, k, seed=100 + idx, stream=stream)
         t = w.time_throughput(steps, warmup=10)
-        tk = w.time_kernel(min(steps, 100))
-        out[name] = {"gbs": round(w.bytes * steps / t / 1e9, 1), "kernel_us": round(tk * 1e6, 2),
-                     "kernel_gbs": round(w.bytes / tk / 1e9, 1), "frac_hbm": round(w.bytes / tk / 1e9 / HBM_PEAK_GBS, 4),
-                     "effective_bytes": w.bytes}
+        te = w.time_eager(min(steps, 200))
+        tk = t / steps
+        out[name] = {"gbs": round(w.bytes / tk / 1e9, 1), "kernel_us": round(tk * 1e6, 2),
+                     "frac_hbm": round(w.bytes / tk / 1e9 / HBM_PEAK_GBS, 4),
+                     "eager_us_per_launch": round(te / min(steps, 200) * 1e6, 2), "effective_bytes": w.bytes}
         w.free()
     out["llama3_8b_decode_resident"] = decode_sweep_resident(stream, steps=max(3, min(steps // 50, 20)))
     return out
@@ -185,20 +199,28 @@ def decode_sweep_resident(stream, steps: int, layers: int = 32) -> dict:
             for name, q, n, k in LLAMA_LAYER:
                 device.gemv(q, dev[L][name], x, y, n, k, stream=stream, w_bytes=host[name].nbytes)
 
-    step()
-    device.synchronize()
-    e0, e1 = device.Event(), device.Event()
-    e0.record(stream)
-    for _ in range(steps):
+    def timed(run) -> float:
+        run()
+        device.synchronize()
+        e0, e1 = device.Event(), device.Event()
+        e0.record(stream)
+        for _ in range(steps):
+            run()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / steps
+
+    ms_eager = timed(step)
+    with device.Graph.capture(stream) as cap:
         step()
-    e1.record(stream)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / steps
+    ms = timed(lambda: cap.launch(stream))
+    cap.destroy()
     for d in dev:
         for b in d.values():
             b.free()
-    return {"ms_per_step": round(ms, 4), "weight_bytes_per_step": total, "gemvs_per_step": layers * len(LLAMA_LAYER),
-            "gbs": round(total / (ms / 1e3) / 1e9, 1), "floor_ms_at_8TBs": round(total / 8e12 * 1e3, 4)}
+    return {"ms_per_step": round(ms, 4), "ms_per_step_eager": round(ms_eager, 4), "weight_bytes_per_step": total,
+            "gemvs_per_step": layers * len(LLAMA_LAYER), "gbs": round(total / (ms / 1e3) / 1e9, 1),
+            "floor_ms_at_8TBs": round(total / 8e12 * 1e3, 4)}
 
 
 def main() -> int:
@@ -226,7 +248,8 @@ def main() -> int:
     work.launch(0)
     y_gpu = work.result()
     t = work.time_throughput(a.steps, a.warmup)
-    t_kernel = work.time_kernel(min(a.steps, 200))
+    t_kernel = t / a.steps                      # mean launch duration over the timed region
+    t_eager = work.time_eager(min(a.steps, 500)) / min(a.steps, 500)
     value = work.bytes * a.steps / t / 1e9
     achieved = work.bytes / t_kernel / 1e9
     rec = {
@@ -249,6 +272,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel_us": round(t_kernel * 1e6, 3)},
+        "eager_launch_us": round(t_eager * 1e6, 3),
     }
     if not a.no_suite:
         rec["configs"] = run_suite(stream, steps=min(a.steps, 500))

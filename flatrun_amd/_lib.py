@@ -29,6 +29,19 @@ QTYPES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K, "Q1_0": Q1_0}
 BLOCKS = {Q8_0: (34, 32), Q4_K: (144, 256), Q5_K: (176, 256), Q6_K: (210, 256), Q1_0: (18, 128)}
 
 
+GEMV_AUTO, GEMV_SPLITK, GEMV_ROWS = 0, 1, 2
+
+
+class GemvConfig(ctypes.Structure):
+    """frq_gemv_config (include/frq.h)."""
+    _fields_ = [("kernel", ctypes.c_int32), ("cpl", ctypes.c_int32), ("rows", ctypes.c_int32),
+                ("unroll", ctypes.c_int32), ("slices", ctypes.c_int32), ("waves_per_wg", ctypes.c_int32),
+                ("items", ctypes.c_int64)]
+
+    def as_dict(self) -> dict:
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
 class LibraryMissing(RuntimeError):
     """libfrq_hip.so is not built or cannot be loaded."""
 
@@ -69,7 +82,7 @@ SIGNATURES: dict[str, list] = {
     "frq_matmul": [_i32, _vp, _sz, _vp, _sz, _sz, _sz, _vp],
     "frq_dev_dequant": [_i32, _vp, _sz, _i64, _vp, _vp],
     "frq_dev_gemv": [_i32, _vp, _sz, _vp, _vp, _i64, _i64, _i64, _vp],
-    "frq_dev_gemv_tuned": [_i32, _vp, _sz, _vp, _vp, _i64, _i64, _i32p, _i32p, _i32p, _i32p, _vp],
+    "frq_dev_gemv_tuned": [_i32, _vp, _sz, _vp, _vp, _i64, _i64, _c.c_void_p, _vp],
     "frq_dev_copy": [_vp, _vp, _sz, _vp],
     "frq_set_device": [_i32],
     "frq_malloc": [_c.POINTER(_vp), _sz],
@@ -91,6 +104,10 @@ SIGNATURES: dict[str, list] = {
     "frq_event_synchronize": [_vp],
     "frq_event_elapsed_ms": [_f32p, _vp, _vp],
     "frq_device_synchronize": [],
+    "frq_stream_begin_capture": [_vp],
+    "frq_stream_end_capture": [_vp, _c.POINTER(_vp)],
+    "frq_graph_launch": [_vp, _vp],
+    "frq_graph_destroy": [_vp],
 }
 _RESTYPES = {"frq_version": _c.c_char_p, "frq_last_error": _c.c_char_p}
 

@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -98,6 +99,69 @@ int workspace(size_t bytes, void** out) {
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Split-K scratch, one per (device, stream): launches on one stream are
+// ordered, so they can share it; launches on different streams get their own.
+// Counters and partial sums live in separate allocations: the counters must
+// be zero before every launch (zeroed once when allocated, left zero by every
+// launch), so nothing else may ever write their memory.
+struct SkScratch {
+    void* part = nullptr;
+    size_t part_cap = 0;
+    void* cnt = nullptr;
+    size_t cnt_cap = 0;
+};
+std::mutex g_sk_mu;
+std::map<std::pair<int, hipStream_t>, SkScratch> g_sk;
+
+int grow(void** ptr, size_t* cap, size_t bytes, bool zero, hipStream_t stream) {
+    if (*cap >= bytes) return FRQ_OK;
+    if (*ptr) {
+        FRQ_HIP(hipStreamSynchronize(stream));   // the old buffer may still be in use
+        FRQ_HIP(hipFree(*ptr));
+        *ptr = nullptr;
+        *cap = 0;
+    }
+    size_t want = bytes < ((size_t)1 << 16) ? ((size_t)1 << 16) : bytes;
+    FRQ_HIP(hipMalloc(ptr, want));
+    if (zero) FRQ_HIP(hipMemset(*ptr, 0, want));
+    *cap = want;
+    return FRQ_OK;
+}
+
+int sk_scratch(hipStream_t stream, size_t part_bytes, size_t cnt_bytes, float** part, uint32_t** cnt) {
+    *part = nullptr;
+    *cnt = nullptr;
+    if (part_bytes == 0 && cnt_bytes == 0) return FRQ_OK;
+    int dev = 0;
+    FRQ_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_sk_mu);
+    SkScratch& sc = g_sk[{dev, stream}];
+    if (int rc = grow(&sc.part, &sc.part_cap, part_bytes, false, stream)) return rc;
+    if (int rc = grow(&sc.cnt, &sc.cnt_cap, cnt_bytes, true, stream)) return rc;
+    *part = static_cast<float*>(sc.part);
+    *cnt = static_cast<uint32_t*>(sc.cnt);
+    return FRQ_OK;
+}
+
+// One GEMV on device buffers: the whole-row kernel when a row fits one
+// workgroup, else the split-K kernel.
+int gemv_device(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s) {
+    if (frq::gemv_supported(qtype, n, k)) {
+        FRQ_HIP(frq::launch_gemv(qtype, w, x, y, n, k, nullptr, s));
+        return FRQ_OK;
+    }
+    frq::SplitKPlan sp;
+    if (!frq::plan_gemv_sk(qtype, n, k, &sp))
+        return fail(FRQ_ERR_UNSUPPORTED, "gemv: k=%lld has no kernel plan for this format", (long long)k);
+    size_t pb = 0, cb = 0;
+    frq::gemv_sk_scratch(sp, n, &pb, &cb);
+    float* part = nullptr;
+    uint32_t* cnt = nullptr;
+    if (int rc = sk_scratch(s, pb, cb, &part, &cnt)) return rc;
+    FRQ_HIP(frq::launch_gemv_sk(qtype, w, x, y, n, k, sp, part, cnt, s));
+    return FRQ_OK;
+}
+
 // Host dequant: stage weight, decode, copy back. n_elems may be ragged.
 int host_dequant(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, float* out) {
     if (n_elems == 0) return FRQ_OK;
@@ -123,7 +187,7 @@ int host_matmul(int qtype, const float* x, size_t seq, const uint8_t* weight, si
         return FRQ_OK;
     }
     if (int rc = have_device()) return rc;
-    if (!frq::gemv_supported(qtype, (int64_t)n, (int64_t)k))
+    if (!frq::gemv_sk_supported(qtype) && !frq::gemv_supported(qtype, (int64_t)n, (int64_t)k))
         return fail(FRQ_ERR_UNSUPPORTED, "matmul: k=%zu is beyond the single-workgroup row limit of this build", k);
     std::lock_guard<std::mutex> lk(g_ws.mu);
     const size_t wb = align256(weight_bytes), xb = align256(seq * k * 4), yb = align256(seq * n * 4);
@@ -135,7 +199,7 @@ int host_matmul(int qtype, const float* x, size_t seq, const uint8_t* weight, si
     FRQ_HIP(hipMemcpy(dw, weight, weight_bytes, hipMemcpyHostToDevice));
     FRQ_HIP(hipMemcpy(dx, x, seq * k * 4, hipMemcpyHostToDevice));
     for (size_t s = 0; s < seq; ++s)
-        FRQ_HIP(frq::launch_gemv(qtype, dw, dx + s * k, dy + s * n, (int64_t)n, (int64_t)k, nullptr, nullptr));
+        if (int rc = gemv_device(qtype, dw, dx + s * k, dy + s * n, (int64_t)n, (int64_t)k, nullptr)) return rc;
     FRQ_HIP(hipMemcpy(out, dy, seq * n * 4, hipMemcpyDeviceToHost));
     return FRQ_OK;
 }
@@ -300,7 +364,7 @@ static int dev_gemv_checks(int qtype, const void* w, size_t w_bytes, const float
     if (n == 0 || batch == 0) return FRQ_OK;
     if (!w || !x || !y) return fail(FRQ_ERR_INVALID, "null buffer");
     if (int rc = check_dev_ptrs(qtype, w, x, y)) return rc;
-    if (k > 0 && !frq::gemv_supported(qtype, n, k))
+    if (k > 0 && !frq::gemv_sk_supported(qtype) && !frq::gemv_supported(qtype, n, k))
         return fail(FRQ_ERR_UNSUPPORTED, "%s matmul: k=%lld is beyond the single-workgroup row limit of this build",
                     f->name, (long long)k);
     return FRQ_OK;
@@ -317,25 +381,54 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
         return FRQ_OK;
     }
     for (int64_t b = 0; b < batch; ++b)
-        FRQ_HIP(frq::launch_gemv(qtype, static_cast<const uint8_t*>(w), x + b * k, y + b * n, n, k, nullptr, s));
+        if (int rc = gemv_device(qtype, static_cast<const uint8_t*>(w), x + b * k, y + b * n, n, k, s)) return rc;
     return FRQ_OK;
 }
 
 int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
-                       int* cpl, int* rows_per_wg, int* unroll, int* waves, void* stream) {
+                       frq_gemv_config* cfg, void* stream) {
     Fmt f;
+    if (!cfg) return fail(FRQ_ERR_INVALID, "null config");
     if (int rc = dev_gemv_checks(qtype, w, w_bytes, x, y, n, k, 1, &f)) return rc;
     if (n == 0 || k == 0) return fail(FRQ_ERR_SHAPE, "tuned gemv needs n > 0 and k > 0");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t* wp = static_cast<const uint8_t*>(w);
+    if (cfg->kernel == FRQ_GEMV_SPLITK ||
+        (cfg->kernel == FRQ_GEMV_AUTO && !frq::gemv_supported(qtype, n, k) && frq::gemv_sk_supported(qtype))) {
+        frq::SplitKPlan p;
+        p.cpl = cfg->cpl;
+        p.rows = cfg->rows;
+        p.unroll = cfg->unroll;
+        if (!frq::plan_gemv_sk(qtype, n, k, &p)) return fail(FRQ_ERR_UNSUPPORTED, "split-K plan rejected");
+        size_t pb = 0, cb = 0;
+        frq::gemv_sk_scratch(p, n, &pb, &cb);
+        float* part = nullptr;
+        uint32_t* cnt = nullptr;
+        if (int rc = sk_scratch(s, pb, cb, &part, &cnt)) return rc;
+        hipError_t e = frq::launch_gemv_sk(qtype, wp, x, y, n, k, p, part, cnt, s);
+        if (e != hipSuccess) return hip_fail(e, "launch_gemv_sk");
+        cfg->kernel = FRQ_GEMV_SPLITK;
+        cfg->cpl = p.cpl;
+        cfg->rows = p.rows;
+        cfg->unroll = p.unroll;
+        cfg->slices = p.slices;
+        cfg->waves_per_wg = p.items >= 4 ? 4 : (int)p.items;
+        cfg->items = p.items;
+        return FRQ_OK;
+    }
     frq::GemvPlan p;
-    p.cpl = cpl ? *cpl : 0;
-    p.rows_per_wg = rows_per_wg ? *rows_per_wg : 0;
-    p.unroll = unroll ? *unroll : 0;
-    hipError_t e = frq::launch_gemv(qtype, static_cast<const uint8_t*>(w), x, y, n, k, &p, static_cast<hipStream_t>(stream));
+    p.cpl = cfg->cpl;
+    p.rows_per_wg = cfg->rows;
+    p.unroll = cfg->unroll;
+    hipError_t e = frq::launch_gemv(qtype, wp, x, y, n, k, &p, s);
     if (e != hipSuccess) return hip_fail(e, "launch_gemv");
-    if (cpl) *cpl = p.cpl;
-    if (rows_per_wg) *rows_per_wg = p.rows_per_wg;
-    if (unroll) *unroll = p.unroll;
-    if (waves) *waves = p.waves;
+    cfg->kernel = FRQ_GEMV_ROWS;
+    cfg->cpl = p.cpl;
+    cfg->rows = p.rows_per_wg;
+    cfg->unroll = p.unroll;
+    cfg->slices = 1;
+    cfg->waves_per_wg = p.waves;
+    cfg->items = p.grid;
     return FRQ_OK;
 }
 
@@ -408,5 +501,31 @@ int frq_event_elapsed_ms(float* ms, void* a, void* b) {
     return FRQ_OK;
 }
 int frq_device_synchronize(void) { FRQ_HIP(hipDeviceSynchronize()); return FRQ_OK; }
+
+int frq_stream_begin_capture(void* s) {
+    if (!s) return fail(FRQ_ERR_INVALID, "graph capture needs a created stream, not the null stream");
+    FRQ_HIP(hipStreamBeginCapture(static_cast<hipStream_t>(s), hipStreamCaptureModeThreadLocal));
+    return FRQ_OK;
+}
+int frq_stream_end_capture(void* s, void** graph_exec) {
+    if (!s || !graph_exec) return fail(FRQ_ERR_INVALID, "null stream or graph handle");
+    hipGraph_t g = nullptr;
+    FRQ_HIP(hipStreamEndCapture(static_cast<hipStream_t>(s), &g));
+    hipGraphExec_t ex = nullptr;
+    const hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    *graph_exec = ex;
+    return FRQ_OK;
+}
+int frq_graph_launch(void* ex, void* s) {
+    if (!ex) return fail(FRQ_ERR_INVALID, "null graph");
+    FRQ_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(ex), static_cast<hipStream_t>(s)));
+    return FRQ_OK;
+}
+int frq_graph_destroy(void* ex) {
+    if (ex) FRQ_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(ex)));
+    return FRQ_OK;
+}
 
 }  // extern "C"

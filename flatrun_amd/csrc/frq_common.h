@@ -18,6 +18,21 @@
 
 namespace frq {
 
+template <int V>
+struct Int {
+    static constexpr int value = V;
+};
+
+// Calls f(Int<J>{}) for J = B .. E-1 with J a compile-time constant, so array
+// indices derived from J stay constant and the arrays stay in registers.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(Int<B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 constexpr int kQ80Bytes = 34, kQ80Elems = 32;
 constexpr int kQ4KBytes = 144, kQ5KBytes = 176, kQ6KBytes = 210, kQKElems = 256;
 constexpr int kQ10Bytes = 18, kQ10Elems = 128;
@@ -85,6 +100,26 @@ __device__ __forceinline__ float dpp_mov(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float acc, float v) {
+    // acc + v[src lane]; rows outside ROW_MASK keep acc unchanged (old = 0).
+    return acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                        0xF, false));
+}
+
+// Sum over the 64 lanes of a wavefront, in VALU only (no LDS round trip):
+// four DPP steps give every lane its 16-lane row sum, then row_bcast:15 and
+// row_bcast:31 fold rows 0..3 upwards. Only lane 63 holds the total.
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+    v += dpp_mov<0xB1>(v);           // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);           // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);          // row_half_mirror
+    v += dpp_mov<0x140>(v);          // row_mirror: every lane holds its row's sum
+    v = dpp_add<0x142, 0xA>(v, v);   // row_bcast:15 -> rows 1, 3 add rows 0, 2
+    v = dpp_add<0x143, 0xC>(v, v);   // row_bcast:31 -> rows 2, 3 add lane 31
+    return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
     v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
@@ -94,5 +129,46 @@ __device__ __forceinline__ float wave_sum(float v) {
     v += __shfl_xor(v, 32, 64);
     return v;
 }
+
+// Decoded per-lane constants for the two 6-bit (scale, min) pairs 2g, 2g+1
+// of a K-quant block (get_scale_min_k4, gguf.py:135-163). With s0, s1, s2 the
+// three scale dwords:
+//   j < 4 : sc = bits [8j, 8j+6) of s0,          m = same bits of s1
+//   j >= 4: sc = bits [8(j-4), +4) of s2 | bits [8(j-4)+6, +2) of s0 << 4
+//           m  = bits [8(j-4)+4, +4) of s2 | bits [8(j-4)+6, +2) of s1 << 4
+// One v_bfe with lane-variable offset/width covers both cases; the high-bit
+// term has width 0 for j < 4.
+struct ScaleDecode {
+    bool hi;                  // g >= 2: low bits come from s2
+    uint32_t o_sc, o_m, w_a;  // offsets / width of the low-bit field (pair 2g)
+    uint32_t o_b, w_b;        // offset / width of the high-bit field (pair 2g)
+
+    __device__ __forceinline__ explicit ScaleDecode(int g) {
+        hi = g >= 2;
+        const uint32_t j = 2 * g;
+        o_sc = hi ? 8 * (j - 4) : 8 * j;
+        o_m = hi ? 8 * (j - 4) + 4 : 8 * j;
+        w_a = hi ? 4 : 6;
+        o_b = hi ? 8 * (j - 4) + 6 : 0;
+        w_b = hi ? 2 : 0;
+    }
+
+    // pair 2g -> (sc0, m0), pair 2g+1 -> (sc1, m1); the second pair's fields
+    // sit 8 bits above the first's.
+    __device__ __forceinline__ void operator()(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc0, uint32_t& m0,
+                                               uint32_t& sc1, uint32_t& m1) const {
+        const uint32_t a_sc = hi ? s2 : s0, a_m = hi ? s2 : s1;
+        sc0 = __builtin_amdgcn_ubfe(a_sc, o_sc, w_a) | (__builtin_amdgcn_ubfe(s0, o_b, w_b) << 4);
+        sc1 = __builtin_amdgcn_ubfe(a_sc, o_sc + 8, w_a) | (__builtin_amdgcn_ubfe(s0, o_b + 8, w_b) << 4);
+        m0 = __builtin_amdgcn_ubfe(a_m, o_m, w_a) | (__builtin_amdgcn_ubfe(s1, o_b, w_b) << 4);
+        m1 = __builtin_amdgcn_ubfe(a_m, o_m + 8, w_a) | (__builtin_amdgcn_ubfe(s1, o_b + 8, w_b) << 4);
+    }
+};
+
+template <int CPL>
+struct Q4KRow {
+    uint4 hd;
+    uint4 q[CPL];
+};
 
 }  // namespace frq

@@ -23,6 +23,9 @@
 //     workgroup's waves through LDS in a fixed order (deterministic output).
 //   * Scale algebra: sum_i (s*q_i - t) x_i = s * sum_i q_i x_i - t * sum_i x_i;
 //     the per-lane sums of x are computed once with x.
+#include <algorithm>
+#include <cstdint>
+
 #include "frq_common.h"
 #include "frq_kernels.h"
 
@@ -70,12 +73,25 @@ __device__ __forceinline__ void finish_rows(int64_t row0, int64_t row_end, float
 // 4 lanes per block); CPL=1 -> half a group (16 qs bytes, 32 elements,
 // 8 lanes per block). qs byte i of the unit holds element base+i in its low
 // nibble and base+32+i in its high nibble (gguf.py:209-219).
-template <int CPL, int U>
-__global__ void __launch_bounds__(512) gemv_q4_k_kernel(const uint8_t* __restrict__ w,
-                                                         const float* __restrict__ x,
-                                                         float* __restrict__ y, int64_t n, int nb,
-                                                         int rows_per_wg) {
-    extern __shared__ float red[];
+//
+// Rows stream through a ring of U register slots: each slot is refilled with
+// the row U ahead as soon as it has been consumed, so every wave keeps U rows
+// of loads in flight (HBM needs ~64 KiB outstanding per CU). The row loop is
+// fully unrolled over R rows, so the compiler's s_waitcnt before each slot
+// waits for that slot alone (a loop back-edge makes it drain every load).
+// There is no per-row guard either:
+// every workgroup runs exactly R rows (a skip path would merge a different
+// count of outstanding loads into the next row and make its wait drain the
+// queue); the last workgroup's rows past n re-read row n-1 and are dropped.
+// Each row's lane partials are reduced with DPP only; results collect in LDS
+// and y is written once at the end.
+template <int CPL, int U, int R>
+__global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) gemv_q4_k_kernel(const uint8_t* __restrict__ w,
+                                                                         const float* __restrict__ x,
+                                                                         float* __restrict__ y, int64_t n,
+                                                                         int nb) {
+    static_assert(U <= R, "ring deeper than the row count");
+    __shared__ float red[R * 16];
     constexpr int LPB = 8 / CPL;
     constexpr int NE = 16 * CPL;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
@@ -83,11 +99,28 @@ __global__ void __launch_bounds__(512) gemv_q4_k_kernel(const uint8_t* __restric
     const bool active = blk < nb;
     const int g = (CPL == 2) ? sub : (sub >> 1);
     const int hh = (CPL == 2) ? 0 : (sub & 1);
+    const ScaleDecode dec(g);
+
+    const int64_t row0 = (int64_t)blockIdx.x * R;
+    const int nrows = (int)(n - row0 < R ? n - row0 : R);
+    const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
+    const uint8_t* wb = w + (int64_t)(active ? blk : 0) * kQ4KBytes;
+    const int qoff = 16 + 32 * g + 16 * hh;
+
+    // Loads are unconditional (no control flow around them): rows past the
+    // end re-read the last row (cache hits; results not stored), and inactive
+    // lanes read block 0 with x zeroed and their partial forced to 0.
+    auto load1 = [&](Q4KRow<CPL>& t, int j) {
+        const uint8_t* p = wb + (row0 + (j < nrows ? j : nrows - 1)) * row_bytes;
+        t.hd = *reinterpret_cast<const uint4*>(p);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) t.q[c] = *reinterpret_cast<const uint4*>(p + qoff + 16 * c);
+    };
 
     float xl[NE], xh[NE];
     float sxl = 0.0f, sxh = 0.0f;
-    if (active) {
-        const float* xb = x + (int64_t)blk * kQKElems + 64 * g + 16 * hh;
+    {
+        const float* xb = x + (int64_t)(active ? blk : 0) * kQKElems + 64 * g + 16 * hh;
 #pragma unroll
         for (int i = 0; i < NE; i += 4) {
             const float4 a = *reinterpret_cast<const float4*>(xb + i);
@@ -95,71 +128,65 @@ __global__ void __launch_bounds__(512) gemv_q4_k_kernel(const uint8_t* __restric
             xl[i] = a.x; xl[i + 1] = a.y; xl[i + 2] = a.z; xl[i + 3] = a.w;
             xh[i] = c.x; xh[i + 1] = c.y; xh[i + 2] = c.z; xh[i + 3] = c.w;
         }
-    } else {
-#pragma unroll
-        for (int i = 0; i < NE; ++i) { xl[i] = 0.0f; xh[i] = 0.0f; }
     }
+    // x first, then the first U rows, then the first use of x: waiting for
+    // x (in-order vmcnt) leaves every row load in flight. The barriers keep
+    // the scheduler from reordering the three phases. Inactive lanes keep
+    // block 0's x; their partial is discarded by a select below.
+    __builtin_amdgcn_sched_barrier(0);
+    Q4KRow<CPL> ring[U];
 #pragma unroll
-    for (int i = 0; i < NE; ++i) { sxl += xl[i]; sxh += xh[i]; }
+    for (int i = 0; i < U; ++i) load1(ring[i], i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        sxl += xl[i];
+        sxh += xh[i];
+    }
 
-    const int64_t row0 = (int64_t)blockIdx.x * rows_per_wg;
-    const int64_t row_end = row0 + rows_per_wg < n ? row0 + rows_per_wg : n;
-    const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
-    const uint8_t* wb = w + row0 * row_bytes + (int64_t)blk * kQ4KBytes;
-    const int qoff = 16 + 32 * g + 16 * hh;
-
-    for (int64_t rb = row0; rb < row_end; rb += U) {
-        uint4 hd[U];
-        uint4 q[U][CPL];
+    static_for<0, R>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        Q4KRow<CPL>& t = ring[j % U];
+        uint32_t sc0, m0, sc1, m1;
+        dec(t.hd.y, t.hd.z, t.hd.w, sc0, m0, sc1, m1);
+        const float d = f16_bits_to_f32(t.hd.x), dm = f16_bits_to_f32(t.hd.x >> 16);
+        float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (active && rb + u < row_end) {
-                const uint8_t* p = wb + (rb - row0 + u) * row_bytes;
-                hd[u] = *reinterpret_cast<const uint4*>(p);
+        for (int c = 0; c < CPL; ++c) {
+            const uint32_t qw[4] = {t.q[c].x, t.q[c].y, t.q[c].z, t.q[c].w};
 #pragma unroll
-                for (int c = 0; c < CPL; ++c) q[u][c] = *reinterpret_cast<const uint4*>(p + qoff + 16 * c);
-            } else {
-                hd[u] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-                for (int c = 0; c < CPL; ++c) q[u][c] = make_uint4(0, 0, 0, 0);
+            for (int wd = 0; wd < 4; ++wd) {
+                const uint32_t lo = vand(qw[wd], 0x0F0F0F0Fu);
+                const uint32_t hi = vand(qw[wd], 0xF0F0F0F0u);   // 16 * high nibble
+                const int e = 16 * c + 4 * wd;
+                a0 = __builtin_fmaf(byte_f(lo, 0), xl[e + 0], a0);
+                a1 = __builtin_fmaf(byte_f(lo, 1), xl[e + 1], a1);
+                a0 = __builtin_fmaf(byte_f(lo, 2), xl[e + 2], a0);
+                a1 = __builtin_fmaf(byte_f(lo, 3), xl[e + 3], a1);
+                b0 = __builtin_fmaf(byte_f(hi, 0), xh[e + 0], b0);
+                b1 = __builtin_fmaf(byte_f(hi, 1), xh[e + 1], b1);
+                b0 = __builtin_fmaf(byte_f(hi, 2), xh[e + 2], b0);
+                b1 = __builtin_fmaf(byte_f(hi, 3), xh[e + 3], b1);
             }
         }
-        float part[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            uint32_t sc0, m0, sc1, m1;
-            k4_scale_min(hd[u].y, hd[u].z, hd[u].w, 2 * g, sc0, m0);
-            k4_scale_min(hd[u].y, hd[u].z, hd[u].w, 2 * g + 1, sc1, m1);
-            const float d = f16_bits_to_f32(hd[u].x), dm = f16_bits_to_f32(hd[u].x >> 16);
-            float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) {
-                const uint32_t qw[4] = {q[u][c].x, q[u][c].y, q[u][c].z, q[u][c].w};
-#pragma unroll
-                for (int wd = 0; wd < 4; ++wd) {
-                    const uint32_t lo = vand(qw[wd], 0x0F0F0F0Fu);
-                    const uint32_t hi = vand(qw[wd], 0xF0F0F0F0u);   // 16 * high nibble
-                    const int e = 16 * c + 4 * wd;
-                    a0 = __builtin_fmaf(byte_f(lo, 0), xl[e + 0], a0);
-                    a1 = __builtin_fmaf(byte_f(lo, 1), xl[e + 1], a1);
-                    a0 = __builtin_fmaf(byte_f(lo, 2), xl[e + 2], a0);
-                    a1 = __builtin_fmaf(byte_f(lo, 3), xl[e + 3], a1);
-                    b0 = __builtin_fmaf(byte_f(hi, 0), xh[e + 0], b0);
-                    b1 = __builtin_fmaf(byte_f(hi, 1), xh[e + 1], b1);
-                    b0 = __builtin_fmaf(byte_f(hi, 2), xh[e + 2], b0);
-                    b1 = __builtin_fmaf(byte_f(hi, 3), xh[e + 3], b1);
-                }
-            }
-            const float s0 = d * (float)sc0, t0 = dm * (float)m0;
-            const float s1 = d * (float)sc1 * 0.0625f, t1 = dm * (float)m1;
-            float pu = s0 * (a0 + a1);
-            pu = __builtin_fmaf(-t0, sxl, pu);
-            pu = __builtin_fmaf(s1, b0 + b1, pu);
-            part[u] = __builtin_fmaf(-t1, sxh, pu);
-        }
-        row_partials_out<U>(part, rb, row0, row_end, y, red, nwaves, wave, lane);
+        if constexpr (j + U < R) load1(t, j + U);               // refill the slot: row j + U
+        const float s0 = d * (float)sc0, t0 = dm * (float)m0;
+        const float s1 = (d * 0.0625f) * (float)sc1, t1 = dm * (float)m1;
+        float pu = s0 * (a0 + a1);
+        pu = __builtin_fmaf(-t0, sxl, pu);
+        pu = __builtin_fmaf(s1, b0 + b1, pu);
+        pu = __builtin_fmaf(-t1, sxh, pu);
+        // results go to LDS (lgkmcnt): a global store would count in vmcnt
+        // and force waits on the in-flight row loads.
+        const float v = wave_sum_lane63(active ? pu : 0.0f);
+        if (lane == 63) red[j * nwaves + wave] = v;
+    });
+    __syncthreads();
+    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+        float s = 0.0f;
+        for (int w2 = 0; w2 < nwaves; ++w2) s += red[r * nwaves + w2];
+        y[row0 + r] = s;
     }
-    finish_rows(row0, row_end, y, red, nwaves);
 }
 
 // ------------------------------------------------------------------ Q5_K
@@ -539,7 +566,8 @@ bool cpl_valid(int qtype, int cpl) {
     }
 }
 
-constexpr int64_t kMaxLanes = 512;   // matches __launch_bounds__(512)
+// Workgroup size cap of each kernel (its __launch_bounds__).
+int64_t max_lanes(int qtype, int cpl) { return (qtype == kTypeQ4K && cpl == 1) ? 1024 : 512; }
 
 // Smallest-waste work unit whose row fits in one workgroup.
 int pick_cpl(int qtype, int64_t nb) {
@@ -548,7 +576,7 @@ int pick_cpl(int qtype, int64_t nb) {
     for (int cpl = 1; cpl <= 4; cpl *= 2) {
         if (!cpl_valid(qtype, cpl)) continue;
         const int64_t lanes = nb * lanes_per_block(qtype, cpl);
-        if (lanes > kMaxLanes) continue;
+        if (lanes > max_lanes(qtype, cpl)) continue;
         const int64_t padded = (lanes + 63) / 64 * 64;
         const double waste = (double)(padded - lanes) / (double)padded;
         // prefer larger units on ties: fewer scale decodes per element
@@ -589,16 +617,84 @@ bool unroll8_ok(int qtype, int cpl) {
     return !((qtype == kTypeQ4K && cpl == 2) || (qtype == kTypeQ6K && cpl == 4) || qtype == kTypeQ5K);
 }
 
+// Q4_K: rows per workgroup is a compile-time constant of the kernel, one of
+// these; the ring depth is 3 or 5 slots (CPL 2) and 4, 6 or 8 (CPL 1).
+constexpr int kQ4KRowSet[] = {1, 2, 4, 7, 8, 14, 16};
+
+bool q4k_rows_ok(int r) {
+    for (int v : kQ4KRowSet)
+        if (v == r) return true;
+    return false;
+}
+
+int q4k_ring(int cpl, int want) {
+    if (cpl == 2) return want <= 3 ? 3 : 5;
+    return want <= 4 ? 4 : (want <= 6 ? 6 : 8);
+}
+
+// Rows per Q4_K workgroup: minimise the rows the busiest CU runs, counting
+// ~2 rows of start-up (x load, first loads in flight) per round of resident
+// workgroups. `waves` is the workgroup size; a CU holds 16 waves of the CPL 1
+// kernel and 12 of the CPL 2 kernel (VGPR budget).
+int pick_rows_q4k(int64_t n, int waves, int cpl) {
+    const int64_t kCUs = 256;
+    const int64_t per_cu = std::max<int64_t>(1, (cpl == 1 ? 16 : 12) / waves);
+    int best = 1;
+    int64_t best_cost = INT64_MAX;
+    for (int r : kQ4KRowSet) {
+        const int64_t grid = (n + r - 1) / r;
+        const int64_t cost = (grid + kCUs - 1) / kCUs * r + 2 * ((grid + kCUs * per_cu - 1) / (kCUs * per_cu));
+        if (cost < best_cost || (cost == best_cost && r > best)) {
+            best = r;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
+template <int CPL, int U, int R>
+void q4k_go(dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n, int nb) {
+    gemv_q4_k_kernel<CPL, (U < R ? U : R), R><<<gd, bd, 0, s>>>(w, x, y, n, nb);
+}
+
+template <int CPL, int U>
+bool q4k_rows(int rows, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n,
+              int nb) {
+    switch (rows) {
+        case 1: q4k_go<CPL, U, 1>(gd, bd, s, w, x, y, n, nb); return true;
+        case 2: q4k_go<CPL, U, 2>(gd, bd, s, w, x, y, n, nb); return true;
+        case 4: q4k_go<CPL, U, 4>(gd, bd, s, w, x, y, n, nb); return true;
+        case 7: q4k_go<CPL, U, 7>(gd, bd, s, w, x, y, n, nb); return true;
+        case 8: q4k_go<CPL, U, 8>(gd, bd, s, w, x, y, n, nb); return true;
+        case 14: q4k_go<CPL, U, 14>(gd, bd, s, w, x, y, n, nb); return true;
+        case 16: q4k_go<CPL, U, 16>(gd, bd, s, w, x, y, n, nb); return true;
+        default: return false;
+    }
+}
+
+hipError_t launch_q4k(int cpl, int ring, int rows, int waves, int64_t grid, const uint8_t* w, const float* x,
+                      float* y, int64_t n, int nb, hipStream_t s) {
+    const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
+    bool ok = false;
+    if (cpl == 2) {
+        ok = ring == 3 ? q4k_rows<2, 3>(rows, gd, bd, s, w, x, y, n, nb) : q4k_rows<2, 5>(rows, gd, bd, s, w, x, y, n, nb);
+    } else if (ring == 4) {
+        ok = q4k_rows<1, 4>(rows, gd, bd, s, w, x, y, n, nb);
+    } else if (ring == 6) {
+        ok = q4k_rows<1, 6>(rows, gd, bd, s, w, x, y, n, nb);
+    } else {
+        ok = q4k_rows<1, 8>(rows, gd, bd, s, w, x, y, n, nb);
+    }
+    if (!ok) return hipErrorInvalidConfiguration;
+    return hipGetLastError();
+}
+
 template <int U>
 hipError_t launch_u(int qtype, int cpl, const uint8_t* w, const float* x, float* y, int64_t n, int nb,
                     int rows, int waves, int64_t grid, hipStream_t s) {
     const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
     const size_t lds = waves > 1 ? sizeof(float) * (size_t)rows * waves : 0;
     switch (qtype) {
-        case kTypeQ4K:
-            if (cpl == 2) gemv_q4_k_kernel<2, 4><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
-            else gemv_q4_k_kernel<1, U><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
-            break;
         case kTypeQ5K: gemv_q5_k_kernel<4><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows); break;
         case kTypeQ6K:
             if (cpl == 4) gemv_q6_k_kernel<4, 4><<<gd, bd, lds, s>>>(w, x, y, n, nb, rows);
@@ -637,11 +733,20 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
     if (p.cpl <= 0) p.cpl = pick_cpl(qtype, nb);
     if (!cpl_valid(qtype, p.cpl)) return hipErrorInvalidValue;
     const int64_t lanes = nb * lanes_per_block(qtype, p.cpl);
-    if (lanes > kMaxLanes) return hipErrorInvalidConfiguration;
+    if (lanes > max_lanes(qtype, p.cpl)) return hipErrorInvalidConfiguration;
     p.waves = (int)((lanes + 63) / 64);
+    if (qtype == kTypeQ4K) {
+        if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q4k(n, p.waves, p.cpl);
+        if (!q4k_rows_ok(p.rows_per_wg)) return hipErrorInvalidConfiguration;
+        p.unroll = q4k_ring(p.cpl, p.unroll > 0 ? p.unroll : (p.cpl == 1 ? 6 : 5));
+        p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
+        if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+        if (plan) *plan = p;
+        return launch_q4k(p.cpl, p.unroll, p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
+    }
     if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows(n, p.waves);
     if (p.unroll != 4 && p.unroll != 8) p.unroll = p.rows_per_wg >= 8 ? 8 : 4;
-    if (!unroll8_ok(qtype, p.cpl)) p.unroll = 4;
+    if (p.unroll == 8 && !unroll8_ok(qtype, p.cpl)) p.unroll = 4;
     p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
     if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
     if (plan) *plan = p;

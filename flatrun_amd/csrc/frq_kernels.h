@@ -40,4 +40,27 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
 // Checks that a GEMV of this shape can be planned; returns false with no launch otherwise.
 bool gemv_supported(int qtype, int64_t n, int64_t k);
 
+// Split-K, software-pipelined GEMV (frq_gemv_sk.hip). Fields left <= 0 are
+// chosen by plan_gemv_sk.
+struct SplitKPlan {
+    int cpl = 0;             // work unit per lane (format specific)
+    int rows = 0;            // rows per work item (one wavefront), <= 64
+    int unroll = 0;          // rows per load batch (2 or 4)
+    int slices = 0;          // K-slices per row (derived)
+    int unit_base = 0;       // work units per slice (derived; first unit_rem slices get one more)
+    int unit_rem = 0;
+    int64_t row_blocks = 0;  // ceil(n / rows) (derived)
+    int64_t items = 0;       // work items = wavefronts launched (derived)
+};
+
+bool gemv_sk_supported(int qtype);
+bool plan_gemv_sk(int qtype, int64_t n, int64_t k, SplitKPlan* plan);
+// Device scratch a plan needs (both 0 when slices == 1): `counter_bytes` of
+// per-row-block counters, which must be zero before the first launch and
+// which every launch leaves zero (keep them in memory nothing else writes),
+// and `partial_bytes` for n * slices partial sums.
+void gemv_sk_scratch(const SplitKPlan& plan, int64_t n, size_t* partial_bytes, size_t* counter_bytes);
+hipError_t launch_gemv_sk(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k,
+                          const SplitKPlan& plan, float* partials, uint32_t* counters, hipStream_t stream);
+
 }  // namespace frq

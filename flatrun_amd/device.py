@@ -176,6 +176,66 @@ class Event:
             pass
 
 
+class Graph:
+    """A recorded launch sequence, replayed with one call.
+
+    ``with Graph.capture(stream) as g: ...`` records every launch issued on
+    ``stream`` inside the block (nothing runs then); ``g.launch(stream)``
+    replays it. The stream must be a :class:`Stream`, not the null stream.
+    """
+
+    def __init__(self, handle: int):
+        self.handle = handle
+
+    @classmethod
+    def capture(cls, stream: "Stream"):
+        return _Capture(stream)
+
+    def launch(self, stream=None) -> None:
+        check(lib().frq_graph_launch(self.handle, _stream(stream)))
+
+    def destroy(self) -> None:
+        if getattr(self, "handle", 0):
+            try:
+                lib().frq_graph_destroy(self.handle)
+            finally:
+                self.handle = 0
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class _Capture:
+    def __init__(self, stream: "Stream"):
+        if not isinstance(stream, Stream):
+            raise TypeError("graph capture needs a device.Stream")
+        self.stream = stream
+        self.graph: Graph | None = None
+
+    def __enter__(self) -> "_Capture":
+        check(lib().frq_stream_begin_capture(self.stream.handle))
+        return self
+
+    def __exit__(self, et, ev, tb) -> None:
+        h = ctypes.c_void_p()
+        rc = lib().frq_stream_end_capture(self.stream.handle, ctypes.byref(h))
+        if et is None:
+            check(rc)
+            self.graph = Graph(int(h.value or 0))
+        elif rc == 0 and h.value:
+            lib().frq_graph_destroy(h.value)
+
+    def launch(self, stream=None) -> None:
+        self.graph.launch(stream)
+
+    def destroy(self) -> None:
+        if self.graph is not None:
+            self.graph.destroy()
+
+
 def synchronize() -> None:
     check(lib().frq_device_synchronize())
 
@@ -193,15 +253,16 @@ def gemv(qtype, w, x, y, n: int, k: int, batch: int = 1, stream=None, w_bytes: i
     check(lib().frq_dev_gemv(q, _addr(w), wb, _addr(x), _addr(y), int(n), int(k), int(batch), _stream(stream)))
 
 
-def gemv_tuned(qtype, w, x, y, n: int, k: int, cpl: int = 0, rows_per_wg: int = 0, unroll: int = 0,
+def gemv_tuned(qtype, w, x, y, n: int, k: int, kernel: int = 0, cpl: int = 0, rows: int = 0, unroll: int = 0,
                stream=None, w_bytes: int | None = None) -> dict:
-    """One GEMV with an explicit launch geometry; returns the geometry used."""
+    """One GEMV with an explicit launch geometry; returns the geometry used
+    (fields of frq_gemv_config)."""
     q = qtype_id(qtype)
     wb = _nbytes(w) if w_bytes is None else int(w_bytes)
-    c, r, u, wv = ctypes.c_int(cpl), ctypes.c_int(rows_per_wg), ctypes.c_int(unroll), ctypes.c_int(0)
-    check(lib().frq_dev_gemv_tuned(q, _addr(w), wb, _addr(x), _addr(y), int(n), int(k), ctypes.byref(c),
-                                   ctypes.byref(r), ctypes.byref(u), ctypes.byref(wv), _stream(stream)))
-    return {"cpl": c.value, "rows_per_wg": r.value, "unroll": u.value, "waves": wv.value}
+    cfg = _lib.GemvConfig(kernel=kernel, cpl=cpl, rows=rows, unroll=unroll)
+    check(lib().frq_dev_gemv_tuned(q, _addr(w), wb, _addr(x), _addr(y), int(n), int(k), ctypes.addressof(cfg),
+                                   _stream(stream)))
+    return cfg.as_dict()
 
 
 def copy(dst, src, nbytes: int, stream=None) -> None:

@@ -130,11 +130,26 @@ int frq_dev_dequant(int qtype, const void* w, size_t w_bytes, int64_t n_elems, f
 int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
                  int64_t batch, void* stream);
 
-/* frq_dev_gemv with an explicit launch geometry (cpl = work unit per lane,
- * rows_per_wg, unroll 4|8; 0 = library choice). Reports the geometry used
- * through the same pointers. For tuning sweeps and profiling. */
+/* Launch geometry of one GEMV, for tuning sweeps and profiling. Fields set
+ * to 0 are chosen by the library; on return every field holds what ran.
+ *   kernel        FRQ_GEMV_AUTO, FRQ_GEMV_SPLITK (one wavefront per
+ *                 (row block, K-slice) work item, deterministic split-K
+ *                 fixup) or FRQ_GEMV_ROWS (one workgroup spans all of k)
+ *   cpl           work unit per lane (format specific)
+ *   rows          rows per work item (SPLITK) / per workgroup (ROWS)
+ *   unroll        rows per load batch
+ *   slices        K-slices per row (output)
+ *   waves_per_wg  wavefronts per workgroup (output)
+ *   items         work items / workgroups launched (output)              */
+enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2 };
+typedef struct {
+    int32_t kernel, cpl, rows, unroll, slices, waves_per_wg;
+    int64_t items;
+} frq_gemv_config;
+
+/* frq_dev_gemv with an explicit launch geometry (batch 1). */
 int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
-                       int* cpl, int* rows_per_wg, int* unroll, int* waves, void* stream);
+                       frq_gemv_config* cfg, void* stream);
 
 /* dst = src on the device with a plain 16-byte-per-lane streaming kernel:
  * the reference point for calibrating HBM traffic counters (bytes a
@@ -164,6 +179,21 @@ int frq_event_record(void* event, void* stream);
 int frq_event_synchronize(void* event);
 int frq_event_elapsed_ms(float* ms, void* start, void* stop);
 int frq_device_synchronize(void);
+
+/* ------------------------------------------------------------ HIP graphs
+ * Record a fixed launch sequence once and replay it with one call: a decode
+ * step issues one GEMV per weight (224 for a 32-layer Llama block stack),
+ * and replay removes the per-launch host cost. Capture runs on a stream made
+ * by frq_stream_create (not the null stream), in thread-local mode. Entry
+ * points that allocate on first use (the split-K scratch of very long rows,
+ * the host workspace) must have run once for the shape before capture.
+ * Captured work records kernels only (no memset nodes). No reference
+ * counterpart: the reference calls its matmuls one by one from Python.     */
+int frq_stream_begin_capture(void* stream);
+/* Ends the capture and instantiates it; *graph_exec receives the handle. */
+int frq_stream_end_capture(void* stream, void** graph_exec);
+int frq_graph_launch(void* graph_exec, void* stream);
+int frq_graph_destroy(void* graph_exec);
 
 #ifdef __cplusplus
 }

@@ -104,33 +104,60 @@ def test_gemv_k_zero_and_n_zero(frq, q):
     assert gpu_matmul(q, np.ones(be, np.float32), np.zeros(0, np.uint8), 0, be).shape == (0,)
 
 
-@pytest.mark.parametrize("q,n,k", [("Q4_K", 300, 18944), ("Q4_K", 600, 3584), ("Q6_K", 300, 3584), ("Q8_0", 500, 896),
-                                   ("Q1_0", 300, 4096)])
+@pytest.mark.parametrize("q,n,k", [("Q4_K", 300, 18944), ("Q4_K", 600, 3584), ("Q4_K", 97, 14336),
+                                   ("Q6_K", 300, 3584), ("Q8_0", 500, 896), ("Q1_0", 300, 4096)])
 def test_launch_geometry_sweep(frq, q, n, k):
-    """Every supported geometry (work unit, rows per workgroup, unroll) gives a
-    result within tolerance; geometries that share a work unit give identical bits."""
+    """Every supported geometry of both kernel families (split-K work items and
+    whole-row workgroups) is within tolerance; for a fixed kernel family and
+    work unit, the row tiling never changes the bits (per-row order is fixed)."""
+    from flatrun_amd import _lib
+
     raw = synth.make_blocks(q, n, k, seed=5)
     x = synth.make_x(k, seed=6)
     y64, absw = G.matmul_f64(q, x, raw, n, k), G.abs_matmul_f64(q, x, raw, n, k)
     w = device.DeviceBuffer.from_host(raw)
     xd = device.DeviceBuffer.from_host(x)
     yd = device.DeviceBuffer(n * 4)
-    by_cpl = {}
-    for cpl in (1, 2, 4):
-        for rows in (1, 3, 7, 8, 16, 32):
-            for unroll in (4, 8):
-                try:
-                    plan = device.gemv_tuned(q, w, xd, yd, n, k, cpl=cpl, rows_per_wg=rows, unroll=unroll)
-                except RuntimeError:
-                    continue                         # work unit not valid for this format / k
-                device.synchronize()
-                y = yd.to_host(np.float32)
-                assert_matvec_close(y, y64, absw, what=f"{plan}")
-                if plan["cpl"] in by_cpl:
-                    assert bits_equal(y, by_cpl[plan["cpl"]]), plan
-                else:
-                    by_cpl[plan["cpl"]] = y
-    assert by_cpl
+    seen = {}
+    for kernel in (_lib.GEMV_SPLITK, _lib.GEMV_ROWS):
+        for cpl in (1, 2, 4):
+            for rows in (1, 3, 4, 7, 8, 16, 32, 64):
+                for unroll in (2, 4, 8):
+                    try:
+                        cfg = device.gemv_tuned(q, w, xd, yd, n, k, kernel=kernel, cpl=cpl, rows=rows, unroll=unroll)
+                    except RuntimeError:
+                        continue                     # geometry not valid for this format / k
+                    device.synchronize()
+                    y = yd.to_host(np.float32)
+                    assert_matvec_close(y, y64, absw, what=f"{cfg}")
+                    key = (cfg["kernel"], cfg["cpl"])
+                    if key in seen:
+                        assert bits_equal(y, seen[key]), cfg
+                    else:
+                        seen[key] = y
+    assert seen
+
+
+def test_split_k_repeated_launches(frq):
+    """The split-K counters are left at zero: many launches in a row, and
+    launches alternating between shapes sharing the scratch, stay correct."""
+    n1, k1, n2, k2 = 257, 18944, 64, 8192
+    r1, r2 = synth.make_blocks("Q4_K", n1, k1, seed=1), synth.make_blocks("Q4_K", n2, k2, seed=2)
+    x1, x2 = synth.make_x(k1, seed=3), synth.make_x(k2, seed=4)
+    w1, w2 = device.DeviceBuffer.from_host(r1), device.DeviceBuffer.from_host(r2)
+    xd1, xd2 = device.DeviceBuffer.from_host(x1), device.DeviceBuffer.from_host(x2)
+    y1, y2 = device.DeviceBuffer(n1 * 4), device.DeviceBuffer(n2 * 4)
+    device.gemv("Q4_K", w1, xd1, y1, n1, k1)
+    device.gemv("Q4_K", w2, xd2, y2, n2, k2)
+    device.synchronize()
+    ref1, ref2 = y1.to_host(np.float32), y2.to_host(np.float32)
+    assert_matvec_close(ref1, G.matmul_f64("Q4_K", x1, r1, n1, k1), G.abs_matmul_f64("Q4_K", x1, r1, n1, k1))
+    for _ in range(50):
+        device.gemv("Q4_K", w1, xd1, y1, n1, k1)
+        device.gemv("Q4_K", w2, xd2, y2, n2, k2)
+    device.synchronize()
+    assert bits_equal(y1.to_host(np.float32), ref1)
+    assert bits_equal(y2.to_host(np.float32), ref2)
 
 
 def test_resident_weights_match_host_path(backend):
@@ -141,3 +168,39 @@ def test_resident_weights_match_host_path(backend):
     assert bits_equal(backend.matmul_q4k(x, w, n, k), backend.matmul_q4k(x, raw, n, k))
     xs = synth.make_x(k, seed=10, batch=4)
     assert bits_equal(backend.matmul_q4k(xs, w, n, k), backend.matmul_q4k(xs, raw, n, k))
+
+
+def test_graph_replay_matches_eager(frq):
+    """A captured sequence of GEMVs (three formats, k = 0 fill included)
+    replays to the eager bits every time, with eager work and host syncs
+    between the replays."""
+    cases = [("Q4_K", 3584, 9472), ("Q6_K", 300, 3584), ("Q8_0", 500, 896), ("Q4_K", 7, 0)]
+    s = device.Stream()
+    bufs = []
+    for i, (q, n, k) in enumerate(cases):
+        raw = synth.make_blocks(q, n, k, seed=40 + i) if k else np.zeros(0, np.uint8)
+        x = synth.make_x(max(k, 1), seed=50 + i)
+        bufs.append((q, n, k, device.DeviceBuffer.from_host(raw) if k else device.DeviceBuffer(16), device.DeviceBuffer.from_host(x),
+                     device.DeviceBuffer(4 * n)))
+
+    def run_all():
+        for q, n, k, w, xd, yd in bufs:
+            device.gemv(q, w, xd, yd, n, k, stream=s, w_bytes=synth.nbytes(q, n, k) if k else 0)
+
+    run_all()
+    s.synchronize()
+    eager = [yd.to_host(np.float32) for *_, yd in bufs]
+    with device.Graph.capture(s) as cap:
+        run_all()
+    try:
+        for rep in range(4):
+            for *_, yd in bufs:
+                device.copy(yd, bufs[0][4], 16, stream=s)   # clobber y eagerly before each replay
+            cap.launch(s)
+            s.synchronize()
+            for (q, n, k, _, _, yd), ref in zip(bufs, eager):
+                assert bits_equal(yd.to_host(np.float32), ref), (rep, q, n, k)
+            run_all()                                       # eager work between replays
+            s.synchronize()
+    finally:
+        cap.destroy()
