@@ -46,6 +46,18 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 ROTATE_BYTES = 1 << 30         # >= 1 GiB of distinct copies per workload
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "q4_k_gemv_3584x18944.traffic.json"
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per launch of the headline kernel, from the committed
+    rocprofv3 FETCH_SIZE + WRITE_SIZE summary (copy-calibrated), if present."""
+    try:
+        return int(json.loads(TRAFFIC_FILE.read_text())["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def effective_bytes(q: str, n: int, k: int, batch: int = 1) -> int:
     return synth.nbytes(q, n, k) + 4 * k * batch + 4 * n * batch
 
@@ -231,6 +243,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-suite", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after the headline, run the library's streaming copy 20 times over MIB MiB "
+                         "(reference traffic for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU (the matvec path is single-device); "
@@ -270,10 +285,18 @@ def main() -> int:
                    "effective_bytes_per_step": work.bytes, "weight_copies_rotated": work.ncopies,
                    "rotation_bytes": work.ncopies * work.raw.nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel_us": round(t_kernel * 1e6, 3)},
         "eager_launch_us": round(t_eager * 1e6, 3),
     }
+    if a.copy_calibration > 0:
+        nbytes = a.copy_calibration << 20
+        src, dst = device.DeviceBuffer(nbytes), device.DeviceBuffer(nbytes)
+        for _ in range(20):
+            device.copy(dst, src, nbytes, stream=stream)
+        device.synchronize()
+        src.free()
+        dst.free()
     if not a.no_suite:
         rec["configs"] = run_suite(stream, steps=min(a.steps, 500))
         rec["decode_step_ms_resident"] = rec["configs"]["llama3_8b_decode_resident"]["ms_per_step"]

@@ -86,6 +86,28 @@ __device__ __forceinline__ uint32_t vand_or(uint32_t a, uint32_t mask, uint32_t 
     asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(c));
     return r;
 }
+// Both nibble planes of a qs dword as eight floats: f[0..3] = the low nibbles
+// of bytes 0..3, f[4..7] = 16 * the high nibbles. One asm block, so the eight
+// conversions issue back to back and the FMAs that consume them come later;
+// left to itself the compiler pairs every conversion with its FMA, and the
+// FMA then waits on the conversion it follows.
+__device__ __forceinline__ void nibbles8(uint32_t w, float (&f)[8]) {
+    uint32_t lo, hi;
+    asm("v_and_b32 %0, %10, %12\n\t"
+        "v_and_b32 %1, %11, %12\n\t"
+        "v_cvt_f32_ubyte0 %2, %0\n\t"
+        "v_cvt_f32_ubyte0 %6, %1\n\t"
+        "v_cvt_f32_ubyte1 %3, %0\n\t"
+        "v_cvt_f32_ubyte1 %7, %1\n\t"
+        "v_cvt_f32_ubyte2 %4, %0\n\t"
+        "v_cvt_f32_ubyte2 %8, %1\n\t"
+        "v_cvt_f32_ubyte3 %5, %0\n\t"
+        "v_cvt_f32_ubyte3 %9, %1"
+        : "=&v"(lo), "=&v"(hi), "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]),
+          "=&v"(f[6]), "=&v"(f[7])
+        : "s"(0x0F0F0F0Fu), "s"(0xF0F0F0F0u), "v"(w));
+}
+
 // Byte b of w as float: one v_cvt_f32_ubyte<b>.
 __device__ __forceinline__ float byte_f(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
 

@@ -156,17 +156,17 @@ __global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) gemv_q4_k_kernel(const 
             const uint32_t qw[4] = {t.q[c].x, t.q[c].y, t.q[c].z, t.q[c].w};
 #pragma unroll
             for (int wd = 0; wd < 4; ++wd) {
-                const uint32_t lo = vand(qw[wd], 0x0F0F0F0Fu);
-                const uint32_t hi = vand(qw[wd], 0xF0F0F0F0u);   // 16 * high nibble
+                float f[8];                                       // f[4..7] = 16 * high nibble
+                nibbles8(qw[wd], f);
                 const int e = 16 * c + 4 * wd;
-                a0 = __builtin_fmaf(byte_f(lo, 0), xl[e + 0], a0);
-                a1 = __builtin_fmaf(byte_f(lo, 1), xl[e + 1], a1);
-                a0 = __builtin_fmaf(byte_f(lo, 2), xl[e + 2], a0);
-                a1 = __builtin_fmaf(byte_f(lo, 3), xl[e + 3], a1);
-                b0 = __builtin_fmaf(byte_f(hi, 0), xh[e + 0], b0);
-                b1 = __builtin_fmaf(byte_f(hi, 1), xh[e + 1], b1);
-                b0 = __builtin_fmaf(byte_f(hi, 2), xh[e + 2], b0);
-                b1 = __builtin_fmaf(byte_f(hi, 3), xh[e + 3], b1);
+                a0 = __builtin_fmaf(f[0], xl[e + 0], a0);
+                a1 = __builtin_fmaf(f[1], xl[e + 1], a1);
+                b0 = __builtin_fmaf(f[4], xh[e + 0], b0);
+                b1 = __builtin_fmaf(f[5], xh[e + 1], b1);
+                a0 = __builtin_fmaf(f[2], xl[e + 2], a0);
+                a1 = __builtin_fmaf(f[3], xl[e + 3], a1);
+                b0 = __builtin_fmaf(f[6], xh[e + 2], b0);
+                b1 = __builtin_fmaf(f[7], xh[e + 3], b1);
             }
         }
         if constexpr (j + U < R) load1(t, j + U);               // refill the slot: row j + U
@@ -569,8 +569,12 @@ bool cpl_valid(int qtype, int cpl) {
 // Workgroup size cap of each kernel (its __launch_bounds__).
 int64_t max_lanes(int qtype, int cpl) { return (qtype == kTypeQ4K && cpl == 1) ? 1024 : 512; }
 
-// Smallest-waste work unit whose row fits in one workgroup.
+// Work unit: Q4_K always takes the 16-byte unit (8 lanes per block) when the
+// row fits a workgroup (twice the waves of the 32-byte unit, which measured
+// slower on every shape); the other formats take the smallest-waste unit
+// whose row fits in one workgroup.
 int pick_cpl(int qtype, int64_t nb) {
+    if (qtype == kTypeQ4K) return nb * 8 <= max_lanes(qtype, 1) ? 1 : 0;
     int best = 0;
     double best_waste = 2.0;
     for (int cpl = 1; cpl <= 4; cpl *= 2) {
@@ -618,7 +622,7 @@ bool unroll8_ok(int qtype, int cpl) {
 }
 
 // Q4_K: rows per workgroup is a compile-time constant of the kernel, one of
-// these; the ring depth is 3 or 5 slots (CPL 2) and 4, 6 or 8 (CPL 1).
+// these; the ring depth is 3 or 5 slots (CPL 2) and 4 or 6 (CPL 1).
 constexpr int kQ4KRowSet[] = {1, 2, 4, 7, 8, 14, 16};
 
 bool q4k_rows_ok(int r) {
@@ -629,27 +633,20 @@ bool q4k_rows_ok(int r) {
 
 int q4k_ring(int cpl, int want) {
     if (cpl == 2) return want <= 3 ? 3 : 5;
-    return want <= 4 ? 4 : (want <= 6 ? 6 : 8);
+    return want <= 4 ? 4 : 6;
 }
 
-// Rows per Q4_K workgroup: minimise the rows the busiest CU runs, counting
-// ~2 rows of start-up (x load, first loads in flight) per round of resident
-// workgroups. `waves` is the workgroup size; a CU holds 16 waves of the CPL 1
-// kernel and 12 of the CPL 2 kernel (VGPR budget).
-int pick_rows_q4k(int64_t n, int waves, int cpl) {
+// Rows per Q4_K workgroup (measured on MI355X, 256 CUs). Workgroups of 4 or
+// more waves run one per CU: take the fewest rows that still cover n with
+// at most 256 workgroups (one round, every CU busy). Smaller workgroups
+// (short rows) want several resident per CU: 4 rows per workgroup up to
+// n = 8192, 7 beyond.
+int pick_rows_q4k(int64_t n, int waves) {
     const int64_t kCUs = 256;
-    const int64_t per_cu = std::max<int64_t>(1, (cpl == 1 ? 16 : 12) / waves);
-    int best = 1;
-    int64_t best_cost = INT64_MAX;
-    for (int r : kQ4KRowSet) {
-        const int64_t grid = (n + r - 1) / r;
-        const int64_t cost = (grid + kCUs - 1) / kCUs * r + 2 * ((grid + kCUs * per_cu - 1) / (kCUs * per_cu));
-        if (cost < best_cost || (cost == best_cost && r > best)) {
-            best = r;
-            best_cost = cost;
-        }
-    }
-    return best;
+    if (waves < 4) return n <= 8192 ? 4 : 7;
+    for (int r : kQ4KRowSet)
+        if ((n + r - 1) / r <= kCUs) return r;
+    return 16;
 }
 
 template <int CPL, int U, int R>
@@ -680,10 +677,8 @@ hipError_t launch_q4k(int cpl, int ring, int rows, int waves, int64_t grid, cons
         ok = ring == 3 ? q4k_rows<2, 3>(rows, gd, bd, s, w, x, y, n, nb) : q4k_rows<2, 5>(rows, gd, bd, s, w, x, y, n, nb);
     } else if (ring == 4) {
         ok = q4k_rows<1, 4>(rows, gd, bd, s, w, x, y, n, nb);
-    } else if (ring == 6) {
-        ok = q4k_rows<1, 6>(rows, gd, bd, s, w, x, y, n, nb);
     } else {
-        ok = q4k_rows<1, 8>(rows, gd, bd, s, w, x, y, n, nb);
+        ok = q4k_rows<1, 6>(rows, gd, bd, s, w, x, y, n, nb);
     }
     if (!ok) return hipErrorInvalidConfiguration;
     return hipGetLastError();
@@ -736,9 +731,9 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
     if (lanes > max_lanes(qtype, p.cpl)) return hipErrorInvalidConfiguration;
     p.waves = (int)((lanes + 63) / 64);
     if (qtype == kTypeQ4K) {
-        if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q4k(n, p.waves, p.cpl);
+        if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q4k(n, p.waves);
         if (!q4k_rows_ok(p.rows_per_wg)) return hipErrorInvalidConfiguration;
-        p.unroll = q4k_ring(p.cpl, p.unroll > 0 ? p.unroll : (p.cpl == 1 ? 6 : 5));
+        p.unroll = q4k_ring(p.cpl, p.unroll > 0 ? p.unroll : (p.cpl == 1 ? 4 : 3));
         p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
         if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
         if (plan) *plan = p;
