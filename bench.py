@@ -193,7 +193,49 @@ def run_suite(stream, steps: int) -> dict:
                      "eager_us_per_launch": round(te / min(steps, 200) * 1e6, 2), "effective_bytes": w.bytes}
         w.free()
     out["llama3_8b_decode_resident"] = decode_sweep_resident(stream, steps=max(3, min(steps // 50, 20)))
+    out["copy_ceiling"] = copy_ceiling(stream)
+    out["host_path_q4_k_3584x18944"] = host_path_rate()
     return out
+
+
+def copy_ceiling(stream, mib: int = 512, reps: int = 20) -> dict:
+    """The library's plain streaming copy (16 B per lane, read + write) over
+    `mib` MiB, replayed from a graph: the practical HBM ceiling to compare
+    the GEMV against."""
+    nbytes = mib << 20
+    src, dst = device.DeviceBuffer(nbytes), device.DeviceBuffer(nbytes)
+    with device.Graph.capture(stream) as cap:
+        for _ in range(reps):
+            device.copy(dst, src, nbytes, stream=stream)
+    cap.launch(stream)
+    device.synchronize()
+    e0, e1 = device.Event(), device.Event()
+    e0.record(stream)
+    cap.launch(stream)
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    cap.destroy()
+    src.free()
+    dst.free()
+    return {"bytes_moved": 2 * nbytes, "us": round(ms * 1e3, 2), "gbs": round(2 * nbytes / (ms / 1e3) / 1e9, 1)}
+
+
+def host_path_rate(reps: int = 20) -> dict:
+    """The reference-shaped host entry point (_C.matmul_q4_k: numpy in, numpy
+    out, weight and x copied host -> device on every call): PCIe-inclusive."""
+    from flatrun_amd import _C
+
+    q, n, k = "Q4_K", 3584, 18944
+    raw = synth.make_blocks(q, n, k, seed=7)
+    x = synth.make_x(k, seed=8)
+    _C.matmul_q4_k(x, raw, n, k)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        _C.matmul_q4_k(x, raw, n, k)
+    dt = (time.perf_counter() - t0) / reps
+    return {"ms_per_call": round(dt * 1e3, 3), "gbs": round(effective_bytes(q, n, k) / dt / 1e9, 2),
+            "note": "pageable host buffers; includes the H2D copy of the raw weight bytes every call"}
 
 
 def decode_sweep_resident(stream, steps: int, layers: int = 32) -> dict:
