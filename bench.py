@@ -43,6 +43,7 @@ sys.path.insert(0, str(ROOT))
 from flatrun_amd import _lib, device, synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, published
 ROTATE_BYTES = 1 << 30         # >= 1 GiB of distinct copies per workload
 
 
@@ -193,9 +194,40 @@ def run_suite(stream, steps: int) -> dict:
                      "eager_us_per_launch": round(te / min(steps, 200) * 1e6, 2), "effective_bytes": w.bytes}
         w.free()
     out["llama3_8b_decode_resident"] = decode_sweep_resident(stream, steps=max(3, min(steps // 50, 20)))
+    out["prefill_gemm_q4_k_bf16_512x14336x4096"] = prefill_gemm(stream)
     out["copy_ceiling"] = copy_ceiling(stream)
     out["host_path_q4_k_3584x18944"] = host_path_rate()
     return out
+
+
+def prefill_gemm(stream, m: int = 512, n: int = 14336, k: int = 4096, reps: int = 20) -> dict:
+    """Q4_K prefill GEMM on the matrix cores, Y[m, n] = X[m, k] (bf16) . W^T,
+    W rotated over 8 distinct copies (264 MB, beyond the Infinity Cache)."""
+    from flatrun_amd import _C
+
+    raw = synth.make_blocks("Q4_K", n, k, seed=31)
+    x = _C.to_bf16_bits(np.random.default_rng(32).standard_normal((m, k)).astype(np.float32))
+    ws = [device.DeviceBuffer.from_host(raw) for _ in range(8)]
+    xd, yd = device.DeviceBuffer.from_host(x), device.DeviceBuffer(4 * m * n)
+    with device.Graph.capture(stream) as cap:
+        for i in range(reps):
+            device.gemm_q4k_bf16(ws[i % len(ws)], xd, yd, m, n, k, stream=stream, w_bytes=raw.nbytes)
+    cap.launch(stream)
+    device.synchronize()
+    e0, e1 = device.Event(), device.Event()
+    e0.record(stream)
+    cap.launch(stream)
+    e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) / reps * 1e3
+    cap.destroy()
+    for b in ws:
+        b.free()
+    xd.free()
+    yd.free()
+    flop = 2 * m * n * k
+    return {"us": round(us, 2), "tflops": round(flop / us / 1e6, 1), "flop": flop,
+            "frac_bf16_peak": round(flop / us / 1e6 / BF16_PEAK_TFLOPS, 4), "peak_tflops": BF16_PEAK_TFLOPS}
 
 
 def copy_ceiling(stream, mib: int = 512, reps: int = 20) -> dict:

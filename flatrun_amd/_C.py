@@ -10,8 +10,9 @@ contiguous). Errors the reference raises as ``std::runtime_error`` arrive as
 
 Additions beyond the reference module, for the formats it lacks:
 ``dequant_q5_k``, ``dequant_q1_0``, ``matmul_q5_k``, ``matmul_q1_0`` and
-their ``_batched`` forms, plus ``dequant(qtype, weight, shape)`` with the NumPy
-decoders' ragged-size rule.
+their ``_batched`` forms, ``dequant(qtype, weight, shape)`` with the NumPy
+decoders' ragged-size rule, and ``matmul_q4_k_bf16`` (prefill GEMM on the
+matrix cores, bf16 inputs).
 """
 
 from __future__ import annotations
@@ -175,6 +176,40 @@ matmul_q5_k = _generic_1d(_lib.Q5_K, "Q5_K")
 matmul_q5_k_batched = _generic_2d(_lib.Q5_K, "Q5_K")
 matmul_q1_0 = _generic_1d(_lib.Q1_0, "Q1_0")
 matmul_q1_0_batched = _generic_2d(_lib.Q1_0, "Q1_0")
+
+
+# ------------------------------------------------------------------ prefill GEMM (matrix cores)
+
+def to_bf16_bits(a) -> np.ndarray:
+    """float32 -> bf16 bit patterns (uint16), round to nearest even; NaN stays
+    NaN (quiet). Input preparation for the bf16 GEMM, not arithmetic on W."""
+    f = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+    u = f.view(np.uint32)
+    r = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+    nan = np.isnan(f)
+    if nan.any():
+        r[nan] = ((u[nan] >> np.uint32(16)) | np.uint32(0x40)).astype(np.uint16)
+    return r
+
+
+def matmul_q4_k_bf16(x, weight, n, k):
+    """out[seq, n] = x[seq, k] . W^T on the matrix cores, x and W in bf16
+    (x given as float32 is rounded to bf16 first; a uint16 array is taken as
+    bf16 bits), fp32 accumulation. 1-D x gives out[n]. The fp32 per-token
+    path is matmul_q4_k_batched (_C.cpp:154-197)."""
+    xa = np.asarray(x)
+    xb = np.ascontiguousarray(xa) if xa.dtype == np.uint16 else to_bf16_bits(xa)
+    one_d = xb.ndim == 1
+    x2 = xb.reshape(1, -1) if one_d else xb
+    if x2.ndim != 2:
+        raise _lib.FrqError(_lib.ERR_SHAPE, "Q4_K gemm: x must be 1-D or 2-D")
+    n, k = _size_t(n, "n"), _size_t(k, "k")
+    if x2.shape[1] != k:
+        raise _lib.FrqError(_lib.ERR_SHAPE, "Q4_K gemm: x.shape[-1] != k")
+    w = _u8(weight)
+    out = np.empty((x2.shape[0], n), dtype=np.float32)
+    check(lib().frq_gemm_q4_k_bf16(ptr(x2), ptr(w), w.size, x2.shape[0], n, k, ptr(out)))
+    return out[0] if one_d else out
 
 
 # ------------------------------------------------------------------ diagnostics

@@ -179,6 +179,29 @@ class NativeBackend:
         """Fused Q1_0 dequant + matvec (no native counterpart in the reference)."""
         return self._matmul("Q1_0", x, weight, n, k)
 
+    def matmul_q4k_bf16(self, x, weight, n: int, k: int):
+        """Prefill GEMM on the matrix cores: x (seq, k) rounded to bf16, W
+        dequantized to bf16, fp32 accumulation -> (seq, n) float32. The fp32
+        per-token path (the reference's contract) is ``matmul_q4k``."""
+        self._require()
+        if not isinstance(weight, DeviceWeight):
+            return _C.matmul_q4_k_bf16(x, _raw_bytes(weight), n, k)
+        from . import device
+        xb = _C.to_bf16_bits(x)
+        x2 = xb.reshape(1, -1) if xb.ndim == 1 else xb
+        if x2.ndim != 2 or x2.shape[1] != k:
+            raise ValueError(f"x must be ({k},) or (seq, {k}), got {np.shape(x)}")
+        xd = device.DeviceBuffer.from_host(x2)
+        yd = device.DeviceBuffer(max(1, x2.shape[0] * n * 4))
+        try:
+            device.gemm_q4k_bf16(weight, xd, yd, x2.shape[0], n, k, w_bytes=weight.nbytes)
+            device.synchronize()
+            y = yd.to_host(np.float32)[: x2.shape[0] * n].reshape(x2.shape[0], n)
+        finally:
+            xd.free()
+            yd.free()
+        return y[0] if xb.ndim == 1 else y
+
     # ------------------------------------------------------------ dequant
     def dequant_q4k(self, weight, shape: tuple[int, int]):
         """Pure Q4_K dequant to f32 (out, in) (python/__init__.py:211-227)."""

@@ -13,6 +13,10 @@ Flags that matter:
                                        never flushes).
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                        no packed-fp32 VALU instructions.
+  -mllvm -disable-promote-alloca-to-lds
+                                       per-thread arrays stay in registers
+                                       (LLVM otherwise moves some into spare
+                                       LDS, adding LDS traffic).
 """
 
 from __future__ import annotations
@@ -51,6 +55,7 @@ def _flags() -> list[str]:
         "-ffp-contract=off",
         "-fno-gpu-flush-denormals-to-zero",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-mllvm", "-disable-promote-alloca-to-lds",
         "-Wno-unused-command-line-argument",
         f"-I{ROOT / 'include'}",
         f"-I{CSRC}",

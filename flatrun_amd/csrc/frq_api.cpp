@@ -432,6 +432,58 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     return FRQ_OK;
 }
 
+static int gemm_checks(const void* w, size_t w_bytes, int64_t m, int64_t n, int64_t k) {
+    if (m < 0 || n < 0 || k < 0) return fail(FRQ_ERR_SHAPE, "Q4_K gemm: negative shape");
+    if (k % 256) return fail(FRQ_ERR_SHAPE, "Q4_K gemm: in_features must be a multiple of 256");
+    if ((int64_t)w_bytes != n * (k / 256) * 144) return fail(FRQ_ERR_SIZE, "Q4_K gemm: weight byte size mismatch");
+    if (m > 0 && n > 0 && k > 0 && !frq::gemm_q4_k_bf16_supported(m, n, k))
+        return fail(FRQ_ERR_UNSUPPORTED, "Q4_K gemm: shape beyond this build's limits");
+    (void)w;
+    return FRQ_OK;
+}
+
+int frq_dev_gemm_q4_k_bf16(const void* w, size_t w_bytes, const uint16_t* x, float* y, int64_t m, int64_t n,
+                           int64_t k, void* stream) {
+    if (int rc = gemm_checks(w, w_bytes, m, n, k)) return rc;
+    if (m == 0 || n == 0) return FRQ_OK;
+    if (!y) return fail(FRQ_ERR_INVALID, "null buffer");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (k == 0) {
+        FRQ_HIP(frq::launch_fill(y, 0.0f, m * n, s));
+        return FRQ_OK;
+    }
+    if (!w || !x) return fail(FRQ_ERR_INVALID, "null buffer");
+    if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15) != 0)
+        return fail(FRQ_ERR_ALIGN, "weight and x must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(y) & 3) return fail(FRQ_ERR_ALIGN, "y must be 4-byte aligned");
+    FRQ_HIP(frq::launch_gemm_q4_k_bf16(static_cast<const uint8_t*>(w), x, y, m, n, k, s));
+    return FRQ_OK;
+}
+
+int frq_gemm_q4_k_bf16(const uint16_t* x, const uint8_t* w, size_t w_bytes, int64_t m, int64_t n, int64_t k,
+                       float* y) {
+    if (int rc = gemm_checks(w, w_bytes, m, n, k)) return rc;
+    if (m == 0 || n == 0) return FRQ_OK;
+    if (!y || (k > 0 && (!x || !w))) return fail(FRQ_ERR_INVALID, "null buffer");
+    if (k == 0) {
+        std::memset(y, 0, (size_t)(m * n) * sizeof(float));
+        return FRQ_OK;
+    }
+    if (int rc = have_device()) return rc;
+    std::lock_guard<std::mutex> lk(g_ws.mu);
+    const size_t wb = align256(w_bytes), xb = align256((size_t)(m * k) * 2), yb = align256((size_t)(m * n) * 4);
+    void* base = nullptr;
+    if (int rc = workspace(wb + xb + yb, &base)) return rc;
+    uint8_t* dw = static_cast<uint8_t*>(base);
+    uint16_t* dx = reinterpret_cast<uint16_t*>(dw + wb);
+    float* dy = reinterpret_cast<float*>(dw + wb + xb);
+    FRQ_HIP(hipMemcpy(dw, w, w_bytes, hipMemcpyHostToDevice));
+    FRQ_HIP(hipMemcpy(dx, x, (size_t)(m * k) * 2, hipMemcpyHostToDevice));
+    FRQ_HIP(frq::launch_gemm_q4_k_bf16(dw, dx, dy, m, n, k, nullptr));
+    FRQ_HIP(hipMemcpy(y, dy, (size_t)(m * n) * 4, hipMemcpyDeviceToHost));
+    return FRQ_OK;
+}
+
 int frq_dev_copy(void* dst, const void* src, size_t bytes, void* stream) {
     if (bytes % 16) return fail(FRQ_ERR_INVALID, "copy size must be a multiple of 16 bytes");
     if (((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15) != 0)

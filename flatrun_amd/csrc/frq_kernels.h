@@ -63,4 +63,11 @@ void gemv_sk_scratch(const SplitKPlan& plan, int64_t n, size_t* partial_bytes, s
 hipError_t launch_gemv_sk(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k,
                           const SplitKPlan& plan, float* partials, uint32_t* counters, hipStream_t stream);
 
+// Q4_K prefill GEMM on the matrix cores (frq_gemm.hip): y[m, n] = x[m, k] (bf16
+// bits, row-major) . W[n, k]^T (raw Q4_K blocks) with W rounded to bf16 and
+// fp32 accumulation. w and x 16-byte aligned, k a multiple of 256.
+bool gemm_q4_k_bf16_supported(int64_t m, int64_t n, int64_t k);
+hipError_t launch_gemm_q4_k_bf16(const uint8_t* w, const uint16_t* x, float* y, int64_t m, int64_t n, int64_t k,
+                                 hipStream_t stream);
+
 }  // namespace frq

@@ -265,6 +265,14 @@ def gemv_tuned(qtype, w, x, y, n: int, k: int, kernel: int = 0, cpl: int = 0, ro
     return cfg.as_dict()
 
 
+def gemm_q4k_bf16(w, x_bf16, y, m: int, n: int, k: int, stream=None, w_bytes: int | None = None) -> None:
+    """y[m, n] = x[m, k] . W[n, k]^T on the matrix cores (x: bf16 bits, row-major;
+    y: fp32). Enqueued, not synchronised."""
+    wb = _nbytes(w) if w_bytes is None else int(w_bytes)
+    check(lib().frq_dev_gemm_q4_k_bf16(_addr(w), wb, _addr(x_bf16), _addr(y), int(m), int(n), int(k),
+                                       _stream(stream)))
+
+
 def copy(dst, src, nbytes: int, stream=None) -> None:
     """dst[:nbytes] = src[:nbytes] with the library's streaming copy kernel (enqueued)."""
     check(lib().frq_dev_copy(_addr(dst), _addr(src), int(nbytes), _stream(stream)))

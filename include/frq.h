@@ -151,6 +151,19 @@ typedef struct {
 int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
                        frq_gemv_config* cfg, void* stream);
 
+/* Q4_K prefill GEMM on the matrix cores: y[m, n] = x[m, k] . W[n, k]^T, where
+ * x holds bf16 bit patterns (row-major), W is raw Q4_K blocks (n rows of k/256
+ * blocks) and y is fp32 row-major. W values are the exact fp32 dequant rounded
+ * to bf16 (nearest even); products and sums are fp32. Replaces, for
+ * activations already in bf16, the per-token loop of matmul_q4_k_batched
+ * (_C.cpp:154-197), which re-dequantizes W for every row of x. Device
+ * pointers (w, x 16-byte aligned); k a multiple of 256. */
+int frq_dev_gemm_q4_k_bf16(const void* w, size_t w_bytes, const uint16_t* x_bf16, float* y, int64_t m, int64_t n,
+                           int64_t k, void* stream);
+/* Same with host buffers (copied to the device and back on every call). */
+int frq_gemm_q4_k_bf16(const uint16_t* x_bf16, const uint8_t* w, size_t w_bytes, int64_t m, int64_t n, int64_t k,
+                       float* y);
+
 /* dst = src on the device with a plain 16-byte-per-lane streaming kernel:
  * the reference point for calibrating HBM traffic counters (bytes a
  * multiple of 16, both pointers 16-byte aligned). No reference counterpart. */

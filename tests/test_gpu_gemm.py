@@ -1,0 +1,91 @@
+"""Q4_K prefill GEMM on the matrix cores (bf16 MFMA) against the oracle.
+
+Contract (written here, checked below):
+  * against fp64 X . bf16(W)^T, with W the exact fp32 dequant (oracle) rounded
+    to bf16 nearest-even: within MATVEC_RTOL (1e-5) normwise and
+    componentwise -- the kernel adds only fp32 accumulation error;
+  * against fp64 X . W^T with the exact fp32 W: normwise within
+    BF16_W_RTOL = 1e-2 -- the bf16 rounding of W (2^-9 relative per weight)
+    is the only intended loss.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_matvec_close, bits_equal
+from flatrun_amd import NativeBackend, _C, _lib, synth
+from oracle import gguf_np as G
+
+pytestmark = pytest.mark.gpu
+
+BF16_W_RTOL = 1e-2
+
+
+def bf16_round(a: np.ndarray) -> np.ndarray:
+    """float32 -> nearest-even bf16 -> float32 (numpy, for the reference side)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32)
+    r = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    return r.view(np.float32)
+
+
+def make_case(m, n, k, seed):
+    raw = synth.make_blocks("Q4_K", n, k, seed=seed)
+    x = np.random.default_rng(seed + 1).standard_normal((m, k)).astype(np.float32)
+    return raw, bf16_round(x)
+
+
+def check(y, raw, xb, n, k):
+    w = G.dequant_q4_k(raw, (n, k)).astype(np.float32)
+    wb = bf16_round(w).astype(np.float64)
+    x64 = xb.astype(np.float64)
+    ref = x64 @ wb.T
+    absw = np.abs(x64) @ np.abs(wb).T
+    assert_matvec_close(y.reshape(-1), ref.reshape(-1), absw.reshape(-1), what=f"gemm {xb.shape[0]}x{n}x{k} vs bf16(W)")
+    exact = x64 @ w.astype(np.float64).T
+    err = np.max(np.abs(y - exact)) / np.max(np.abs(exact))
+    assert err <= BF16_W_RTOL, f"gemm vs exact W: normwise {err:.3e} > {BF16_W_RTOL}"
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 256), (5, 37, 512), (256, 128, 256), (300, 200, 1024), (513, 130, 768),
+                                   (64, 1000, 4096)])
+def test_gemm_shapes(frq, m, n, k):
+    raw, xb = make_case(m, n, k, seed=m + n + k)
+    y = _C.matmul_q4_k_bf16(xb, raw, n, k)
+    assert y.shape == (m, n) and y.dtype == np.float32
+    check(y, raw, xb, n, k)
+
+
+def test_gemm_prefill_config(frq):
+    """The prefill workload itself: Y[512 x 14336] = X[512 x 4096] . W^T."""
+    m, n, k = 512, 14336, 4096
+    raw, xb = make_case(m, n, k, seed=11)
+    check(_C.matmul_q4_k_bf16(xb, raw, n, k), raw, xb, n, k)
+
+
+def test_gemm_bf16_bits_input_and_1d(frq):
+    m, n, k = 3, 70, 512
+    raw, xb = make_case(m, n, k, seed=4)
+    y = _C.matmul_q4_k_bf16(xb, raw, n, k)
+    assert bits_equal(_C.matmul_q4_k_bf16(_C.to_bf16_bits(xb), raw, n, k), y)
+    assert bits_equal(_C.matmul_q4_k_bf16(xb[1], raw, n, k), y[1])
+
+
+def test_gemm_resident_weight_matches_host_path(frq):
+    m, n, k = 40, 300, 1024
+    raw, xb = make_case(m, n, k, seed=9)
+    nb = NativeBackend()
+    dw = nb.upload(raw)
+    assert bits_equal(nb.matmul_q4k_bf16(xb, dw, n, k), nb.matmul_q4k_bf16(xb, raw, n, k))
+
+
+def test_gemm_edges_and_errors(frq):
+    assert _C.matmul_q4_k_bf16(np.zeros((0, 256), np.float32), np.zeros(144 * 3, np.uint8), 3, 256).shape == (0, 3)
+    assert np.array_equal(_C.matmul_q4_k_bf16(np.zeros((2, 0), np.float32), np.zeros(0, np.uint8), 4, 0),
+                          np.zeros((2, 4), np.float32))
+    with pytest.raises(RuntimeError):
+        _C.matmul_q4_k_bf16(np.zeros((2, 300), np.float32), np.zeros(144, np.uint8), 1, 300)
+    with pytest.raises(RuntimeError):
+        _C.matmul_q4_k_bf16(np.zeros((2, 256), np.float32), np.zeros(100, np.uint8), 1, 256)
+    assert _lib.lib().frq_dev_gemm_q4_k_bf16(None, 144, None, None, 1, 1, 256, None) != 0
