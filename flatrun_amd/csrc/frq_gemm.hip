@@ -11,15 +11,16 @@
 // X is taken as given in bf16; products and sums are fp32. The result equals
 // fp64 X . bf16(W)^T to fp32 accumulation error.
 //
-// Tiling: a workgroup (4 waves) owns a 256 (M) x 128 (N) tile of Y and walks K
-// in steps of 64 (one Q4_K group: 32 qs bytes per row). Wave (wm, wn) owns the
-// 128 x 64 sub-tile at (128 wm, 64 wn): 4 x 2 MFMA tiles of 32 x 32, 128 fp32
-// accumulators per lane. Each K-step:
+// Tiling: a workgroup (8 waves, two per SIMD) owns a 256 (M) x 128 (N) tile of
+// Y and walks K in steps of 64 (one Q4_K group: 32 qs bytes per row). Wave
+// (wm, wn) owns the 64 x 64 sub-tile at (64 wm, 64 wn): 2 x 2 MFMA tiles of
+// 32 x 32, 64 fp32 accumulators per lane; while one wave of a SIMD dequantizes
+// or waits on LDS the other issues MFMAs. Each K-step:
 //   * X tile [256][64] bf16 and the W tile [128][64] (dequantized by the
-//     workgroup, one half-group of 16 qs bytes per thread) go to LDS, double
-//     buffered; the global loads of step t+1 are issued before the MFMAs of
-//     step t and written to the other buffer after them, so the dequant
-//     arithmetic runs while the matrix cores work.
+//     workgroup, a quarter group of 8 qs bytes per thread) go to LDS, double
+//     buffered; global loads run two steps ahead (two register staging
+//     sets), and each step's dequant + LDS writes for step t+1 follow its
+//     MFMAs, so the arithmetic runs while the matrix cores work.
 //   * LDS rows are padded to 72 bf16 (144 B) so a fragment read by 32 lanes
 //     of consecutive rows spreads over the banks.
 // MFMA operand layouts (32x32x16, 8 bf16 per lane): A lane l holds row l%32,
@@ -38,6 +39,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // Native vector, not HIP's uint4 class: values of the class type held across
 // the K loop's barrier stay in scratch memory; native vectors go to registers.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBM = 256, kBN = 128, kBK = 64;
 constexpr int kLds = kBK + 8;   // bf16 per LDS row
@@ -47,68 +49,74 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
-__global__ void __launch_bounds__(256) gemm_q4_k_bf16_kernel(const uint8_t* __restrict__ w,
+__global__ void __launch_bounds__(512) gemm_q4_k_bf16_kernel(const uint8_t* __restrict__ w,
                                                              const uint16_t* __restrict__ x,
                                                              float* __restrict__ y, int M, int N, int K) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[2][kBM * kLds];
     __shared__ __attribute__((aligned(16))) uint16_t ws[2][kBN * kLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
-    const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM;
+    const int wm = wave & 3, wn = wave >> 2;
+    // 1-D grid, M-tile fastest: workgroups are dealt to the 8 XCDs round-robin,
+    // so with 2 (or 4, 8) M-tiles each XCD only ever needs its own M-tile of X
+    // (2 MB at M-tile 256, K 4096), which then stays in that XCD's L2.
+    const int mtiles = (M + kBM - 1) / kBM;
+    const int n0 = (int)(blockIdx.x / mtiles) * kBN, m0 = (int)(blockIdx.x % mtiles) * kBM;
     const int64_t row_bytes = (int64_t)(K / kQKElems) * kQ4KBytes;
     const int ksteps = K / kBK;
 
-    // X staging: 8 threads per row (16 B each), rows xr + 32 j.
+    // X staging: 8 threads per row (16 B each), rows xr + 64 j.
     const int xc = tid & 7, xr = tid >> 3;
-    // W staging: thread owns half wh of the group's 32 qs bytes of W row wr.
-    const int wr = tid >> 1, wh = tid & 1;
+    // W staging: thread owns quarter wq (8 bytes) of the group's 32 qs bytes of W row wr.
+    const int wr = tid >> 2, wq = tid & 3;
     const uint8_t* wrow = w + (int64_t)(n0 + wr < N ? n0 + wr : N - 1) * row_bytes;
 
-    u32x4 xreg[8];
-    u32x4 hreg, qreg;
-    auto load_tile = [&](int kt) __attribute__((always_inline)) {
+    struct Stage {
+        u32x4 x[4];
+        u32x4 h;
+        u32x2 q;
+    };
+    Stage st[2];
+    auto load_tile = [&](Stage& sg, int kt) __attribute__((always_inline)) {
         const int kb = kt * kBK;
-        static_for<0, 8>([&](auto jc) {
+        static_for<0, 4>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
-            const int r = m0 + xr + 32 * j;
-            xreg[j] = *reinterpret_cast<const u32x4*>(x + (int64_t)(r < M ? r : M - 1) * K + kb + 8 * xc);
+            const int r = m0 + xr + 64 * j;
+            sg.x[j] = *reinterpret_cast<const u32x4*>(x + (int64_t)(r < M ? r : M - 1) * K + kb + 8 * xc);
         });
         const uint8_t* bp = wrow + (int64_t)(kb >> 8) * kQ4KBytes;
-        hreg = *reinterpret_cast<const u32x4*>(bp);
-        qreg = *reinterpret_cast<const u32x4*>(bp + 16 + 32 * ((kb >> 6) & 3) + 16 * wh);
+        sg.h = *reinterpret_cast<const u32x4*>(bp);
+        sg.q = *reinterpret_cast<const u32x2*>(bp + 16 + 32 * ((kb >> 6) & 3) + 8 * wq);
     };
-    auto store_tile = [&](int buf, int kt) __attribute__((always_inline)) {
-        static_for<0, 8>([&](auto jc) {
+    auto store_tile = [&](const Stage& sg, int buf, int kt) __attribute__((always_inline)) {
+        static_for<0, 4>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
-            *reinterpret_cast<u32x4*>(&xs[buf][(xr + 32 * j) * kLds + 8 * xc]) = xreg[j];
+            *reinterpret_cast<u32x4*>(&xs[buf][(xr + 64 * j) * kLds + 8 * xc]) = sg.x[j];
         });
         const int g = ((kt * kBK) >> 6) & 3;
         uint32_t sc0, mn0, sc1, mn1;
-        k4_scale_min(hreg[1], hreg[2], hreg[3], 2 * g, sc0, mn0);
-        k4_scale_min(hreg[1], hreg[2], hreg[3], 2 * g + 1, sc1, mn1);
-        const float d = f16_bits_to_f32(hreg[0]), dmin = f16_bits_to_f32(hreg[0] >> 16);
+        k4_scale_min(sg.h[1], sg.h[2], sg.h[3], 2 * g, sc0, mn0);
+        k4_scale_min(sg.h[1], sg.h[2], sg.h[3], 2 * g + 1, sc1, mn1);
+        const float d = f16_bits_to_f32(sg.h[0]), dmin = f16_bits_to_f32(sg.h[0] >> 16);
         const float s0 = d * (float)sc0, t0 = dmin * (float)mn0;
         const float s1 = d * (float)sc1, t1 = dmin * (float)mn1;
-        const uint32_t qw[4] = {qreg[0], qreg[1], qreg[2], qreg[3]};
-        uint32_t lo[8], hi[8];
+        const uint32_t qw[2] = {sg.q[0], sg.q[1]};
+        uint32_t lo[4], hi[4];
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            const uint32_t v = qw[p >> 1] >> (16 * (p & 1));   // bytes 2p, 2p+1 of the half
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t v = qw[p >> 1] >> (16 * (p & 1));   // bytes 2p, 2p+1 of the quarter
             // same arithmetic as the dequant kernels: fl(fl(s * q) - t)
             lo[p] = pack_bf16(s0 * (float)(v & 15u) - t0, s0 * (float)((v >> 8) & 15u) - t0);
             hi[p] = pack_bf16(s1 * (float)((v >> 4) & 15u) - t1, s1 * (float)((v >> 12) & 15u) - t1);
         }
-        // low nibbles -> k 16 wh + i (sub-block 2g), high -> 32 + 16 wh + i (2g + 1)
+        // low nibbles -> k 8 wq + i (sub-block 2g), high -> 32 + 8 wq + i (2g + 1)
         uint16_t* dst = &ws[buf][wr * kLds];
-        *reinterpret_cast<u32x4*>(dst + 16 * wh) = u32x4{lo[0], lo[1], lo[2], lo[3]};
-        *reinterpret_cast<u32x4*>(dst + 16 * wh + 8) = u32x4{lo[4], lo[5], lo[6], lo[7]};
-        *reinterpret_cast<u32x4*>(dst + 32 + 16 * wh) = u32x4{hi[0], hi[1], hi[2], hi[3]};
-        *reinterpret_cast<u32x4*>(dst + 32 + 16 * wh + 8) = u32x4{hi[4], hi[5], hi[6], hi[7]};
+        *reinterpret_cast<u32x4*>(dst + 8 * wq) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<u32x4*>(dst + 32 + 8 * wq) = u32x4{hi[0], hi[1], hi[2], hi[3]};
     };
 
-    f32x16 acc[4][2];
+    f32x16 acc[2][2];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
@@ -118,41 +126,52 @@ __global__ void __launch_bounds__(256) gemm_q4_k_bf16_kernel(const uint8_t* __re
 #pragma unroll
         for (int kk = 0; kk < kBK / 16; ++kk) {
             const int kof = 16 * kk + 8 * (lane >> 5);
-            bf16x8 a[4], b[2];
+            bf16x8 a[2], b[2];
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-                a[mi] = *reinterpret_cast<const bf16x8*>(&xs[buf][(128 * wm + 32 * mi + (lane & 31)) * kLds + kof]);
+            for (int mi = 0; mi < 2; ++mi)
+                a[mi] = *reinterpret_cast<const bf16x8*>(&xs[buf][(64 * wm + 32 * mi + (lane & 31)) * kLds + kof]);
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni)
                 b[ni] = *reinterpret_cast<const bf16x8*>(&ws[buf][(64 * wn + 32 * ni + (lane & 31)) * kLds + kof]);
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
+            for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni)
                     acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
         }
     };
 
-    load_tile(0);
-    store_tile(0, 0);
+    // Global loads run two K-steps ahead of the MFMAs: the loads for step
+    // t + 2 are issued at step t (staging set t % 2) and reach LDS at the end
+    // of step t + 1. The loop is unrolled by two (the step count K/64 is a
+    // multiple of 4) so the staging set of every step is a compile-time
+    // choice, and loads and LDS writes are unconditional -- past the last
+    // step they repeat it into the buffer nothing reads again -- so the
+    // compiler's wait before each LDS write covers one staging set only.
+    const int last = ksteps - 1;
+    load_tile(st[0], 0);
+    load_tile(st[1], 1 < last ? 1 : last);
+    store_tile(st[0], 0, 0);
     __syncthreads();
-    for (int kt = 0; kt < ksteps; ++kt) {
-        const int buf = kt & 1;
-        const bool more = kt + 1 < ksteps;
-        if (more) load_tile(kt + 1);
-        compute(buf);
-        if (more) store_tile(buf ^ 1, kt + 1);
-        __syncthreads();
+    for (int kt0 = 0; kt0 < ksteps; kt0 += 2) {
+        static_for<0, 2>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;      // kt % 2: LDS buffer and staging set
+            const int kt = kt0 + j;
+            load_tile(st[j], kt + 2 < last ? kt + 2 : last);
+            compute(j);
+            store_tile(st[j ^ 1], j ^ 1, kt + 1 < last ? kt + 1 : last);
+            __syncthreads();
+        });
     }
 
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {
             const int n = n0 + 64 * wn + 32 * ni + (lane & 31);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + 128 * wm + 32 * mi + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int m = m0 + 64 * wm + 32 * mi + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < M && n < N) y[(int64_t)m * N + n] = acc[mi][ni][r];
             }
         }
@@ -162,14 +181,14 @@ __global__ void __launch_bounds__(256) gemm_q4_k_bf16_kernel(const uint8_t* __re
 
 bool gemm_q4_k_bf16_supported(int64_t m, int64_t n, int64_t k) {
     return m > 0 && n > 0 && k > 0 && k % kQKElems == 0 && m <= 0x7FFFFFFF && n <= 0x7FFFFFFF &&
-           k <= 0x7FFFFFFF && (n + kBN - 1) / kBN <= 0x7FFFFFFF && (m + kBM - 1) / kBM <= 65535;
+           k <= 0x7FFFFFFF && ((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM) <= 0x7FFFFFFF;
 }
 
 hipError_t launch_gemm_q4_k_bf16(const uint8_t* w, const uint16_t* x, float* y, int64_t m, int64_t n, int64_t k,
                                  hipStream_t stream) {
     if (!gemm_q4_k_bf16_supported(m, n, k)) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((n + kBN - 1) / kBN), (unsigned)((m + kBM - 1) / kBM));
-    gemm_q4_k_bf16_kernel<<<grid, dim3(256), 0, stream>>>(w, x, y, (int)m, (int)n, (int)k);
+    const dim3 grid((unsigned)(((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM)));
+    gemm_q4_k_bf16_kernel<<<grid, dim3(512), 0, stream>>>(w, x, y, (int)m, (int)n, (int)k);
     return hipGetLastError();
 }
 
