@@ -273,6 +273,12 @@ def gemm_q4k_bf16(w, x_bf16, y, m: int, n: int, k: int, stream=None, w_bytes: in
                                        _stream(stream)))
 
 
+def memcpy_h2d_async(dst, src_host_ptr: int, nbytes: int, stream=None) -> None:
+    """Enqueues a host -> device copy (the host memory should be pinned for it
+    to run asynchronously)."""
+    check(lib().frq_memcpy_h2d_async(_addr(dst), int(src_host_ptr), int(nbytes), _stream(stream)))
+
+
 def copy(dst, src, nbytes: int, stream=None) -> None:
     """dst[:nbytes] = src[:nbytes] with the library's streaming copy kernel (enqueued)."""
     check(lib().frq_dev_copy(_addr(dst), _addr(src), int(nbytes), _stream(stream)))
