@@ -382,6 +382,148 @@ __global__ void __launch_bounds__(512) gemv_q6_k_kernel(const uint8_t* __restric
     finish_rows(row0, row_end, y, red, nwaves);
 }
 
+// Q6_K, register-ring variant (used when the weight base is 4-byte aligned
+// and a row has an even number of blocks: every block then starts at 0 or
+// 2 mod 4, alternating). Work unit as CPL=2 above: half h of a block and 8
+// consecutive l (l0 = 8p), 32 elements. Each 8-byte field (ql, ql+32, qh,
+// scales) is read as the three aligned dwords around it: even blocks read
+// [f, f+12) -- at most 2 bytes into the next block, which exists because the
+// row's block count is even -- and odd blocks [f-2, f+10), whose first 2
+// bytes are the previous block's; v_alignbit by 0 or 16 bits then extracts
+// the field, so every lane runs the same loads (no divergent alignment
+// branch, no 16-bit load pairs). Rows stream through a ring of U register
+// slots, the row loop is unrolled over R rows without guards (as in the Q4_K
+// ring kernel), and partials are reduced with DPP into LDS.
+struct Q6Row {
+    uint32_t ql0[3], ql1[3], qh[3], sc[3];
+    uint32_t d;
+};
+
+__device__ __forceinline__ void load_win3(const uint8_t* p, uint32_t (&wv)[3]) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+    wv[0] = q[0];
+    wv[1] = q[1];
+    wv[2] = q[2];
+}
+
+// Four 6-bit quants of one dword as floats: (src & 0x0F0F0F0F) | (hsh & 0x30303030),
+// one v_cvt_f32_ubyteN each, grouped so the FMAs that follow do not stall.
+__device__ __forceinline__ void q6_quad(uint32_t src, uint32_t hsh, float (&f)[4]) {
+    uint32_t t, q;
+    asm("v_and_b32 %0, %6, %7\n\t"
+        "v_and_or_b32 %1, %8, %9, %0\n\t"
+        "v_cvt_f32_ubyte0 %2, %1\n\t"
+        "v_cvt_f32_ubyte1 %3, %1\n\t"
+        "v_cvt_f32_ubyte2 %4, %1\n\t"
+        "v_cvt_f32_ubyte3 %5, %1"
+        : "=&v"(t), "=&v"(q), "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3])
+        : "s"(0x30303030u), "v"(hsh), "v"(src), "s"(0x0F0F0F0Fu));
+}
+
+template <int U, int R>
+__global__ void __launch_bounds__(1024) gemv_q6_k_ring_kernel(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ y, int64_t n, int nb) {
+    static_assert(U <= R, "ring deeper than the row count");
+    __shared__ float red[R * 16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const int blk_raw = tid >> 3, sub = tid & 7;
+    const bool active = blk_raw < nb;
+    const int blk = active ? blk_raw : 0;
+    const int h = sub >> 2, l0 = 8 * (sub & 3);
+    const int mis = (blk & 1) ? 2 : 0;              // block start mod 4
+    const uint32_t sh = 8u * (uint32_t)mis;
+    const int s = (sub & 3) >> 1;                  // l0 / 16
+
+    const int64_t row0 = (int64_t)blockIdx.x * R;
+    const int nrows = (int)(n - row0 < R ? n - row0 : R);
+    const int64_t row_bytes = (int64_t)nb * kQ6KBytes;
+    const uint32_t boff = (uint32_t)(blk * kQ6KBytes);
+    const uint32_t o_ql0 = boff + 64 * h + l0 - mis, o_ql1 = o_ql0 + 32;
+    const uint32_t o_qh = boff + 128 + 32 * h + l0 - mis, o_sc = boff + 192 + 8 * h - mis, o_d = boff + 208;
+
+    auto load1 = [&](Q6Row& t, int j) {
+        const uint8_t* rp = w + (row0 + (j < nrows ? j : nrows - 1)) * row_bytes;
+        load_win3(rp + o_ql0, t.ql0);
+        load_win3(rp + o_ql1, t.ql1);
+        load_win3(rp + o_qh, t.qh);
+        load_win3(rp + o_sc, t.sc);
+        t.d = ld_u16(rp + o_d);
+    };
+
+    float xv[4][8];
+    float xs[4];
+    {
+        const float* xb = x + (int64_t)blk * kQKElems + 128 * h + l0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 a = *reinterpret_cast<const float4*>(xb + 32 * k);
+            const float4 c = *reinterpret_cast<const float4*>(xb + 32 * k + 4);
+            xv[k][0] = a.x; xv[k][1] = a.y; xv[k][2] = a.z; xv[k][3] = a.w;
+            xv[k][4] = c.x; xv[k][5] = c.y; xv[k][6] = c.z; xv[k][7] = c.w;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Q6Row ring[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) load1(ring[i], i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        xs[k] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xs[k] += xv[k][i];
+    }
+
+    static_for<0, R>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        Q6Row& t = ring[j % U];
+        uint32_t ql0[2], ql1[2], qh[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            ql0[c] = __builtin_amdgcn_alignbit(t.ql0[c + 1], t.ql0[c], sh);
+            ql1[c] = __builtin_amdgcn_alignbit(t.ql1[c + 1], t.ql1[c], sh);
+            qh[c] = __builtin_amdgcn_alignbit(t.qh[c + 1], t.qh[c], sh);
+        }
+        const uint32_t sc0 = __builtin_amdgcn_alignbit(t.sc[1], t.sc[0], sh);   // scale bytes 8h .. 8h+3
+        const uint32_t sc1 = __builtin_amdgcn_alignbit(t.sc[2], t.sc[1], sh);   // 8h+4 .. 8h+7
+        const float d = f16_bits_to_f32(t.d);
+        // int8 scales sc[8h + s + 2k]: bytes s, s+2 of sc0 (k = 0, 1) and of sc1 (k = 2, 3)
+        const float sk[4] = {(float)(int8_t)(sc0 >> (8 * s)), (float)(int8_t)(sc0 >> (8 * s + 16)),
+                             (float)(int8_t)(sc1 >> (8 * s)), (float)(int8_t)(sc1 >> (8 * s + 16))};
+        float pu = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const uint32_t src = (k & 1) ? ql1[c] : ql0[c];
+                // bits 2k, 2k+1 of each qh byte -> bits 4, 5
+                const uint32_t hsh = (k == 0) ? (qh[c] << 4) : (k == 1) ? (qh[c] << 2) : (k == 2) ? qh[c] : (qh[c] >> 2);
+                float f[4];
+                q6_quad((k >= 2) ? (src >> 4) : src, hsh, f);
+                a0 = __builtin_fmaf(f[0], xv[k][4 * c + 0], a0);
+                a1 = __builtin_fmaf(f[1], xv[k][4 * c + 1], a1);
+                a0 = __builtin_fmaf(f[2], xv[k][4 * c + 2], a0);
+                a1 = __builtin_fmaf(f[3], xv[k][4 * c + 3], a1);
+            }
+            // sum_l (q - 32) x = sum_l q x - 32 sum_l x
+            const float dotk = __builtin_fmaf(-32.0f, xs[k], a0 + a1);
+            pu = __builtin_fmaf(d * sk[k], dotk, pu);
+        }
+        if constexpr (j + U < R) load1(t, j + U);
+        __builtin_amdgcn_sched_barrier(0);                  // keep the rows in ring order
+        const float v = wave_sum_lane63(active ? pu : 0.0f);
+        if (lane == 63) red[j * nwaves + wave] = v;
+    });
+    __syncthreads();
+    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+        float acc = 0.0f;
+        for (int w2 = 0; w2 < nwaves; ++w2) acc += red[r * nwaves + w2];
+        y[row0 + r] = acc;
+    }
+}
+
 // ------------------------------------------------------------------ Q8_0
 // Work unit: 8*CPL consecutive int8 of one 34-byte block (32/(8*CPL) lanes
 // per block); y = sum_b d_b * sum_i q_i x_i.
@@ -684,6 +826,53 @@ hipError_t launch_q4k(int cpl, int ring, int rows, int waves, int64_t grid, cons
     return hipGetLastError();
 }
 
+// Q6_K ring kernel: work unit 8 in GemvPlan::cpl (8 lanes per block); needs a
+// 4-byte aligned weight base and an even block count per row (see the kernel).
+constexpr int kQ6KRingUnit = 8;
+
+bool q6k_ring_ok(const uint8_t* w, int64_t nb) {
+    return (reinterpret_cast<uintptr_t>(w) & 3) == 0 && nb % 2 == 0 && nb * 8 <= 1024;
+}
+
+// Rows per Q6_K ring workgroup (measured on MI355X): as for Q4_K when a
+// workgroup has 4 or more waves; smaller workgroups take the most rows that
+// still leave >= 1024 workgroups (lm_head 152064 rows: 16; 4096: 4; 1024: 1).
+int pick_rows_q6k(int64_t n, int waves) {
+    if (waves >= 4) return pick_rows_q4k(n, waves);
+    int best = 1;
+    for (int r : kQ4KRowSet)
+        if (n / r >= 1024) best = r;
+    return best;
+}
+
+template <int U, int R>
+void q6k_go(dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n, int nb) {
+    gemv_q6_k_ring_kernel<(U < R ? U : R), R><<<gd, bd, 0, s>>>(w, x, y, n, nb);
+}
+
+template <int U>
+bool q6k_rows(int rows, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n,
+              int nb) {
+    switch (rows) {
+        case 1: q6k_go<U, 1>(gd, bd, s, w, x, y, n, nb); return true;
+        case 2: q6k_go<U, 2>(gd, bd, s, w, x, y, n, nb); return true;
+        case 4: q6k_go<U, 4>(gd, bd, s, w, x, y, n, nb); return true;
+        case 7: q6k_go<U, 7>(gd, bd, s, w, x, y, n, nb); return true;
+        case 8: q6k_go<U, 8>(gd, bd, s, w, x, y, n, nb); return true;
+        case 14: q6k_go<U, 14>(gd, bd, s, w, x, y, n, nb); return true;
+        case 16: q6k_go<U, 16>(gd, bd, s, w, x, y, n, nb); return true;
+        default: return false;
+    }
+}
+
+hipError_t launch_q6k_ring(int ring, int rows, int waves, int64_t grid, const uint8_t* w, const float* x, float* y,
+                           int64_t n, int nb, hipStream_t s) {
+    const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
+    (void)ring;
+    if (!q6k_rows<4>(rows, gd, bd, s, w, x, y, n, nb)) return hipErrorInvalidConfiguration;
+    return hipGetLastError();
+}
+
 template <int U>
 hipError_t launch_u(int qtype, int cpl, const uint8_t* w, const float* x, float* y, int64_t n, int nb,
                     int rows, int waves, int64_t grid, hipStream_t s) {
@@ -725,6 +914,18 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
     if (n <= 0) return hipSuccess;
     const int64_t nb = k / f.belems;
     GemvPlan p = plan ? *plan : GemvPlan{};
+    if (qtype == kTypeQ6K && (p.cpl <= 0 || p.cpl == kQ6KRingUnit) && q6k_ring_ok(w, nb)) {
+        p.cpl = kQ6KRingUnit;
+        p.waves = (int)((nb * 8 + 63) / 64);
+        if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q6k(n, p.waves);
+        if (!q4k_rows_ok(p.rows_per_wg)) return hipErrorInvalidConfiguration;
+        p.unroll = 4;
+        p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
+        if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+        if (plan) *plan = p;
+        return launch_q6k_ring(p.unroll, p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
+    }
+    if (qtype == kTypeQ6K && p.cpl == kQ6KRingUnit) return hipErrorInvalidValue;   // layout not eligible
     if (p.cpl <= 0) p.cpl = pick_cpl(qtype, nb);
     if (!cpl_valid(qtype, p.cpl)) return hipErrorInvalidValue;
     const int64_t lanes = nb * lanes_per_block(qtype, p.cpl);

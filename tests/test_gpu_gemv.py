@@ -105,7 +105,8 @@ def test_gemv_k_zero_and_n_zero(frq, q):
 
 
 @pytest.mark.parametrize("q,n,k", [("Q4_K", 300, 18944), ("Q4_K", 600, 3584), ("Q4_K", 97, 14336),
-                                   ("Q6_K", 300, 3584), ("Q8_0", 500, 896), ("Q1_0", 300, 4096)])
+                                   ("Q6_K", 300, 3584), ("Q6_K", 77, 14336), ("Q6_K", 50, 768), ("Q8_0", 500, 896),
+                                   ("Q1_0", 300, 4096)])
 def test_launch_geometry_sweep(frq, q, n, k):
     """Every supported geometry of both kernel families (split-K work items and
     whole-row workgroups) is within tolerance; for a fixed kernel family and
@@ -120,8 +121,8 @@ def test_launch_geometry_sweep(frq, q, n, k):
     yd = device.DeviceBuffer(n * 4)
     seen = {}
     for kernel in (_lib.GEMV_SPLITK, _lib.GEMV_ROWS):
-        for cpl in (1, 2, 4):
-            for rows in (1, 3, 4, 7, 8, 16, 32, 64):
+        for cpl in (1, 2, 4, 8):
+            for rows in (1, 3, 4, 7, 8, 14, 16, 32, 64):
                 for unroll in (2, 4, 8):
                     try:
                         cfg = device.gemv_tuned(q, w, xd, yd, n, k, kernel=kernel, cpl=cpl, rows=rows, unroll=unroll)
