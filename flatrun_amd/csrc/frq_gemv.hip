@@ -86,7 +86,7 @@ __device__ __forceinline__ void finish_rows(int64_t row0, int64_t row_end, float
 // Each row's lane partials are reduced with DPP only; results collect in LDS
 // and y is written once at the end.
 template <int CPL, int U, int R>
-__global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) gemv_q4_k_kernel(const uint8_t* __restrict__ w,
+__global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_waves_per_eu(CPL == 1 ? 5 : 1))) gemv_q4_k_kernel(const uint8_t* __restrict__ w,
                                                                          const float* __restrict__ x,
                                                                          float* __restrict__ y, int64_t n,
                                                                          int nb) {
@@ -764,7 +764,8 @@ bool unroll8_ok(int qtype, int cpl) {
 }
 
 // Q4_K: rows per workgroup is a compile-time constant of the kernel, one of
-// these; the ring depth is 3 or 5 slots (CPL 2) and 4 or 6 (CPL 1).
+// these; the ring depth is 3 or 5 slots (CPL 2) and 3 (CPL 1: compiled for
+// 5 waves per SIMD, <= 96 VGPRs, which measured fastest; deeper rings spill).
 constexpr int kQ4KRowSet[] = {1, 2, 4, 7, 8, 14, 16};
 
 bool q4k_rows_ok(int r) {
@@ -775,17 +776,23 @@ bool q4k_rows_ok(int r) {
 
 int q4k_ring(int cpl, int want) {
     if (cpl == 2) return want <= 3 ? 3 : 5;
-    return want <= 4 ? 4 : 6;
+    (void)want;
+    return 3;
 }
 
 // Rows per Q4_K workgroup (measured on MI355X, 256 CUs). Workgroups of 4 or
 // more waves run one per CU: take the fewest rows that still cover n with
 // at most 256 workgroups (one round, every CU busy). Smaller workgroups
 // (short rows) want several resident per CU: 4 rows per workgroup up to
-// n = 8192, 7 beyond.
+// n = 8192, beyond that the fewest rows that keep <= 2560 workgroups.
 int pick_rows_q4k(int64_t n, int waves) {
     const int64_t kCUs = 256;
-    if (waves < 4) return n <= 8192 ? 4 : 7;
+    if (waves < 4) {
+        if (n <= 8192) return 4;
+        for (int r : kQ4KRowSet)
+            if ((n + r - 1) / r <= 2560) return r;
+        return 16;
+    }
     for (int r : kQ4KRowSet)
         if ((n + r - 1) / r <= kCUs) return r;
     return 16;
@@ -817,10 +824,8 @@ hipError_t launch_q4k(int cpl, int ring, int rows, int waves, int64_t grid, cons
     bool ok = false;
     if (cpl == 2) {
         ok = ring == 3 ? q4k_rows<2, 3>(rows, gd, bd, s, w, x, y, n, nb) : q4k_rows<2, 5>(rows, gd, bd, s, w, x, y, n, nb);
-    } else if (ring == 4) {
-        ok = q4k_rows<1, 4>(rows, gd, bd, s, w, x, y, n, nb);
     } else {
-        ok = q4k_rows<1, 6>(rows, gd, bd, s, w, x, y, n, nb);
+        ok = q4k_rows<1, 3>(rows, gd, bd, s, w, x, y, n, nb);
     }
     if (!ok) return hipErrorInvalidConfiguration;
     return hipGetLastError();
@@ -934,7 +939,7 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
     if (qtype == kTypeQ4K) {
         if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q4k(n, p.waves);
         if (!q4k_rows_ok(p.rows_per_wg)) return hipErrorInvalidConfiguration;
-        p.unroll = q4k_ring(p.cpl, p.unroll > 0 ? p.unroll : (p.cpl == 1 ? 4 : 3));
+        p.unroll = q4k_ring(p.cpl, p.unroll > 0 ? p.unroll : 3);
         p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
         if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
         if (plan) *plan = p;
