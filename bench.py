@@ -182,9 +182,15 @@ LLAMA_LAYER = [
 ]
 
 
-def run_suite(stream, steps: int) -> dict:
+def run_suite(stream, steps: int, only: set | None = None) -> dict:
     out = {}
+
+    def want(name: str) -> bool:
+        return not only or name in only
+
     for idx, (name, q, n, k) in enumerate(SUITE):
+        if not want(name):
+            continue
         w = GemvWorkload(q, n, k, seed=100 + idx, stream=stream)
         t = w.time_throughput(steps, warmup=10)
         te = w.time_eager(min(steps, 200))
@@ -193,11 +199,14 @@ def run_suite(stream, steps: int) -> dict:
                      "frac_hbm": round(w.bytes / tk / 1e9 / HBM_PEAK_GBS, 4),
                      "eager_us_per_launch": round(te / min(steps, 200) * 1e6, 2), "effective_bytes": w.bytes}
         w.free()
-    out["llama3_8b_decode_resident"] = decode_sweep_resident(stream, steps=max(3, min(steps // 50, 20)))
-    out["llama3_8b_decode_streamed"] = decode_sweep_streamed(stream)
-    out["prefill_gemm_q4_k_bf16_512x14336x4096"] = prefill_gemm(stream)
-    out["copy_ceiling"] = copy_ceiling(stream)
-    out["host_path_q4_k_3584x18944"] = host_path_rate()
+    extra = [("llama3_8b_decode_resident", lambda: decode_sweep_resident(stream, steps=max(3, min(steps // 50, 20)))),
+             ("llama3_8b_decode_streamed", lambda: decode_sweep_streamed(stream)),
+             ("prefill_gemm_q4_k_bf16_512x14336x4096", lambda: prefill_gemm(stream)),
+             ("copy_ceiling", lambda: copy_ceiling(stream)),
+             ("host_path_q4_k_3584x18944", host_path_rate)]
+    for name, fn in extra:
+        if want(name):
+            out[name] = fn()
     return out
 
 
@@ -350,6 +359,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-suite", action="store_true")
+    ap.add_argument("--configs", default="",
+                    help="comma-separated subset of the other workloads to run (names as in the output's configs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after the headline, run the library's streaming copy 20 times over MIB MiB "
                          "(reference traffic for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
@@ -405,8 +416,10 @@ def main() -> int:
         src.free()
         dst.free()
     if not a.no_suite:
-        rec["configs"] = run_suite(stream, steps=min(a.steps, 500))
-        rec["decode_step_ms_resident"] = rec["configs"]["llama3_8b_decode_resident"]["ms_per_step"]
+        only = {c for c in a.configs.split(",") if c}
+        rec["configs"] = run_suite(stream, steps=min(a.steps, 500), only=only)
+        if "llama3_8b_decode_resident" in rec["configs"]:
+            rec["decode_step_ms_resident"] = rec["configs"]["llama3_8b_decode_resident"]["ms_per_step"]
     if not a.no_cpu:
         rec["cpu_baseline"] = cpu_baseline(work, y_gpu, a.cpu_seconds)
     work.free()
