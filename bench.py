@@ -76,6 +76,8 @@ class GemvWorkload:
         self.y = device.DeviceBuffer(4 * n)
         self.stream = stream
         self.bytes = effective_bytes(q, n, k)
+        self.launch(0)                     # first launch allocates any per-stream scratch, outside graph capture
+        device.synchronize()
 
     def launch(self, i: int) -> None:
         device.gemv(self.q, self.w[i % self.ncopies], self.x, self.y, self.n, self.k, stream=self.stream,

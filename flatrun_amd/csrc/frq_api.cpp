@@ -146,7 +146,7 @@ int sk_scratch(hipStream_t stream, size_t part_bytes, size_t cnt_bytes, float** 
 // One GEMV on device buffers: the whole-row kernel when a row fits one
 // workgroup, else the split-K kernel.
 int gemv_device(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s) {
-    if (frq::gemv_supported(qtype, n, k)) {
+    if (frq::gemv_supported(qtype, n, k)) {   // whole-row kernel, one slice: no scratch
         FRQ_HIP(frq::launch_gemv(qtype, w, x, y, n, k, nullptr, s));
         return FRQ_OK;
     }
@@ -420,13 +420,22 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     p.cpl = cfg->cpl;
     p.rows_per_wg = cfg->rows;
     p.unroll = cfg->unroll;
-    hipError_t e = frq::launch_gemv(qtype, wp, x, y, n, k, &p, s);
+    p.slices = cfg->slices;
+    float* part = nullptr;
+    uint32_t* cnt = nullptr;
+    if (p.slices == 2) {                       // the two-slice Q4_K kernel meets through scratch
+        size_t pb = 0, cb = 0;
+        frq::gemv_split_scratch(qtype, n, &pb, &cb);
+        if (pb && cb)
+            if (int rc = sk_scratch(s, pb, cb, &part, &cnt)) return rc;
+    }
+    hipError_t e = frq::launch_gemv(qtype, wp, x, y, n, k, &p, s, part, cnt);
     if (e != hipSuccess) return hip_fail(e, "launch_gemv");
     cfg->kernel = FRQ_GEMV_ROWS;
     cfg->cpl = p.cpl;
     cfg->rows = p.rows_per_wg;
     cfg->unroll = p.unroll;
-    cfg->slices = 1;
+    cfg->slices = p.slices > 0 ? p.slices : 1;
     cfg->waves_per_wg = p.waves;
     cfg->items = p.grid;
     return FRQ_OK;

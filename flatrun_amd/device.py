@@ -254,12 +254,12 @@ def gemv(qtype, w, x, y, n: int, k: int, batch: int = 1, stream=None, w_bytes: i
 
 
 def gemv_tuned(qtype, w, x, y, n: int, k: int, kernel: int = 0, cpl: int = 0, rows: int = 0, unroll: int = 0,
-               stream=None, w_bytes: int | None = None) -> dict:
+               stream=None, w_bytes: int | None = None, slices: int = 0) -> dict:
     """One GEMV with an explicit launch geometry; returns the geometry used
     (fields of frq_gemv_config)."""
     q = qtype_id(qtype)
     wb = _nbytes(w) if w_bytes is None else int(w_bytes)
-    cfg = _lib.GemvConfig(kernel=kernel, cpl=cpl, rows=rows, unroll=unroll)
+    cfg = _lib.GemvConfig(kernel=kernel, cpl=cpl, rows=rows, unroll=unroll, slices=slices)
     check(lib().frq_dev_gemv_tuned(q, _addr(w), wb, _addr(x), _addr(y), int(n), int(k), ctypes.addressof(cfg),
                                    _stream(stream)))
     return cfg.as_dict()

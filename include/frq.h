@@ -138,7 +138,9 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  *   cpl           work unit per lane (format specific)
  *   rows          rows per work item (SPLITK) / per workgroup (ROWS)
  *   unroll        rows per load batch
- *   slices        K-slices per row (output)
+ *   slices        K-slices per row: output for SPLITK; for the ROWS kernel
+ *                 of Q4_K also an input (0 = choose, 1, or 2: every row in
+ *                 two halves, one workgroup each, combined through memory)
  *   waves_per_wg  wavefronts per workgroup (output)
  *   items         work items / workgroups launched (output)              */
 enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2 };

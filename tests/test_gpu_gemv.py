@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from conftest import GOLDEN, MATVEC_RTOL, assert_matvec_close, assert_rel_close_to, bits_equal
-from flatrun_amd import _C, device, synth
+from flatrun_amd import _C, _lib, device, synth
 from oracle import gguf_np as G
 from oracle.loader import c_oracle
 
@@ -124,19 +124,60 @@ def test_launch_geometry_sweep(frq, q, n, k):
         for cpl in (1, 2, 4, 8):
             for rows in (1, 3, 4, 7, 8, 14, 16, 32, 64):
                 for unroll in (2, 4, 8):
-                    try:
-                        cfg = device.gemv_tuned(q, w, xd, yd, n, k, kernel=kernel, cpl=cpl, rows=rows, unroll=unroll)
-                    except RuntimeError:
-                        continue                     # geometry not valid for this format / k
-                    device.synchronize()
-                    y = yd.to_host(np.float32)
-                    assert_matvec_close(y, y64, absw, what=f"{cfg}")
-                    key = (cfg["kernel"], cfg["cpl"])
-                    if key in seen:
-                        assert bits_equal(y, seen[key]), cfg
-                    else:
-                        seen[key] = y
+                    for slices in ((0, 1, 2) if (q == "Q4_K" and kernel == _lib.GEMV_ROWS) else (0,)):
+                        try:
+                            cfg = device.gemv_tuned(q, w, xd, yd, n, k, kernel=kernel, cpl=cpl, rows=rows,
+                                                    unroll=unroll, slices=slices)
+                        except RuntimeError:
+                            continue                     # geometry not valid for this format / k
+                        device.synchronize()
+                        y = yd.to_host(np.float32)
+                        assert_matvec_close(y, y64, absw, what=f"{cfg}")
+                        key = (cfg["kernel"], cfg["cpl"], cfg["slices"] if kernel == _lib.GEMV_ROWS else 0)
+                        if key in seen:
+                            assert bits_equal(y, seen[key]), cfg
+                        else:
+                            seen[key] = y
     assert seen
+
+
+def test_two_slice_rows_repeated_and_alternating(frq):
+    """The two-slice Q4_K kernel (halves combined through memory) gives the
+    same bits launch after launch, alternating with other shapes that share
+    the stream's scratch, and in a captured graph replayed several times."""
+    cases = [(3584, 18944, 1), (257, 18944, 2), (1000, 16384, 3)]
+    s = device.Stream()
+    bufs = []
+    for n, k, seed in cases:
+        raw = synth.make_blocks("Q4_K", n, k, seed=seed)
+        x = synth.make_x(k, seed=seed + 10)
+        bufs.append((n, k, raw, x, device.DeviceBuffer.from_host(raw), device.DeviceBuffer.from_host(x),
+                     device.DeviceBuffer(4 * n)))
+    ref = []
+    for n, k, raw, x, w, xd, yd in bufs:
+        cfg = device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_lib.GEMV_ROWS, slices=2, stream=s)
+        assert cfg["slices"] == 2
+        s.synchronize()
+        y = yd.to_host(np.float32)
+        assert_matvec_close(y, G.matmul_f64("Q4_K", x, raw, n, k), G.abs_matmul_f64("Q4_K", x, raw, n, k))
+        ref.append(y)
+    for _ in range(20):
+        for n, k, raw, x, w, xd, yd in bufs:
+            device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_lib.GEMV_ROWS, slices=2, stream=s)
+    s.synchronize()
+    for (n, k, *_, yd), r in zip(bufs, ref):
+        assert bits_equal(yd.to_host(np.float32), r)
+    with device.Graph.capture(s) as cap:
+        for n, k, raw, x, w, xd, yd in bufs:
+            device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_lib.GEMV_ROWS, slices=2, stream=s)
+    try:
+        for _ in range(3):
+            cap.launch(s)
+            s.synchronize()
+            for (n, k, *_, yd), r in zip(bufs, ref):
+                assert bits_equal(yd.to_host(np.float32), r)
+    finally:
+        cap.destroy()
 
 
 def test_split_k_repeated_launches(frq):
