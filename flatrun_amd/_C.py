@@ -9,7 +9,8 @@ contiguous). Errors the reference raises as ``std::runtime_error`` arrive as
 :class:`flatrun_amd._lib.FrqError`, a ``RuntimeError``.
 
 Additions beyond the reference module, for the formats it lacks:
-``dequant_q5_k``, ``dequant_q1_0``, ``matmul_q5_k``, ``matmul_q1_0`` and
+``dequant_q5_k``, ``dequant_q1_0``, ``dequant_q4_0``, ``dequant_q5_0``,
+``dequant_q5_1``, ``matmul_q5_k``, ``matmul_q1_0`` and
 their ``_batched`` forms, ``dequant(qtype, weight, shape)`` with the NumPy
 decoders' ragged-size rule, and ``matmul_q4_k_bf16`` (prefill GEMM on the
 matrix cores, bf16 inputs).
@@ -92,6 +93,18 @@ def dequant_q5_k(weight, shape):
 
 def dequant_q1_0(weight, shape):
     return dequant(_lib.Q1_0, weight, shape)
+
+
+def dequant_q4_0(weight, shape):
+    return dequant(_lib.Q4_0, weight, shape)
+
+
+def dequant_q5_0(weight, shape):
+    return dequant(_lib.Q5_0, weight, shape)
+
+
+def dequant_q5_1(weight, shape):
+    return dequant(_lib.Q5_1, weight, shape)
 
 
 # ------------------------------------------------------------------ matmul

@@ -223,3 +223,18 @@ class NativeBackend:
     def dequant_q1_0(self, weight, shape):
         self._require()
         return _C.dequant_q1_0(_raw_bytes(weight), shape)
+
+    def dequant_q4_0(self, weight, shape):
+        """Q4_0 dequant (the reference decodes it in NumPy, dequant/gguf.py:81-107)."""
+        self._require()
+        return _C.dequant_q4_0(_raw_bytes(weight), shape)
+
+    def dequant_q5_0(self, weight, shape):
+        """Q5_0 dequant (dequant/gguf.py:302-330)."""
+        self._require()
+        return _C.dequant_q5_0(_raw_bytes(weight), shape)
+
+    def dequant_q5_1(self, weight, shape):
+        """Q5_1 dequant (dequant/gguf.py:333-362)."""
+        self._require()
+        return _C.dequant_q5_1(_raw_bytes(weight), shape)

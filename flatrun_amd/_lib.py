@@ -25,7 +25,9 @@ STATUS_NAMES = {
 
 # GGML type ids (src/flatrun/backend/gguf.py:59-86)
 Q8_0, Q4_K, Q5_K, Q6_K, Q1_0 = 8, 12, 13, 14, 41
-QTYPES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K, "Q1_0": Q1_0}
+Q4_0, Q5_0, Q5_1 = 2, 6, 7          # dequant only
+QTYPES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K, "Q1_0": Q1_0,
+          "Q4_0": Q4_0, "Q5_0": Q5_0, "Q5_1": Q5_1}
 BLOCKS = {Q8_0: (34, 32), Q4_K: (144, 256), Q5_K: (176, 256), Q6_K: (210, 256), Q1_0: (18, 128)}
 
 

@@ -55,6 +55,9 @@ bool fmt_of(int qtype, Fmt* f) {
         case FRQ_Q5_K: *f = {"Q5_K", 176, 256}; return true;
         case FRQ_Q6_K: *f = {"Q6_K", 210, 256}; return true;
         case FRQ_Q1_0: *f = {"Q1_0", 18, 128}; return true;
+        case FRQ_Q4_0: *f = {"Q4_0", 18, 32}; return true;
+        case FRQ_Q5_0: *f = {"Q5_0", 22, 32}; return true;
+        case FRQ_Q5_1: *f = {"Q5_1", 24, 32}; return true;
         default: return false;
     }
 }
@@ -278,7 +281,7 @@ int check_dev_ptrs(int qtype, const void* w, const float* x, const float* y) {
 
 extern "C" {
 
-const char* frq_version(void) { return "flatrun_amd 0.1.0 (gfx950 HIP: Q8_0, Q4_K, Q5_K, Q6_K, Q1_0)"; }
+const char* frq_version(void) { return "flatrun_amd 0.2.0 (gfx950 HIP: Q8_0, Q4_K, Q5_K, Q6_K, Q1_0; dequant Q4_0, Q5_0, Q5_1)"; }
 int frq_is_neon(void) { return 0; }
 const char* frq_last_error(void) { return g_err.c_str(); }
 

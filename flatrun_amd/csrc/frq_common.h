@@ -7,6 +7,9 @@
 //   Q5_K  id 13 176 B / 256   [d f16][dmin f16][scales 12][qh 32][qs 128]
 //   Q6_K  id 14 210 B / 256   [ql 128][qh 64][scales i8 x16][d f16]
 //   Q1_0  id 41  18 B / 128   [d f16][qs 16]  (1 sign bit per element, LSB first)
+//   Q4_0  id 2   18 B /  32   [d f16][qs 16]
+//   Q5_0  id 6   22 B /  32   [d f16][qh 4][qs 16]
+//   Q5_1  id 7   24 B /  32   [d f16][m f16][qh 4][qs 16]
 //
 // All code here is compiled with -ffp-contract=off: every product and sum
 // rounds on its own exactly where it is written, which the bit-exact dequant
@@ -36,6 +39,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 constexpr int kQ80Bytes = 34, kQ80Elems = 32;
 constexpr int kQ4KBytes = 144, kQ5KBytes = 176, kQ6KBytes = 210, kQKElems = 256;
 constexpr int kQ10Bytes = 18, kQ10Elems = 128;
+constexpr int kQ40Bytes = 18, kQ50Bytes = 22, kQ51Bytes = 24;   // 32 elements each
 
 // IEEE binary16 -> binary32. v_cvt_f32_f16 is exact for every finite input,
 // subnormals included (f16 denormals are enabled in the default FP mode).

@@ -7,6 +7,11 @@
 //   Q5_K  fl32(fl64(fl32(d*sc) * v) - fl32(dmin*m))       gguf.py:223-263
 //   Q6_K  fl32(fl32(d*sc) * (q - 32))                     gguf.py:365-420
 //   Q1_0  +d / -d by bit, LSB first                       gguf.py:266-299
+//   Q4_0  fl32((q - 8) * d)                               gguf.py:81-107
+//   Q5_0  fl32((q - 16) * d), q = nibble | qh bit << 4    gguf.py:302-330
+//   Q5_1  fl32(fl32(d * q) + m)                           gguf.py:333-362
+// (every product above except Q4_K's and Q5_K's is exact in fp32: an fp16
+// scale times an integer of at most 6 bits).
 // This translation unit is built with -ffp-contract=off, so none of the
 // products above is fused into the following add.
 //
@@ -125,6 +130,39 @@ __global__ void __launch_bounds__(256) dequant_q1_0_kernel(const uint8_t* __rest
     store4(y, e0, n, v[0], v[1], v[2], v[3]);
 }
 
+// Q4_0 / Q5_0 / Q5_1: 32-element blocks; byte j of qs holds element j in its
+// low nibble and element j + 16 in its high nibble; for Q5_x the 5th bit of
+// element j (j < 16) is bit j of the little-endian qh word and of element
+// j + 16 bit j + 16. A thread's four outputs are four consecutive elements of
+// one half: bytes 4p .. 4p+3 of qs (p = offset / 4 within the half).
+template <int BB, int QS_OFF, bool FIVE, bool MIN>
+__global__ void __launch_bounds__(256) dequant_q32_kernel(const uint8_t* __restrict__ w, float* __restrict__ y,
+                                                          int64_t n) {
+    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (e0 >= n) return;
+    const int64_t b = e0 / 32;
+    const int o = (int)(e0 % 32);
+    const int half = o >> 4, j0 = o & 15;
+    const uint8_t* blk = w + b * BB;
+    const float d = f16_bits_to_f32(ld_u16(blk));
+    const uint32_t qs = ld_u32_a2(blk + QS_OFF + j0);
+    uint32_t qh = 0;
+    if constexpr (FIVE) qh = ld_u32_a2(blk + (MIN ? 4 : 2)) >> (16 * half + j0);
+    float v[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        uint32_t q = (qs >> (8 * c + 4 * half)) & 15u;
+        if constexpr (FIVE) q |= ((qh >> c) & 1u) << 4;
+        if constexpr (MIN) {
+            const float m = f16_bits_to_f32(ld_u16(blk + 2));
+            v[c] = d * (float)q + m;
+        } else {
+            v[c] = (float)((int)q - (FIVE ? 16 : 8)) * d;
+        }
+    }
+    store4(y, e0, n, v[0], v[1], v[2], v[3]);
+}
+
 __global__ void __launch_bounds__(256) fill_kernel(float* __restrict__ y, float v, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) y[i] = v;
@@ -164,6 +202,9 @@ hipError_t launch_dequant(int qtype, const uint8_t* w, float* y, int64_t n, hipS
         case kTypeQ6K: dequant_q6_k_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
         case kTypeQ80: dequant_q8_0_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
         case kTypeQ10: dequant_q1_0_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
+        case kTypeQ40: dequant_q32_kernel<kQ40Bytes, 2, false, false><<<grid, block, 0, stream>>>(w, y, n); break;
+        case kTypeQ50: dequant_q32_kernel<kQ50Bytes, 6, true, false><<<grid, block, 0, stream>>>(w, y, n); break;
+        case kTypeQ51: dequant_q32_kernel<kQ51Bytes, 8, true, true><<<grid, block, 0, stream>>>(w, y, n); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

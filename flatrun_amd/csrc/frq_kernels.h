@@ -12,6 +12,9 @@ constexpr int kTypeQ4K = 12;
 constexpr int kTypeQ5K = 13;
 constexpr int kTypeQ6K = 14;
 constexpr int kTypeQ10 = 41;
+constexpr int kTypeQ40 = 2;     // dequant only
+constexpr int kTypeQ50 = 6;     // dequant only
+constexpr int kTypeQ51 = 7;     // dequant only
 
 // Launch geometry of one GEMV: lanes per row, waves per workgroup, rows per
 // workgroup and the per-format work unit chosen for it.

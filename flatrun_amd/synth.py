@@ -8,6 +8,8 @@ with the distributions of the benchmark workloads:
 * Q5_K: as Q4_K, plus the 5th bit of every element Bernoulli(0.5)
 * Q6_K: q6 U[0, 63]; 16 int8 scales U[-64, 63]; d fp16(U[1e-4, 5e-3])
 * Q1_0: d = fp16(U[1e-3, 1e-2]); sign bits Bernoulli(0.5)
+* Q4_0 / Q5_0: d = fp16(U[1e-3, 1e-2]); nibbles (and 5th bits) uniform
+* Q5_1: d = fp16(U[1e-3, 1e-2]), m = fp16(U[-0.1, 0.1]); as Q5_0
 
 Uniform random bytes are exactly uniform on every packed field: the 12-byte
 K-quant scale field is a bijection of the sixteen 6-bit values (high bits
@@ -24,7 +26,8 @@ from __future__ import annotations
 
 import numpy as np
 
-BLOCK = {"Q8_0": (34, 32), "Q4_K": (144, 256), "Q5_K": (176, 256), "Q6_K": (210, 256), "Q1_0": (18, 128)}
+BLOCK = {"Q8_0": (34, 32), "Q4_K": (144, 256), "Q5_K": (176, 256), "Q6_K": (210, 256), "Q1_0": (18, 128),
+         "Q4_0": (18, 32), "Q5_0": (22, 32), "Q5_1": (24, 32)}
 
 
 def nbytes(qname: str, n: int, k: int) -> int:
@@ -57,6 +60,10 @@ def make_blocks(qname: str, n: int, k: int, seed: int = 0) -> np.ndarray:
     elif qname in ("Q4_K", "Q5_K"):
         _put_u16(b, 0, _f16(rng, 1e-4, 5e-3, nblk))
         _put_u16(b, 2, _f16(rng, 1e-4, 5e-3, nblk))
+    elif qname in ("Q4_0", "Q5_0", "Q5_1"):
+        _put_u16(b, 0, _f16(rng, 1e-3, 1e-2, nblk))
+        if qname == "Q5_1":
+            _put_u16(b, 2, _f16(rng, -0.1, 0.1, nblk))
     elif qname == "Q6_K":
         b[:, 192:208] = rng.integers(-64, 64, size=(nblk, 16), dtype=np.int8).view(np.uint8)
         _put_u16(b, 208, _f16(rng, 1e-4, 5e-3, nblk))

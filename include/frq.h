@@ -26,7 +26,10 @@
  * Quant types are GGML type ids (src/flatrun/backend/gguf.py:59-86):
  *   FRQ_Q8_0 = 8 (34 B / 32), FRQ_Q4_K = 12 (144 B / 256),
  *   FRQ_Q5_K = 13 (176 B / 256), FRQ_Q6_K = 14 (210 B / 256),
- *   FRQ_Q1_0 = 41 (18 B / 128).
+ *   FRQ_Q1_0 = 41 (18 B / 128),
+ *   FRQ_Q4_0 = 2 (18 B / 32), FRQ_Q5_0 = 6 (22 B / 32), FRQ_Q5_1 = 7
+ *   (24 B / 32): dequant only (the reference decodes them in NumPy,
+ *   dequant/gguf.py:81-107, 302-362; no native matvec exists for them).
  *
  * Numerics: dequant is bit-exact with the reference NumPy decoders
  * (src/flatrun/dequant/gguf.py); matmul accumulates in fp32 and is held to
@@ -54,7 +57,8 @@ typedef enum {
     FRQ_ERR_ALIGN = 7         /* device pointer misaligned for its format       */
 } frq_status;
 
-enum { FRQ_Q8_0 = 8, FRQ_Q4_K = 12, FRQ_Q5_K = 13, FRQ_Q6_K = 14, FRQ_Q1_0 = 41 };
+enum { FRQ_Q4_0 = 2, FRQ_Q5_0 = 6, FRQ_Q5_1 = 7, FRQ_Q8_0 = 8, FRQ_Q4_K = 12, FRQ_Q5_K = 13, FRQ_Q6_K = 14,
+       FRQ_Q1_0 = 41 };
 
 /* ---------------------------------------------------------------- general */
 

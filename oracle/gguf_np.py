@@ -14,6 +14,9 @@ kernels are held to *bit-exact* agreement with those functions:
         are float64 and the result is rounded twice (f64, then f32 on store).
 * Q6_K  ``y = fl32(fl32(d*sc) * (q - 32))``                    (gguf.py:365-420)
 * Q1_0  ``y = +d`` if bit set else ``-d``, bits LSB-first      (gguf.py:266-299)
+* Q4_0  ``y = fl32((q - 8) * d)``, low nibbles first half      (gguf.py:81-107)
+* Q5_0  ``y = fl32((q - 16) * d)``, 5th bit from ``qh``        (gguf.py:302-330)
+* Q5_1  ``y = fl32(fl32(d * q) + m)``                          (gguf.py:333-362)
 
 Like the reference, every decoder accepts a size that is not a multiple of the
 block and trims the decoded tail (``_finish``, gguf.py:61-73); the tail block
@@ -32,6 +35,10 @@ Parity pins (tests/test_oracle_*.py):
   the zero-block KAT.
 * Q1_0: the reference KATs (0xAA/0x01 pattern, zero block, 130-element tail)
   and the closed form ``+-d``.
+* Q4_0 / Q5_0 / Q5_1: the reference KATs (test_dequant.py:60-72, 212-238),
+  plus hand blocks that set one qs nibble or one qh bit at a time and check
+  the one element it lands on (element order and bit position), and the
+  exactness of every product (fp16 scale times a <= 5-bit integer).
 """
 
 from __future__ import annotations
@@ -48,6 +55,9 @@ GGML_TYPES = {
     13: ("Q5_K", 176, 256),
     14: ("Q6_K", 210, 256),
     41: ("Q1_0", 18, 128),
+    2: ("Q4_0", 18, 32),
+    6: ("Q5_0", 22, 32),
+    7: ("Q5_1", 24, 32),
 }
 BLOCK = {name: (nbytes, nel) for _, (name, nbytes, nel) in GGML_TYPES.items()}
 
@@ -181,7 +191,56 @@ def dequant_q1_0(raw, shape, dtype=np.float32) -> np.ndarray:
     return _done(sign * d[:, None], size, shape, dtype)
 
 
+def _q5_high(a: np.ndarray, off: int) -> tuple[np.ndarray, np.ndarray]:
+    """16 * (5th bit) for elements j and j + 16 of each block: bit j and bit
+    j + 16 of the little-endian uint32 at byte ``off`` (gguf.py:316-319)."""
+    qh = a[:, off:off + 4].copy().view(np.uint32).reshape(-1)
+    j = np.arange(16, dtype=np.uint32)
+    lo = ((qh[:, None] >> j[None, :]) & np.uint32(1)) << np.uint32(4)
+    hi = ((qh[:, None] >> (j[None, :] + np.uint32(16))) & np.uint32(1)) << np.uint32(4)
+    return lo.astype(np.uint8), hi.astype(np.uint8)
+
+
+def dequant_q4_0(raw, shape, dtype=np.float32) -> np.ndarray:
+    size = int(np.prod(shape))
+    if size == 0:
+        return np.empty(0, dtype=dtype).reshape(shape)
+    size, nblk, a = _blocks(raw, shape, "Q4_0")
+    d = _half(a[:, 0:2])
+    qs = a[:, 2:18]
+    q = np.concatenate([qs & 0x0F, qs >> 4], axis=1).astype(np.float32) - np.float32(8.0)
+    return _done(q * d[:, None], size, shape, dtype)
+
+
+def dequant_q5_0(raw, shape, dtype=np.float32) -> np.ndarray:
+    size = int(np.prod(shape))
+    if size == 0:
+        return np.empty(0, dtype=dtype).reshape(shape)
+    size, nblk, a = _blocks(raw, shape, "Q5_0")
+    d = _half(a[:, 0:2])
+    hlo, hhi = _q5_high(a, 2)
+    qs = a[:, 6:22]
+    q = np.concatenate([(qs & 0x0F) | hlo, (qs >> 4) | hhi], axis=1).astype(np.float32) - np.float32(16.0)
+    return _done(q * d[:, None], size, shape, dtype)
+
+
+def dequant_q5_1(raw, shape, dtype=np.float32) -> np.ndarray:
+    size = int(np.prod(shape))
+    if size == 0:
+        return np.empty(0, dtype=dtype).reshape(shape)
+    size, nblk, a = _blocks(raw, shape, "Q5_1")
+    d = _half(a[:, 0:2])
+    m = _half(a[:, 2:4])
+    hlo, hhi = _q5_high(a, 4)
+    qs = a[:, 8:24]
+    q = np.concatenate([(qs & 0x0F) | hlo, (qs >> 4) | hhi], axis=1).astype(np.float32)
+    return _done(d[:, None] * q + m[:, None], size, shape, dtype)
+
+
 DEQUANT = {
+    "Q4_0": dequant_q4_0,
+    "Q5_0": dequant_q5_0,
+    "Q5_1": dequant_q5_1,
     "Q8_0": dequant_q8_0,
     "Q4_K": dequant_q4_k,
     "Q5_K": dequant_q5_k,

@@ -17,7 +17,7 @@ from oracle import gguf_np as G
 
 pytestmark = pytest.mark.gpu
 
-QS = ["Q8_0", "Q4_K", "Q5_K", "Q6_K", "Q1_0"]
+QS = ["Q8_0", "Q4_K", "Q5_K", "Q6_K", "Q1_0", "Q4_0", "Q5_0", "Q5_1"]
 
 
 def gpu_dequant(q, raw, shape):
@@ -53,7 +53,8 @@ def test_dequant_fp16_edge_scales(frq, q):
     edge = np.array([0x0001, 0x03FF, 0x8200, 0x7BFF, 0xFBFF, 0x0000, 0x8000, 0x3C00, 0x7C00, 0xFE00],
                     dtype=np.uint16)
     raw = synth.make_blocks(q, 1, len(edge) * be, seed=5).reshape(-1, bb)
-    offs = {"Q8_0": [0], "Q4_K": [0, 2], "Q5_K": [0, 2], "Q6_K": [208], "Q1_0": [0]}[q]
+    offs = {"Q8_0": [0], "Q4_K": [0, 2], "Q5_K": [0, 2], "Q6_K": [208], "Q1_0": [0], "Q4_0": [0], "Q5_0": [0],
+            "Q5_1": [0, 2]}[q]
     for i, h in enumerate(edge):
         for o in offs:
             raw[i, o], raw[i, o + 1] = h & 0xFF, h >> 8
@@ -68,9 +69,11 @@ def test_dequant_fp16_edge_scales(frq, q):
 
 def test_reference_kats_on_gpu(frq):
     """The KATs of src/flatrun/tests/test_dequant.py on the HIP kernels."""
-    from test_oracle_kats import kat_q1_0_pattern, kat_q6_k_qh_pairs, kat_q8_0_simple, kat_q8_0_two_blocks
+    from test_oracle_kats import (kat_q1_0_pattern, kat_q4_0_nibble_order, kat_q5_0_all_high_bits, kat_q5_1_offset,
+                                  kat_q6_k_qh_pairs, kat_q8_0_simple, kat_q8_0_two_blocks)
 
-    for q, make in (("Q8_0", kat_q8_0_simple), ("Q8_0", kat_q8_0_two_blocks), ("Q1_0", kat_q1_0_pattern)):
+    for q, make in (("Q8_0", kat_q8_0_simple), ("Q8_0", kat_q8_0_two_blocks), ("Q1_0", kat_q1_0_pattern),
+                    ("Q4_0", kat_q4_0_nibble_order), ("Q5_0", kat_q5_0_all_high_bits), ("Q5_1", kat_q5_1_offset)):
         raw, shape, exp = make()
         assert np.array_equal(gpu_dequant(q, np.frombuffer(raw, np.uint8), shape), exp)
     raw, shape, _ = kat_q6_k_qh_pairs()

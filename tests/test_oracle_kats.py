@@ -46,7 +46,26 @@ def kat_q6_k_qh_pairs():
     return raw, (256,), None
 
 
+def kat_q4_0_nibble_order():
+    raw = np.float16(0.5).tobytes() + np.full(16, 0xF7, np.uint8).tobytes()
+    return raw, (32,), np.concatenate([np.full(16, -0.5, F32), np.full(16, 3.5, F32)])
+
+
+def kat_q5_0_all_high_bits():
+    raw = np.float16(0.25).tobytes() + np.uint32(0xFFFFFFFF).tobytes() + np.zeros(16, np.uint8).tobytes()
+    return raw, (32,), np.zeros(32, F32)
+
+
+def kat_q5_1_offset():
+    raw = (np.float16(0.5).tobytes() + np.float16(1.0).tobytes() + np.uint32(0).tobytes()
+           + np.full(16, 0x55, np.uint8).tobytes())
+    return raw, (32,), np.full(32, 5 * 0.5 + 1.0, F32)
+
+
 KATS = {
+    "q4_0_nibble_order": ("Q4_0", kat_q4_0_nibble_order),   # test_dequant.py:60-72
+    "q5_0_all_high_bits": ("Q5_0", kat_q5_0_all_high_bits),  # test_dequant.py:212-224
+    "q5_1_offset": ("Q5_1", kat_q5_1_offset),                # test_dequant.py:227-238
     "q8_0_simple": ("Q8_0", kat_q8_0_simple),          # test_dequant.py:32-42
     "q8_0_two_blocks": ("Q8_0", kat_q8_0_two_blocks),  # test_dequant.py:45-57
     "q1_0_pattern": ("Q1_0", kat_q1_0_pattern),        # test_dequant.py:297-317 (and :274-294)

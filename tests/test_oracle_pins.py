@@ -233,3 +233,59 @@ def test_c_oracle_threads_match_single(ref_C):
     x = synth.make_x(1024, seed=4)
     assert bits_equal(c_oracle().matmul("Q4_K", x, raw, 64, 1024, threads=4),
                       c_oracle().matmul("Q4_K", x, raw, 64, 1024, threads=1))
+
+
+# ---------------------------------------------------------------- Q4_0 / Q5_0 / Q5_1
+# One nibble or one qh bit is changed at a time; exactly the element it belongs
+# to (low nibble of byte j -> element j, high nibble -> j + 16, qh bit b ->
+# element b) must move, by the closed-form amount.
+
+def _blk32(q, d=0.5, m=0.25, qh=0, qs=None):
+    qs = np.zeros(16, np.uint8) if qs is None else qs
+    head = np.float16(d).tobytes()
+    if q == "Q5_1":
+        head += np.float16(m).tobytes()
+    if q in ("Q5_0", "Q5_1"):
+        head += np.uint32(qh).tobytes()
+    return np.frombuffer(head + qs.tobytes(), np.uint8)
+
+
+def test_q4_0_each_nibble_lands_on_its_element():
+    base = np.full(16, 0x88, np.uint8)                      # every element (8 - 8) * d = 0
+    assert np.array_equal(G.dequant_q4_0(_blk32("Q4_0", qs=base), (32,)), np.zeros(32, np.float32))
+    for j in range(16):
+        for hi in (False, True):
+            qs = base.copy()
+            qs[j] = 0x8F if not hi else 0xF8                # nibble 15: (15 - 8) * 0.5 = 3.5
+            out = G.dequant_q4_0(_blk32("Q4_0", qs=qs), (32,))
+            exp = np.zeros(32, np.float32)
+            exp[j + 16 * hi] = 3.5
+            assert np.array_equal(out, exp), (j, hi)
+
+
+@pytest.mark.parametrize("q", ["Q5_0", "Q5_1"])
+def test_q5_each_qh_bit_lands_on_its_element(q):
+    d, m = 0.5, 0.25
+    low = -16 * d if q == "Q5_0" else m                     # qs = 0, no high bit
+    for b in range(32):
+        out = G.DEQUANT[q](_blk32(q, d=d, m=m, qh=1 << b), (32,))
+        exp = np.full(32, low, np.float32)
+        exp[b] = low + 16 * d
+        assert np.array_equal(out, exp), (q, b)
+
+
+@pytest.mark.parametrize("q", ["Q5_0", "Q5_1"])
+def test_q5_nibbles_and_high_bit_combine(q):
+    """q = nibble | 16 * bit, for every (nibble, bit) on every position."""
+    rng = np.random.default_rng(3)
+    for _ in range(20):
+        qs = rng.integers(0, 256, 16, dtype=np.uint8)
+        qh = int(rng.integers(0, 2 ** 32, dtype=np.uint64))
+        d = float(np.float16(rng.uniform(1e-3, 1e-2)))
+        m = float(np.float16(rng.uniform(-0.1, 0.1)))
+        out = G.DEQUANT[q](_blk32(q, d=d, m=m, qh=qh, qs=qs), (32,)).astype(np.float64)
+        for e in range(32):
+            nib = (int(qs[e % 16]) >> (4 * (e // 16))) & 15
+            v = nib + 16 * ((qh >> e) & 1)
+            ref = (v - 16) * d if q == "Q5_0" else np.float32(np.float32(d) * np.float32(v) + np.float32(m))
+            assert out[e] == ref, (q, e)
