@@ -13,7 +13,8 @@ Additions beyond the reference module, for the formats it lacks:
 ``dequant_q5_1``, ``matmul_q5_k``, ``matmul_q1_0`` and
 their ``_batched`` forms, ``dequant(qtype, weight, shape)`` with the NumPy
 decoders' ragged-size rule, and ``matmul_q4_k_bf16`` (prefill GEMM on the
-matrix cores, bf16 inputs).
+matrix cores, bf16 inputs; also ``matmul_q6_k_bf16``, ``matmul_q8_0_bf16``,
+``matmul_bf16(qtype, ...)``).
 """
 
 from __future__ import annotations
@@ -205,24 +206,37 @@ def to_bf16_bits(a) -> np.ndarray:
     return r
 
 
-def matmul_q4_k_bf16(x, weight, n, k):
+def matmul_bf16(qtype, x, weight, n, k):
     """out[seq, n] = x[seq, k] . W^T on the matrix cores, x and W in bf16
     (x given as float32 is rounded to bf16 first; a uint16 array is taken as
-    bf16 bits), fp32 accumulation. 1-D x gives out[n]. The fp32 per-token
-    path is matmul_q4_k_batched (_C.cpp:154-197)."""
+    bf16 bits), fp32 accumulation; W is Q4_K, Q6_K or Q8_0. 1-D x gives
+    out[n]. The fp32 per-token paths are matmul_<q>_batched (_C.cpp:154-283)."""
     xa = np.asarray(x)
     xb = np.ascontiguousarray(xa) if xa.dtype == np.uint16 else to_bf16_bits(xa)
     one_d = xb.ndim == 1
     x2 = xb.reshape(1, -1) if one_d else xb
     if x2.ndim != 2:
-        raise _lib.FrqError(_lib.ERR_SHAPE, "Q4_K gemm: x must be 1-D or 2-D")
+        raise _lib.FrqError(_lib.ERR_SHAPE, "gemm: x must be 1-D or 2-D")
     n, k = _size_t(n, "n"), _size_t(k, "k")
     if x2.shape[1] != k:
-        raise _lib.FrqError(_lib.ERR_SHAPE, "Q4_K gemm: x.shape[-1] != k")
+        raise _lib.FrqError(_lib.ERR_SHAPE, "gemm: x.shape[-1] != k")
     w = _u8(weight)
+    q = _lib.QTYPES[qtype.upper()] if isinstance(qtype, str) else int(qtype)
     out = np.empty((x2.shape[0], n), dtype=np.float32)
-    check(lib().frq_gemm_q4_k_bf16(ptr(x2), ptr(w), w.size, x2.shape[0], n, k, ptr(out)))
+    check(lib().frq_gemm_bf16(q, ptr(x2), ptr(w), w.size, x2.shape[0], n, k, ptr(out)))
     return out[0] if one_d else out
+
+
+def matmul_q4_k_bf16(x, weight, n, k):
+    return matmul_bf16(_lib.Q4_K, x, weight, n, k)
+
+
+def matmul_q6_k_bf16(x, weight, n, k):
+    return matmul_bf16(_lib.Q6_K, x, weight, n, k)
+
+
+def matmul_q8_0_bf16(x, weight, n, k):
+    return matmul_bf16(_lib.Q8_0, x, weight, n, k)
 
 
 # ------------------------------------------------------------------ diagnostics

@@ -179,13 +179,10 @@ class NativeBackend:
         """Fused Q1_0 dequant + matvec (no native counterpart in the reference)."""
         return self._matmul("Q1_0", x, weight, n, k)
 
-    def matmul_q4k_bf16(self, x, weight, n: int, k: int):
-        """Prefill GEMM on the matrix cores: x (seq, k) rounded to bf16, W
-        dequantized to bf16, fp32 accumulation -> (seq, n) float32. The fp32
-        per-token path (the reference's contract) is ``matmul_q4k``."""
+    def _gemm_bf16(self, qname: str, x, weight, n: int, k: int):
         self._require()
         if not isinstance(weight, DeviceWeight):
-            return _C.matmul_q4_k_bf16(x, _raw_bytes(weight), n, k)
+            return _C.matmul_bf16(qname, x, _raw_bytes(weight), n, k)
         from . import device
         xb = _C.to_bf16_bits(x)
         x2 = xb.reshape(1, -1) if xb.ndim == 1 else xb
@@ -194,13 +191,27 @@ class NativeBackend:
         xd = device.DeviceBuffer.from_host(x2)
         yd = device.DeviceBuffer(max(1, x2.shape[0] * n * 4))
         try:
-            device.gemm_q4k_bf16(weight, xd, yd, x2.shape[0], n, k, w_bytes=weight.nbytes)
+            device.gemm_bf16(qname, weight, xd, yd, x2.shape[0], n, k, w_bytes=weight.nbytes)
             device.synchronize()
             y = yd.to_host(np.float32)[: x2.shape[0] * n].reshape(x2.shape[0], n)
         finally:
             xd.free()
             yd.free()
         return y[0] if xb.ndim == 1 else y
+
+    def matmul_q4k_bf16(self, x, weight, n: int, k: int):
+        """Prefill GEMM on the matrix cores: x (seq, k) rounded to bf16, W
+        dequantized to bf16, fp32 accumulation -> (seq, n) float32. The fp32
+        per-token path (the reference's contract) is ``matmul_q4k``."""
+        return self._gemm_bf16("Q4_K", x, weight, n, k)
+
+    def matmul_q6k_bf16(self, x, weight, n: int, k: int):
+        """As matmul_q4k_bf16 for Q6_K weights (fp32 path: ``matmul_q6_k``)."""
+        return self._gemm_bf16("Q6_K", x, weight, n, k)
+
+    def matmul_q8_0_bf16(self, x, weight, n: int, k: int):
+        """As matmul_q4k_bf16 for Q8_0 weights (fp32 path: ``matmul_q8_0``)."""
+        return self._gemm_bf16("Q8_0", x, weight, n, k)
 
     # ------------------------------------------------------------ dequant
     def dequant_q4k(self, weight, shape: tuple[int, int]):

@@ -444,19 +444,24 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     return FRQ_OK;
 }
 
-static int gemm_checks(const void* w, size_t w_bytes, int64_t m, int64_t n, int64_t k) {
-    if (m < 0 || n < 0 || k < 0) return fail(FRQ_ERR_SHAPE, "Q4_K gemm: negative shape");
-    if (k % 256) return fail(FRQ_ERR_SHAPE, "Q4_K gemm: in_features must be a multiple of 256");
-    if ((int64_t)w_bytes != n * (k / 256) * 144) return fail(FRQ_ERR_SIZE, "Q4_K gemm: weight byte size mismatch");
-    if (m > 0 && n > 0 && k > 0 && !frq::gemm_q4_k_bf16_supported(m, n, k))
-        return fail(FRQ_ERR_UNSUPPORTED, "Q4_K gemm: shape beyond this build's limits");
-    (void)w;
+static int gemm_checks(int qtype, size_t w_bytes, int64_t m, int64_t n, int64_t k, Fmt* f) {
+    if (qtype != FRQ_Q4_K && qtype != FRQ_Q6_K && qtype != FRQ_Q8_0)
+        return fail(FRQ_ERR_UNSUPPORTED, "gemm: quant type %d has no matrix-core GEMM (Q4_K, Q6_K, Q8_0)", qtype);
+    fmt_of(qtype, f);
+    const int64_t kq = qtype == FRQ_Q8_0 ? 128 : 256;
+    if (m < 0 || n < 0 || k < 0) return fail(FRQ_ERR_SHAPE, "%s gemm: negative shape", f->name);
+    if (k % kq) return fail(FRQ_ERR_SHAPE, "%s gemm: in_features must be a multiple of %lld", f->name, (long long)kq);
+    if ((int64_t)w_bytes != n * (k / f->belems) * f->bbytes)
+        return fail(FRQ_ERR_SIZE, "%s gemm: weight byte size mismatch", f->name);
+    if (m > 0 && n > 0 && k > 0 && !frq::gemm_bf16_supported(qtype, m, n, k))
+        return fail(FRQ_ERR_UNSUPPORTED, "%s gemm: shape beyond this build's limits", f->name);
     return FRQ_OK;
 }
 
-int frq_dev_gemm_q4_k_bf16(const void* w, size_t w_bytes, const uint16_t* x, float* y, int64_t m, int64_t n,
-                           int64_t k, void* stream) {
-    if (int rc = gemm_checks(w, w_bytes, m, n, k)) return rc;
+int frq_dev_gemm_bf16(int qtype, const void* w, size_t w_bytes, const uint16_t* x, float* y, int64_t m, int64_t n,
+                      int64_t k, void* stream) {
+    Fmt f;
+    if (int rc = gemm_checks(qtype, w_bytes, m, n, k, &f)) return rc;
     if (m == 0 || n == 0) return FRQ_OK;
     if (!y) return fail(FRQ_ERR_INVALID, "null buffer");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -465,16 +470,18 @@ int frq_dev_gemm_q4_k_bf16(const void* w, size_t w_bytes, const uint16_t* x, flo
         return FRQ_OK;
     }
     if (!w || !x) return fail(FRQ_ERR_INVALID, "null buffer");
-    if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15) != 0)
-        return fail(FRQ_ERR_ALIGN, "weight and x must be 16-byte aligned");
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
+    if ((qtype == FRQ_Q4_K ? (wa & 15) : (wa & 1)) || (reinterpret_cast<uintptr_t>(x) & 15))
+        return fail(FRQ_ERR_ALIGN, "%s gemm: weight or x misaligned", f.name);
     if (reinterpret_cast<uintptr_t>(y) & 3) return fail(FRQ_ERR_ALIGN, "y must be 4-byte aligned");
-    FRQ_HIP(frq::launch_gemm_q4_k_bf16(static_cast<const uint8_t*>(w), x, y, m, n, k, s));
+    FRQ_HIP(frq::launch_gemm_bf16(qtype, static_cast<const uint8_t*>(w), x, y, m, n, k, s));
     return FRQ_OK;
 }
 
-int frq_gemm_q4_k_bf16(const uint16_t* x, const uint8_t* w, size_t w_bytes, int64_t m, int64_t n, int64_t k,
-                       float* y) {
-    if (int rc = gemm_checks(w, w_bytes, m, n, k)) return rc;
+int frq_gemm_bf16(int qtype, const uint16_t* x, const uint8_t* w, size_t w_bytes, int64_t m, int64_t n, int64_t k,
+                  float* y) {
+    Fmt f;
+    if (int rc = gemm_checks(qtype, w_bytes, m, n, k, &f)) return rc;
     if (m == 0 || n == 0) return FRQ_OK;
     if (!y || (k > 0 && (!x || !w))) return fail(FRQ_ERR_INVALID, "null buffer");
     if (k == 0) {
@@ -491,9 +498,19 @@ int frq_gemm_q4_k_bf16(const uint16_t* x, const uint8_t* w, size_t w_bytes, int6
     float* dy = reinterpret_cast<float*>(dw + wb + xb);
     FRQ_HIP(hipMemcpy(dw, w, w_bytes, hipMemcpyHostToDevice));
     FRQ_HIP(hipMemcpy(dx, x, (size_t)(m * k) * 2, hipMemcpyHostToDevice));
-    FRQ_HIP(frq::launch_gemm_q4_k_bf16(dw, dx, dy, m, n, k, nullptr));
+    FRQ_HIP(frq::launch_gemm_bf16(qtype, dw, dx, dy, m, n, k, nullptr));
     FRQ_HIP(hipMemcpy(y, dy, (size_t)(m * n) * 4, hipMemcpyDeviceToHost));
     return FRQ_OK;
+}
+
+int frq_dev_gemm_q4_k_bf16(const void* w, size_t w_bytes, const uint16_t* x, float* y, int64_t m, int64_t n,
+                           int64_t k, void* stream) {
+    return frq_dev_gemm_bf16(FRQ_Q4_K, w, w_bytes, x, y, m, n, k, stream);
+}
+
+int frq_gemm_q4_k_bf16(const uint16_t* x, const uint8_t* w, size_t w_bytes, int64_t m, int64_t n, int64_t k,
+                       float* y) {
+    return frq_gemm_bf16(FRQ_Q4_K, x, w, w_bytes, m, n, k, y);
 }
 
 int frq_dev_copy(void* dst, const void* src, size_t bytes, void* stream) {

@@ -1,13 +1,15 @@
-// Q4_K prefill GEMM on the gfx950 matrix cores:
-//   Y[M, N] (fp32) = X[M, K] (bf16) . W[N, K]^T, W = raw Q4_K blocks.
+// Prefill GEMM on the gfx950 matrix cores:
+//   Y[M, N] (fp32) = X[M, K] (bf16) . W[N, K]^T, W = raw Q4_K, Q6_K or Q8_0 blocks.
 //
 // The reference prefills by re-running the matvec for every token
-// (matmul_q4_k_batched, _C.cpp:154-197): W is dequantized M times and there
+// (matmul_<q>_batched, _C.cpp:154-283): W is dequantized M times and there
 // is no reuse. Here W is dequantized once per output tile into LDS as bf16
-// and multiplied with v_mfma_f32_32x32x16_bf16 (fp32 accumulation).
+// and multiplied with v_mfma_f32_32x32x16_bf16 (fp32 accumulation). The
+// kernel is one template; only the W staging (which raw bytes a thread
+// loads, and how it turns them into 16 bf16 weights) depends on the format.
 //
-// Precision contract: W values are the exact fp32 dequant (d*sc*q - dmin*m,
-// the same arithmetic as the dequant kernels) rounded to bf16 (nearest even);
+// Precision contract: W values are the exact fp32 dequant (the same
+// arithmetic as the dequant kernels) rounded to bf16 (nearest even);
 // X is taken as given in bf16; products and sums are fp32. The result equals
 // fp64 X . bf16(W)^T to fp32 accumulation error.
 //
@@ -17,7 +19,7 @@
 // 32 x 32, 64 fp32 accumulators per lane; while one wave of a SIMD dequantizes
 // or waits on LDS the other issues MFMAs. Each K-step:
 //   * X tile [256][64] bf16 and the W tile [128][64] (dequantized by the
-//     workgroup, a quarter group of 8 qs bytes per thread) go to LDS, double
+//     workgroup, 16 weights of one row per thread) go to LDS, double
 //     buffered; global loads run two steps ahead (two register staging
 //     sets), and each step's dequant + LDS writes for step t+1 follow its
 //     MFMAs, so the arithmetic runs while the matrix cores work.
@@ -49,7 +51,121 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
-__global__ void __launch_bounds__(512) gemm_q4_k_bf16_kernel(const uint8_t* __restrict__ w,
+// W staging per format. A K-step is 64 consecutive k of 128 rows; thread
+// (row wr, quarter wq) stages 16 weights of row wr. load() issues the global
+// reads for step `kb` (first k of the step), store() dequantizes them (same
+// rounding sequence as the format's dequant kernel) into bf16 LDS row `dst`.
+template <int QT>
+struct WFmt;
+
+// Q4_K: the step is one 32-byte qs group g; the quarter wq owns qs bytes
+// 8wq .. 8wq+7, whose low nibbles are k = 8wq + i (sub-block 2g) and high
+// nibbles k = 32 + 8wq + i (sub-block 2g + 1) (gguf.py:209-219).
+template <>
+struct WFmt<kTypeQ4K> {
+    static constexpr int kBytes = kQ4KBytes, kElems = kQKElems;
+    struct Raw {
+        u32x4 h;
+        u32x2 q;
+    };
+    __device__ static void load(Raw& r, const uint8_t* wrow, int kb, int wq) {
+        const uint8_t* bp = wrow + (int64_t)(kb >> 8) * kQ4KBytes;
+        r.h = *reinterpret_cast<const u32x4*>(bp);
+        r.q = *reinterpret_cast<const u32x2*>(bp + 16 + 32 * ((kb >> 6) & 3) + 8 * wq);
+    }
+    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq) {
+        const int g = (kb >> 6) & 3;
+        uint32_t sc0, mn0, sc1, mn1;
+        k4_scale_min(r.h[1], r.h[2], r.h[3], 2 * g, sc0, mn0);
+        k4_scale_min(r.h[1], r.h[2], r.h[3], 2 * g + 1, sc1, mn1);
+        const float d = f16_bits_to_f32(r.h[0]), dmin = f16_bits_to_f32(r.h[0] >> 16);
+        const float s0 = d * (float)sc0, t0 = dmin * (float)mn0;
+        const float s1 = d * (float)sc1, t1 = dmin * (float)mn1;
+        const uint32_t qw[2] = {r.q[0], r.q[1]};
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t v = qw[p >> 1] >> (16 * (p & 1));   // bytes 2p, 2p+1 of the quarter
+            lo[p] = pack_bf16(s0 * (float)(v & 15u) - t0, s0 * (float)((v >> 8) & 15u) - t0);
+            hi[p] = pack_bf16(s1 * (float)((v >> 4) & 15u) - t1, s1 * (float)((v >> 12) & 15u) - t1);
+        }
+        *reinterpret_cast<u32x4*>(dst + 8 * wq) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<u32x4*>(dst + 32 + 8 * wq) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    }
+};
+
+// Q8_0: the step is two 34-byte blocks; quarter wq owns elements
+// 16 (wq & 1) .. +15 of block wq >> 1, i.e. k = 16 wq + i: y = fl(q * d).
+template <>
+struct WFmt<kTypeQ80> {
+    static constexpr int kBytes = kQ80Bytes, kElems = kQ80Elems;
+    struct Raw {
+        uint32_t d;
+        uint32_t q[4];
+    };
+    __device__ static void load(Raw& r, const uint8_t* wrow, int kb, int wq) {
+        const uint8_t* bp = wrow + (int64_t)((kb >> 5) + (wq >> 1)) * kQ80Bytes;
+        r.d = ld_u16(bp);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.q[i] = ld_u32_a2(bp + 2 + 16 * (wq & 1) + 4 * i);
+    }
+    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq) {
+        (void)kb;
+        const float d = f16_bits_to_f32(r.d);
+        uint32_t o[8];
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const uint32_t v = r.q[p >> 1] >> (16 * (p & 1));
+            o[p] = pack_bf16((float)(int)(int8_t)(v & 0xFFu) * d, (float)(int)(int8_t)((v >> 8) & 0xFFu) * d);
+        }
+        *reinterpret_cast<u32x4*>(dst + 16 * wq) = u32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<u32x4*>(dst + 16 * wq + 8) = u32x4{o[4], o[5], o[6], o[7]};
+    }
+};
+
+// Q6_K: the step is 64 k of one half h of a block: elements 128h + 32ks + l
+// for ks = 2kp, 2kp+1 (kp = which 64 of the half). Quarter wq takes
+// ks = 2kp + (wq >> 1) and l = 16 (wq & 1) .. +15, i.e. k = 16 wq + i:
+// q = nibble of ql[64h + 32 (ks & 1) + l] (high nibble for ks >= 2) | bits
+// 2ks, 2ks+1 of qh[32h + l] << 4; y = fl(fl(d * sc[8h + l/16 + 2ks]) * (q - 32))
+// (gguf.py:401-419). Fields are only 2-byte aligned (210-byte blocks).
+template <>
+struct WFmt<kTypeQ6K> {
+    static constexpr int kBytes = kQ6KBytes, kElems = kQKElems;
+    struct Raw {
+        uint32_t ql[4], qh[4];
+        uint32_t sc, d;
+    };
+    __device__ static void load(Raw& r, const uint8_t* wrow, int kb, int wq) {
+        const uint8_t* bp = wrow + (int64_t)(kb >> 8) * kQ6KBytes;
+        const int kt4 = (kb & 255) >> 6, h = kt4 >> 1, ks = 2 * (kt4 & 1) + (wq >> 1), l0 = 16 * (wq & 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r.ql[i] = ld_u32_a2(bp + 64 * h + 32 * (ks & 1) + l0 + 4 * i);
+            r.qh[i] = ld_u32_a2(bp + 128 + 32 * h + l0 + 4 * i);
+        }
+        r.sc = bp[192 + 8 * h + (wq & 1) + 2 * ks];
+        r.d = ld_u16(bp + 208);
+    }
+    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq) {
+        const int kt4 = (kb & 255) >> 6, ks = 2 * (kt4 & 1) + (wq >> 1);
+        const float s = f16_bits_to_f32(r.d) * (float)(int)(int8_t)(r.sc & 0xFFu);
+        uint32_t o[8];
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const int i = p >> 1;
+            const uint32_t nib = (ks >= 2 ? (r.ql[i] >> 4) : r.ql[i]) & 0x0F0F0F0Fu;
+            const uint32_t q = nib | (((r.qh[i] >> (2 * ks)) & 0x03030303u) << 4);
+            const uint32_t v = q >> (16 * (p & 1));
+            o[p] = pack_bf16(s * (float)((int)(v & 0xFFu) - 32), s * (float)((int)((v >> 8) & 0xFFu) - 32));
+        }
+        *reinterpret_cast<u32x4*>(dst + 16 * wq) = u32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<u32x4*>(dst + 16 * wq + 8) = u32x4{o[4], o[5], o[6], o[7]};
+    }
+};
+
+template <int QT>
+__global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restrict__ w,
                                                              const uint16_t* __restrict__ x,
                                                              float* __restrict__ y, int M, int N, int K) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[2][kBM * kLds];
@@ -61,7 +177,8 @@ __global__ void __launch_bounds__(512) gemm_q4_k_bf16_kernel(const uint8_t* __re
     // (2 MB at M-tile 256, K 4096), which then stays in that XCD's L2.
     const int mtiles = (M + kBM - 1) / kBM;
     const int n0 = (int)(blockIdx.x / mtiles) * kBN, m0 = (int)(blockIdx.x % mtiles) * kBM;
-    const int64_t row_bytes = (int64_t)(K / kQKElems) * kQ4KBytes;
+    using F = WFmt<QT>;
+    const int64_t row_bytes = (int64_t)(K / F::kElems) * F::kBytes;
     const int ksteps = K / kBK;
 
     // X staging: 8 threads per row (16 B each), rows xr + 64 j.
@@ -72,8 +189,7 @@ __global__ void __launch_bounds__(512) gemm_q4_k_bf16_kernel(const uint8_t* __re
 
     struct Stage {
         u32x4 x[4];
-        u32x4 h;
-        u32x2 q;
+        typename F::Raw w;
     };
     Stage st[2];
     auto load_tile = [&](Stage& sg, int kt) __attribute__((always_inline)) {
@@ -83,35 +199,14 @@ __global__ void __launch_bounds__(512) gemm_q4_k_bf16_kernel(const uint8_t* __re
             const int r = m0 + xr + 64 * j;
             sg.x[j] = *reinterpret_cast<const u32x4*>(x + (int64_t)(r < M ? r : M - 1) * K + kb + 8 * xc);
         });
-        const uint8_t* bp = wrow + (int64_t)(kb >> 8) * kQ4KBytes;
-        sg.h = *reinterpret_cast<const u32x4*>(bp);
-        sg.q = *reinterpret_cast<const u32x2*>(bp + 16 + 32 * ((kb >> 6) & 3) + 8 * wq);
+        F::load(sg.w, wrow, kb, wq);
     };
     auto store_tile = [&](const Stage& sg, int buf, int kt) __attribute__((always_inline)) {
         static_for<0, 4>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             *reinterpret_cast<u32x4*>(&xs[buf][(xr + 64 * j) * kLds + 8 * xc]) = sg.x[j];
         });
-        const int g = ((kt * kBK) >> 6) & 3;
-        uint32_t sc0, mn0, sc1, mn1;
-        k4_scale_min(sg.h[1], sg.h[2], sg.h[3], 2 * g, sc0, mn0);
-        k4_scale_min(sg.h[1], sg.h[2], sg.h[3], 2 * g + 1, sc1, mn1);
-        const float d = f16_bits_to_f32(sg.h[0]), dmin = f16_bits_to_f32(sg.h[0] >> 16);
-        const float s0 = d * (float)sc0, t0 = dmin * (float)mn0;
-        const float s1 = d * (float)sc1, t1 = dmin * (float)mn1;
-        const uint32_t qw[2] = {sg.q[0], sg.q[1]};
-        uint32_t lo[4], hi[4];
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const uint32_t v = qw[p >> 1] >> (16 * (p & 1));   // bytes 2p, 2p+1 of the quarter
-            // same arithmetic as the dequant kernels: fl(fl(s * q) - t)
-            lo[p] = pack_bf16(s0 * (float)(v & 15u) - t0, s0 * (float)((v >> 8) & 15u) - t0);
-            hi[p] = pack_bf16(s1 * (float)((v >> 4) & 15u) - t1, s1 * (float)((v >> 12) & 15u) - t1);
-        }
-        // low nibbles -> k 8 wq + i (sub-block 2g), high -> 32 + 8 wq + i (2g + 1)
-        uint16_t* dst = &ws[buf][wr * kLds];
-        *reinterpret_cast<u32x4*>(dst + 8 * wq) = u32x4{lo[0], lo[1], lo[2], lo[3]};
-        *reinterpret_cast<u32x4*>(dst + 32 + 8 * wq) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+        F::store(sg.w, &ws[buf][wr * kLds], kt * kBK, wq);
     };
 
     f32x16 acc[2][2];
@@ -143,9 +238,10 @@ __global__ void __launch_bounds__(512) gemm_q4_k_bf16_kernel(const uint8_t* __re
 
     // Global loads run two K-steps ahead of the MFMAs: the loads for step
     // t + 2 are issued at step t (staging set t % 2) and reach LDS at the end
-    // of step t + 1. The loop is unrolled by two (the step count K/64 is a
-    // multiple of 4) so the staging set of every step is a compile-time
-    // choice, and loads and LDS writes are unconditional -- past the last
+    // of step t + 1. The loop is unrolled by two so the staging set of every
+    // step is a compile-time
+    // choice (K is a multiple of 128, so the count is even), and loads and
+    // LDS writes are unconditional -- past the last
     // step they repeat it into the buffer nothing reads again -- so the
     // compiler's wait before each LDS write covers one staging set only.
     const int last = ksteps - 1;
@@ -179,16 +275,23 @@ __global__ void __launch_bounds__(512) gemm_q4_k_bf16_kernel(const uint8_t* __re
 
 }  // namespace
 
-bool gemm_q4_k_bf16_supported(int64_t m, int64_t n, int64_t k) {
-    return m > 0 && n > 0 && k > 0 && k % kQKElems == 0 && m <= 0x7FFFFFFF && n <= 0x7FFFFFFF &&
+bool gemm_bf16_supported(int qtype, int64_t m, int64_t n, int64_t k) {
+    // K-steps of 64 must come in pairs (the pipeline is unrolled by two)
+    const int64_t kq = qtype == kTypeQ80 ? 128 : (qtype == kTypeQ4K || qtype == kTypeQ6K) ? kQKElems : 0;
+    return kq > 0 && m > 0 && n > 0 && k > 0 && k % kq == 0 && m <= 0x7FFFFFFF && n <= 0x7FFFFFFF &&
            k <= 0x7FFFFFFF && ((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM) <= 0x7FFFFFFF;
 }
 
-hipError_t launch_gemm_q4_k_bf16(const uint8_t* w, const uint16_t* x, float* y, int64_t m, int64_t n, int64_t k,
-                                 hipStream_t stream) {
-    if (!gemm_q4_k_bf16_supported(m, n, k)) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM)));
-    gemm_q4_k_bf16_kernel<<<grid, dim3(512), 0, stream>>>(w, x, y, (int)m, (int)n, (int)k);
+hipError_t launch_gemm_bf16(int qtype, const uint8_t* w, const uint16_t* x, float* y, int64_t m, int64_t n, int64_t k,
+                            hipStream_t stream) {
+    if (!gemm_bf16_supported(qtype, m, n, k)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM))), block(512);
+    switch (qtype) {
+        case kTypeQ4K: gemm_bf16_kernel<kTypeQ4K><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k); break;
+        case kTypeQ6K: gemm_bf16_kernel<kTypeQ6K><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k); break;
+        case kTypeQ80: gemm_bf16_kernel<kTypeQ80><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

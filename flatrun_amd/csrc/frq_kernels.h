@@ -72,11 +72,12 @@ void gemv_sk_scratch(const SplitKPlan& plan, int64_t n, size_t* partial_bytes, s
 hipError_t launch_gemv_sk(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k,
                           const SplitKPlan& plan, float* partials, uint32_t* counters, hipStream_t stream);
 
-// Q4_K prefill GEMM on the matrix cores (frq_gemm.hip): y[m, n] = x[m, k] (bf16
-// bits, row-major) . W[n, k]^T (raw Q4_K blocks) with W rounded to bf16 and
-// fp32 accumulation. w and x 16-byte aligned, k a multiple of 256.
-bool gemm_q4_k_bf16_supported(int64_t m, int64_t n, int64_t k);
-hipError_t launch_gemm_q4_k_bf16(const uint8_t* w, const uint16_t* x, float* y, int64_t m, int64_t n, int64_t k,
-                                 hipStream_t stream);
+// Prefill GEMM on the matrix cores (frq_gemm.hip): y[m, n] = x[m, k] (bf16
+// bits, row-major) . W[n, k]^T (raw Q4_K, Q6_K or Q8_0 blocks) with W rounded
+// to bf16 and fp32 accumulation. x 16-byte aligned; w 16-byte aligned for
+// Q4_K, 2-byte for the others; k a multiple of 256 (Q4_K, Q6_K) or 128 (Q8_0).
+bool gemm_bf16_supported(int qtype, int64_t m, int64_t n, int64_t k);
+hipError_t launch_gemm_bf16(int qtype, const uint8_t* w, const uint16_t* x, float* y, int64_t m, int64_t n, int64_t k,
+                            hipStream_t stream);
 
 }  // namespace frq

@@ -265,12 +265,16 @@ def gemv_tuned(qtype, w, x, y, n: int, k: int, kernel: int = 0, cpl: int = 0, ro
     return cfg.as_dict()
 
 
-def gemm_q4k_bf16(w, x_bf16, y, m: int, n: int, k: int, stream=None, w_bytes: int | None = None) -> None:
-    """y[m, n] = x[m, k] . W[n, k]^T on the matrix cores (x: bf16 bits, row-major;
-    y: fp32). Enqueued, not synchronised."""
+def gemm_bf16(qtype, w, x_bf16, y, m: int, n: int, k: int, stream=None, w_bytes: int | None = None) -> None:
+    """y[m, n] = x[m, k] . W[n, k]^T on the matrix cores (W: Q4_K, Q6_K or Q8_0
+    blocks; x: bf16 bits, row-major; y: fp32). Enqueued, not synchronised."""
     wb = _nbytes(w) if w_bytes is None else int(w_bytes)
-    check(lib().frq_dev_gemm_q4_k_bf16(_addr(w), wb, _addr(x_bf16), _addr(y), int(m), int(n), int(k),
-                                       _stream(stream)))
+    check(lib().frq_dev_gemm_bf16(qtype_id(qtype), _addr(w), wb, _addr(x_bf16), _addr(y), int(m), int(n), int(k),
+                                  _stream(stream)))
+
+
+def gemm_q4k_bf16(w, x_bf16, y, m: int, n: int, k: int, stream=None, w_bytes: int | None = None) -> None:
+    gemm_bf16("Q4_K", w, x_bf16, y, m, n, k, stream=stream, w_bytes=w_bytes)
 
 
 def memcpy_h2d_async(dst, src_host_ptr: int, nbytes: int, stream=None) -> None:

@@ -169,6 +169,14 @@ int frq_dev_gemm_q4_k_bf16(const void* w, size_t w_bytes, const uint16_t* x_bf16
 /* Same with host buffers (copied to the device and back on every call). */
 int frq_gemm_q4_k_bf16(const uint16_t* x_bf16, const uint8_t* w, size_t w_bytes, int64_t m, int64_t n, int64_t k,
                        float* y);
+/* The same GEMM for any of Q4_K, Q6_K, Q8_0 (qtype); k a multiple of 256
+ * (Q4_K, Q6_K) or 128 (Q8_0); w 16-byte aligned (Q4_K) or 2-byte aligned.
+ * Replaces, for bf16 activations, matmul_q6_k_batched (_C.cpp:244-283) and
+ * matmul_q8_0_batched (_C.cpp:199-242) as well. */
+int frq_dev_gemm_bf16(int qtype, const void* w, size_t w_bytes, const uint16_t* x_bf16, float* y, int64_t m,
+                      int64_t n, int64_t k, void* stream);
+int frq_gemm_bf16(int qtype, const uint16_t* x_bf16, const uint8_t* w, size_t w_bytes, int64_t m, int64_t n,
+                  int64_t k, float* y);
 
 /* dst = src on the device with a plain 16-byte-per-lane streaming kernel:
  * the reference point for calibrating HBM traffic counters (bytes a

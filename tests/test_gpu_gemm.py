@@ -1,4 +1,5 @@
-"""Q4_K prefill GEMM on the matrix cores (bf16 MFMA) against the oracle.
+"""Prefill GEMM on the matrix cores (bf16 MFMA), Q4_K / Q6_K / Q8_0 weights,
+against the oracle.
 
 Contract (written here, checked below):
   * against fp64 X . bf16(W)^T, with W the exact fp32 dequant (oracle) rounded
@@ -30,19 +31,19 @@ def bf16_round(a: np.ndarray) -> np.ndarray:
     return r.view(np.float32)
 
 
-def make_case(m, n, k, seed):
-    raw = synth.make_blocks("Q4_K", n, k, seed=seed)
+def make_case(m, n, k, seed, q="Q4_K"):
+    raw = synth.make_blocks(q, n, k, seed=seed)
     x = np.random.default_rng(seed + 1).standard_normal((m, k)).astype(np.float32)
     return raw, bf16_round(x)
 
 
-def check(y, raw, xb, n, k):
-    w = G.dequant_q4_k(raw, (n, k)).astype(np.float32)
+def check(y, raw, xb, n, k, q="Q4_K"):
+    w = G.DEQUANT[q](raw, (n, k)).astype(np.float32)
     wb = bf16_round(w).astype(np.float64)
     x64 = xb.astype(np.float64)
     ref = x64 @ wb.T
     absw = np.abs(x64) @ np.abs(wb).T
-    assert_matvec_close(y.reshape(-1), ref.reshape(-1), absw.reshape(-1), what=f"gemm {xb.shape[0]}x{n}x{k} vs bf16(W)")
+    assert_matvec_close(y.reshape(-1), ref.reshape(-1), absw.reshape(-1), what=f"{q} gemm {xb.shape[0]}x{n}x{k} vs bf16(W)")
     exact = x64 @ w.astype(np.float64).T
     err = np.max(np.abs(y - exact)) / np.max(np.abs(exact))
     assert err <= BF16_W_RTOL, f"gemm vs exact W: normwise {err:.3e} > {BF16_W_RTOL}"
@@ -55,6 +56,37 @@ def test_gemm_shapes(frq, m, n, k):
     y = _C.matmul_q4_k_bf16(xb, raw, n, k)
     assert y.shape == (m, n) and y.dtype == np.float32
     check(y, raw, xb, n, k)
+
+
+@pytest.mark.parametrize("q", ["Q6_K", "Q8_0"])
+@pytest.mark.parametrize("m,n,k", [(1, 1, 256), (5, 37, 512), (300, 200, 1024), (513, 130, 768), (64, 1000, 4096)])
+def test_gemm_other_formats(frq, q, m, n, k):
+    raw, xb = make_case(m, n, k, seed=m + 2 * n + k, q=q)
+    y = _C.matmul_bf16(q, xb, raw, n, k)
+    assert y.shape == (m, n)
+    check(y, raw, xb, n, k, q=q)
+
+
+def test_gemm_q8_0_k_multiple_of_128(frq):
+    m, n, k = 9, 33, 128 * 3
+    raw, xb = make_case(m, n, k, seed=3, q="Q8_0")
+    check(_C.matmul_q8_0_bf16(xb, raw, n, k), raw, xb, n, k, q="Q8_0")
+    with pytest.raises(RuntimeError):
+        _C.matmul_q8_0_bf16(np.zeros((2, 320), np.float32), np.zeros(33 * 10 * 34, np.uint8), 33, 320)
+
+
+def test_gemm_llama_down_q6_k(frq):
+    """Llama-3-8B prefill down projection: Y[512 x 4096] = X[512 x 14336] . W^T, W Q6_K."""
+    m, n, k = 512, 4096, 14336
+    raw, xb = make_case(m, n, k, seed=12, q="Q6_K")
+    check(_C.matmul_q6_k_bf16(xb, raw, n, k), raw, xb, n, k, q="Q6_K")
+
+
+def test_gemm_resident_weight_q6_k(frq):
+    m, n, k = 17, 96, 512
+    raw, xb = make_case(m, n, k, seed=19, q="Q6_K")
+    nb = NativeBackend()
+    assert bits_equal(nb.matmul_q6k_bf16(xb, nb.upload(raw), n, k), nb.matmul_q6k_bf16(xb, raw, n, k))
 
 
 def test_gemm_prefill_config(frq):
