@@ -41,6 +41,30 @@ constexpr int kQ4KBytes = 144, kQ5KBytes = 176, kQ6KBytes = 210, kQKElems = 256;
 constexpr int kQ10Bytes = 18, kQ10Elems = 128;
 constexpr int kQ40Bytes = 18, kQ50Bytes = 22, kQ51Bytes = 24;   // 32 elements each
 
+// Raw (untyped) buffer descriptor over [base, base + bytes). Loads through it
+// take a 32-bit VGPR byte offset against a base held in scalar registers, so
+// a lane pays no 64-bit address arithmetic, and an access past `bytes` reads
+// zeros instead of touching memory. Word 3 is the gfx9-family raw-access
+// setting (32-bit data format, no swizzle, no index).
+constexpr int kBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferWord3);
+}
+__device__ __forceinline__ uint4 bload_b128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void bload_b96(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t (&wv)[3]) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, (int)off, 0, 0);
+    wv[0] = v[0];
+    wv[1] = v[1];
+    wv[2] = v[2];
+}
+__device__ __forceinline__ uint32_t bload_u16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
 // IEEE binary16 -> binary32. v_cvt_f32_f16 is exact for every finite input,
 // subnormals included (f16 denormals are enabled in the default FP mode).
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
@@ -95,7 +119,11 @@ __device__ __forceinline__ uint32_t vand_or(uint32_t a, uint32_t mask, uint32_t 
 // conversions issue back to back and the FMAs that consume them come later;
 // left to itself the compiler pairs every conversion with its FMA, and the
 // FMA then waits on the conversion it follows.
-__device__ __forceinline__ void nibbles8(uint32_t w, float (&f)[8]) {
+// Masks come in registers: kernels that give each lane its own plane order
+// (see the Q4_K GEMV) pass per-lane masks, f[0..3] then being the lane's
+// "own" plane.
+__device__ __forceinline__ void nibbles8(uint32_t w, float (&f)[8], uint32_t mask_a = 0x0F0F0F0Fu,
+                                         uint32_t mask_b = 0xF0F0F0F0u) {
     uint32_t lo, hi;
     asm("v_and_b32 %0, %10, %12\n\t"
         "v_and_b32 %1, %11, %12\n\t"
@@ -109,7 +137,7 @@ __device__ __forceinline__ void nibbles8(uint32_t w, float (&f)[8]) {
         "v_cvt_f32_ubyte3 %9, %1"
         : "=&v"(lo), "=&v"(hi), "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]),
           "=&v"(f[6]), "=&v"(f[7])
-        : "s"(0x0F0F0F0Fu), "s"(0xF0F0F0F0u), "v"(w));
+        : "v"(mask_a), "v"(mask_b), "v"(w));
 }
 
 // Byte b of w as float: one v_cvt_f32_ubyte<b>.
@@ -121,9 +149,12 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
 
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
 // Four DPP steps reduce each 16-lane row, two cross-row swizzles finish.
+// Only for controls that give every lane a source inside its row (quad_perm,
+// row_half_mirror, row_mirror): the old value is never used, so it is left
+// undefined and the compiler folds the move into the add that consumes it.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
 template <int CTRL, int ROW_MASK>
@@ -143,6 +174,18 @@ __device__ __forceinline__ float wave_sum_lane63(float v) {
     v += dpp_mov<0x140>(v);          // row_mirror: every lane holds its row's sum
     v = dpp_add<0x142, 0xA>(v, v);   // row_bcast:15 -> rows 1, 3 add rows 0, 2
     v = dpp_add<0x143, 0xC>(v, v);   // row_bcast:31 -> rows 2, 3 add lane 31
+    return v;
+}
+
+// The four in-row DPP steps of wave_sum_lane63: every lane ends with the sum
+// of its 16-lane DPP row. Callers park the four row sums (lanes 15, 31, 47,
+// 63) in LDS and add them with the other waves' in a fixed order, which
+// saves the two row_bcast steps and their zeroed operands per reduction.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);  // row_half_mirror
+    v += dpp_mov<0x140>(v);  // row_mirror
     return v;
 }
 
@@ -188,6 +231,30 @@ struct ScaleDecode {
         sc1 = __builtin_amdgcn_ubfe(a_sc, o_sc + 8, w_a) | (__builtin_amdgcn_ubfe(s0, o_b + 8, w_b) << 4);
         m0 = __builtin_amdgcn_ubfe(a_m, o_m, w_a) | (__builtin_amdgcn_ubfe(s1, o_b, w_b) << 4);
         m1 = __builtin_amdgcn_ubfe(a_m, o_m + 8, w_a) | (__builtin_amdgcn_ubfe(s1, o_b + 8, w_b) << 4);
+    }
+};
+
+// One (scale, min) pair j of a K-quant block per lane (same fields as
+// k4_scale_min): lanes that share a block decode one pair each and read the
+// others' with DPP instead of all decoding every pair they use.
+struct PairDecode {
+    bool hi;                          // j >= 4: low bits come from s2
+    uint32_t o_sc, o_m, w_a, o_b, w_b;
+
+    __device__ __forceinline__ explicit PairDecode(int j) {
+        hi = j >= 4;
+        const uint32_t b = hi ? 8u * (uint32_t)(j - 4) : 8u * (uint32_t)j;
+        o_sc = b;
+        o_m = hi ? b + 4 : b;
+        w_a = hi ? 4 : 6;
+        o_b = hi ? b + 6 : 0;
+        w_b = hi ? 2 : 0;
+    }
+    __device__ __forceinline__ void operator()(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc,
+                                               uint32_t& m) const {
+        const uint32_t a_sc = hi ? s2 : s0, a_m = hi ? s2 : s1;
+        sc = __builtin_amdgcn_ubfe(a_sc, o_sc, w_a) | (__builtin_amdgcn_ubfe(s0, o_b, w_b) << 4);
+        m = __builtin_amdgcn_ubfe(a_m, o_m, w_a) | (__builtin_amdgcn_ubfe(s1, o_b, w_b) << 4);
     }
 };
 

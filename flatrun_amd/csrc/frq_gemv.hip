@@ -83,8 +83,9 @@ __device__ __forceinline__ void finish_rows(int64_t row0, int64_t row_end, float
 // every workgroup runs exactly R rows (a skip path would merge a different
 // count of outstanding loads into the next row and make its wait drain the
 // queue); the last workgroup's rows past n re-read row n-1 and are dropped.
-// Each row's lane partials are reduced with DPP only; results collect in LDS
-// and y is written once at the end.
+// Each row's lane partials are reduced over 16-lane DPP rows; the four row
+// sums per wave collect in LDS and are added in a fixed order when y is
+// written once at the end.
 //
 // S = 2 splits every row in two halves of its blocks, one workgroup each, so
 // a long row (74 blocks at k = 18944) runs as two 5-wave workgroups instead of
@@ -95,14 +96,14 @@ __device__ __forceinline__ void finish_rows(int64_t row0, int64_t row_end, float
 // half's sums with system-scope loads (past the L2), writes y = a + b (the
 // same bits in either order) and returns the counter to zero.
 template <int CPL, int U, int R, int S = 1>
-__global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_waves_per_eu(CPL == 1 ? 5 : 1))) gemv_q4_k_kernel(const uint8_t* __restrict__ w,
+__global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_waves_per_eu((CPL == 1 && U <= 3) ? 5 : 1))) gemv_q4_k_kernel(const uint8_t* __restrict__ w,
                                                                          const float* __restrict__ x,
                                                                          float* __restrict__ y, int64_t n,
                                                                          int nb, float* __restrict__ part,
                                                                          uint32_t* __restrict__ cnt) {
     static_assert(U <= R, "ring deeper than the row count");
     static_assert(S == 1 || S == 2, "one or two slices");
-    __shared__ float red[R * 16];
+    __shared__ float red[R * 64];                           // [row][wave][DPP row]
     constexpr int LPB = 8 / CPL;
     constexpr int NE = 16 * CPL;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
@@ -116,31 +117,48 @@ __global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_w
     const int g = (CPL == 2) ? sub : (sub >> 1);
     const int hh = (CPL == 2) ? 0 : (sub & 1);
     const ScaleDecode dec(g);
+    // CPL = 1, plane ownership. The two lanes of group g (hh = 0, 1) are DPP
+    // neighbours and read the same 32 qs bytes' halves; lane hh "owns" scale
+    // pair 2g + hh: its nibble plane A is the low nibbles (hh = 0) or the high
+    // nibbles (hh = 1), with A's x loaded to match, and plane B is the other.
+    // Each lane decodes only its own pair (pre-divided by 16 for the high
+    // nibbles, which enter as 16 q), adds its neighbour's plane-B dot (which
+    // belongs to this lane's pair) with one DPP add, and applies its own
+    // scale. The row sum over all lanes is unchanged.
+    const PairDecode pdec(sub);
+    const bool own_hi = CPL == 1 && hh;
+    const float hfac = own_hi ? 0.0625f : 1.0f;
+    const uint32_t mask_a = own_hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu, mask_b = ~mask_a;
 
     const int64_t row0 = rb * R;
     const int nrows = (int)(n - row0 < R ? n - row0 : R);
     const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
-    const uint8_t* wb = w + (int64_t)gblk * kQ4KBytes;
-    const int qoff = 16 + 32 * g + 16 * hh;
+    const uint32_t hoff = (uint32_t)gblk * kQ4KBytes;       // lane's block inside a row
+    const uint32_t qoff = hoff + 16 + 32 * g + 16 * hh;
 
     // Loads are unconditional (no control flow around them): rows past the
     // end re-read the last row (cache hits; results not stored), and inactive
-    // lanes read block 0 with x zeroed and their partial forced to 0.
+    // lanes read block 0 with x zeroed and their partial forced to 0. Each row
+    // is one buffer descriptor (wave-uniform, scalar registers) read at the
+    // lane's 32-bit offset: no VALU address math per row.
     auto load1 = [&](Q4KRow<CPL>& t, int j) {
-        const uint8_t* p = wb + (row0 + (j < nrows ? j : nrows - 1)) * row_bytes;
-        t.hd = *reinterpret_cast<const uint4*>(p);
+        const uint8_t* rp = w + (row0 + (j < nrows ? j : nrows - 1)) * row_bytes;
+        const auto rs = buffer_rsrc(rp, (uint32_t)row_bytes);
+        t.hd = bload_b128(rs, hoff);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) t.q[c] = *reinterpret_cast<const uint4*>(p + qoff + 16 * c);
+        for (int c = 0; c < CPL; ++c) t.q[c] = bload_b128(rs, qoff + 16 * c);
     };
 
-    float xl[NE], xh[NE];
+    float xl[NE], xh[NE];                                   // x of plane A, plane B
     float sxl = 0.0f, sxh = 0.0f;
     {
         const float* xb = x + (int64_t)gblk * kQKElems + 64 * g + 16 * hh;
+        const float* xa = xb + (own_hi ? 32 : 0);
+        const float* xo = xb + (own_hi ? 0 : 32);
 #pragma unroll
         for (int i = 0; i < NE; i += 4) {
-            const float4 a = *reinterpret_cast<const float4*>(xb + i);
-            const float4 c = *reinterpret_cast<const float4*>(xb + 32 + i);
+            const float4 a = *reinterpret_cast<const float4*>(xa + i);
+            const float4 c = *reinterpret_cast<const float4*>(xo + i);
             xl[i] = a.x; xl[i + 1] = a.y; xl[i + 2] = a.z; xl[i + 3] = a.w;
             xh[i] = c.x; xh[i + 1] = c.y; xh[i + 2] = c.z; xh[i + 3] = c.w;
         }
@@ -159,21 +177,27 @@ __global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_w
         sxl += xl[i];
         sxh += xh[i];
     }
+    // CPL = 1: sum of x over this lane's pair, both lanes' shares
+    const float sxt = sxl + dpp_mov<0xB1>(sxh);             // quad_perm [1,0,3,2]
 
     static_for<0, R>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         Q4KRow<CPL>& t = ring[j % U];
-        uint32_t sc0, m0, sc1, m1;
-        dec(t.hd.y, t.hd.z, t.hd.w, sc0, m0, sc1, m1);
+        // everything read from the slot is read before the slot is refilled
         const float d = f16_bits_to_f32(t.hd.x), dm = f16_bits_to_f32(t.hd.x >> 16);
+        uint32_t sc0 = 0, m0 = 0, sc1 = 0, m1 = 0;
+        if constexpr (CPL == 1)
+            pdec(t.hd.y, t.hd.z, t.hd.w, sc0, m0);          // this lane's pair 2g + hh
+        else
+            dec(t.hd.y, t.hd.z, t.hd.w, sc0, m0, sc1, m1);
         float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             const uint32_t qw[4] = {t.q[c].x, t.q[c].y, t.q[c].z, t.q[c].w};
 #pragma unroll
             for (int wd = 0; wd < 4; ++wd) {
-                float f[8];                                       // f[4..7] = 16 * high nibble
-                nibbles8(qw[wd], f);
+                float f[8];                                       // plane A, plane B
+                nibbles8(qw[wd], f, mask_a, mask_b);
                 const int e = 16 * c + 4 * wd;
                 a0 = __builtin_fmaf(f[0], xl[e + 0], a0);
                 a1 = __builtin_fmaf(f[1], xl[e + 1], a1);
@@ -186,29 +210,36 @@ __global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_w
             }
         }
         if constexpr (j + U < R) load1(t, j + U);               // refill the slot: row j + U
-        const float s0 = d * (float)sc0, t0 = dm * (float)m0;
-        const float s1 = (d * 0.0625f) * (float)sc1, t1 = dm * (float)m1;
-        float pu = s0 * (a0 + a1);
-        pu = __builtin_fmaf(-t0, sxl, pu);
-        pu = __builtin_fmaf(s1, b0 + b1, pu);
-        pu = __builtin_fmaf(-t1, sxh, pu);
+        float pu;
+        if constexpr (CPL == 1) {
+            const float so = (d * hfac) * (float)sc0, to = dm * (float)m0;
+            const float dot = (a0 + a1) + dpp_mov<0xB1>(b0 + b1);   // this lane's pair, both halves
+            pu = __builtin_fmaf(-to, sxt, so * dot);
+        } else {
+            const float s0 = d * (float)sc0, t0 = dm * (float)m0;
+            const float s1 = (d * 0.0625f) * (float)sc1, t1 = dm * (float)m1;
+            pu = s0 * (a0 + a1);
+            pu = __builtin_fmaf(-t0, sxl, pu);
+            pu = __builtin_fmaf(s1, b0 + b1, pu);
+            pu = __builtin_fmaf(-t1, sxh, pu);
+        }
         // results go to LDS (lgkmcnt): a global store would count in vmcnt
         // and force waits on the in-flight row loads.
-        const float v = wave_sum_lane63(active ? pu : 0.0f);
-        if (lane == 63) red[j * nwaves + wave] = v;
+        const float v = row16_sum(active ? pu : 0.0f);
+        if ((lane & 15) == 15) red[j * 4 * nwaves + 4 * wave + (lane >> 4)] = v;
     });
     __syncthreads();
     if constexpr (S == 1) {
         for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
             float s = 0.0f;
-            for (int w2 = 0; w2 < nwaves; ++w2) s += red[r * nwaves + w2];
+            for (int w2 = 0; w2 < 4 * nwaves; ++w2) s += red[r * 4 * nwaves + w2];
             y[row0 + r] = s;
         }
     } else {
         __shared__ uint32_t arrival;
         float s = 0.0f;
         if (tid < nrows) {
-            for (int w2 = 0; w2 < nwaves; ++w2) s += red[tid * nwaves + w2];
+            for (int w2 = 0; w2 < 4 * nwaves; ++w2) s += red[tid * 4 * nwaves + w2];
             __hip_atomic_store(part + (rb * 2 + slice) * R + tid, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
         __builtin_amdgcn_s_waitcnt(0);              // this thread's stores are acknowledged
@@ -460,7 +491,7 @@ __global__ void __launch_bounds__(1024) gemv_q6_k_ring_kernel(const uint8_t* __r
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, int64_t n, int nb) {
     static_assert(U <= R, "ring deeper than the row count");
-    __shared__ float red[R * 16];
+    __shared__ float red[R * 64];                           // [row][wave][DPP row]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
     const int blk_raw = tid >> 3, sub = tid & 7;
     const bool active = blk_raw < nb;
@@ -479,11 +510,12 @@ __global__ void __launch_bounds__(1024) gemv_q6_k_ring_kernel(const uint8_t* __r
 
     auto load1 = [&](Q6Row& t, int j) {
         const uint8_t* rp = w + (row0 + (j < nrows ? j : nrows - 1)) * row_bytes;
-        load_win3(rp + o_ql0, t.ql0);
-        load_win3(rp + o_ql1, t.ql1);
-        load_win3(rp + o_qh, t.qh);
-        load_win3(rp + o_sc, t.sc);
-        t.d = ld_u16(rp + o_d);
+        const auto rs = buffer_rsrc(rp, (uint32_t)row_bytes);
+        bload_b96(rs, o_ql0, t.ql0);
+        bload_b96(rs, o_ql1, t.ql1);
+        bload_b96(rs, o_qh, t.qh);
+        bload_b96(rs, o_sc, t.sc);
+        t.d = bload_u16(rs, o_d);
     };
 
     float xv[4][8];
@@ -548,13 +580,13 @@ __global__ void __launch_bounds__(1024) gemv_q6_k_ring_kernel(const uint8_t* __r
         }
         if constexpr (j + U < R) load1(t, j + U);
         __builtin_amdgcn_sched_barrier(0);                  // keep the rows in ring order
-        const float v = wave_sum_lane63(active ? pu : 0.0f);
-        if (lane == 63) red[j * nwaves + wave] = v;
+        const float v = row16_sum(active ? pu : 0.0f);
+        if ((lane & 15) == 15) red[j * 4 * nwaves + 4 * wave + (lane >> 4)] = v;
     });
     __syncthreads();
     for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
         float acc = 0.0f;
-        for (int w2 = 0; w2 < nwaves; ++w2) acc += red[r * nwaves + w2];
+        for (int w2 = 0; w2 < 4 * nwaves; ++w2) acc += red[r * 4 * nwaves + w2];
         y[row0 + r] = acc;
     }
 }
@@ -811,8 +843,7 @@ bool q4k_rows_ok(int r) {
 
 int q4k_ring(int cpl, int want) {
     if (cpl == 2) return want <= 3 ? 3 : 5;
-    (void)want;
-    return 3;
+    return want >= 6 ? 6 : want >= 4 ? 4 : 3;
 }
 
 // Rows per Q4_K workgroup (measured on MI355X, 256 CUs). Workgroups of 4 or
@@ -871,6 +902,10 @@ hipError_t launch_q4k(int cpl, int ring, int rows, int slices, int waves, int64_
                        : q4k_rows<2, 5, 1>(rows, gd, bd, s, w, x, y, n, nb, part, cnt);
     } else if (slices == 2) {
         ok = q4k_rows<1, 3, 2>(rows, gd, bd, s, w, x, y, n, nb, part, cnt);
+    } else if (ring == 6) {
+        ok = q4k_rows<1, 6, 1>(rows, gd, bd, s, w, x, y, n, nb, part, cnt);
+    } else if (ring == 4) {
+        ok = q4k_rows<1, 4, 1>(rows, gd, bd, s, w, x, y, n, nb, part, cnt);
     } else {
         ok = q4k_rows<1, 3, 1>(rows, gd, bd, s, w, x, y, n, nb, part, cnt);
     }
