@@ -21,8 +21,9 @@ Printed: ONE JSON line with
              from its sources, 1 thread) on the same bytes, timed on the host
              for a bounded number of full-shape repetitions; plus the NumPy path;
   configs    every other benchmark workload (GB/s, mean kernel us, fraction of
-             HBM peak) and the Llama-3-8B decode-step weight sweep (ms/step,
-             graph replay and eager).
+             HBM peak), the Llama-3-8B decode-step weight sweep (ms/step,
+             graph replay and eager; resident and streamed), the prefill
+             GEMM, the copy ceiling, and a GGUF file -> HBM load.
 """
 
 from __future__ import annotations
@@ -205,10 +206,57 @@ def run_suite(stream, steps: int, only: set | None = None) -> dict:
              ("llama3_8b_decode_streamed", lambda: decode_sweep_streamed(stream)),
              ("prefill_gemm_q4_k_bf16_512x14336x4096", lambda: prefill_gemm(stream)),
              ("copy_ceiling", lambda: copy_ceiling(stream)),
+             ("gguf_load_llama3_8b_4_layers", lambda: gguf_load(stream)),
              ("host_path_q4_k_3584x18944", host_path_rate)]
     for name, fn in extra:
         if want(name):
             out[name] = fn()
+    return out
+
+
+GGUF_PROJ = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate", "up": "ffn_up",
+             "down": "ffn_down"}
+
+
+def gguf_load(stream, layers: int = 4) -> dict:
+    """A synthetic Llama-3-8B-shaped GGUF file (``layers`` decoder layers, the
+    Q4_K_M projection mix, llama.cpp tensor names) written to a temporary
+    directory, then loaded by ResidentModel: parse + mmap + page cache ->
+    pinned -> HBM. The file was just written, so its pages are in the page
+    cache (a cold disk read would add the disk's own rate). One decode step
+    over the loaded tensors checks that they serve the GEMVs."""
+    import tempfile
+
+    from flatrun_amd import gguf
+
+    host = {name: synth.make_blocks(q, n, k, seed=i) for i, (name, q, n, k) in enumerate(LLAMA_LAYER)}
+    tensors = [(f"blk.{L}.{GGUF_PROJ[name]}.weight", (n, k), q, host[name].tobytes())
+               for L in range(layers) for name, q, n, k in LLAMA_LAYER]
+    with tempfile.TemporaryDirectory() as d:
+        path = Path(d) / "llama3_8b_layers.gguf"
+        gguf.write_gguf(path, tensors, {"general.architecture": "llama", "llama.block_count": layers})
+        t0 = time.perf_counter()
+        f = gguf.GGUFFile(path)
+        t_parse = time.perf_counter() - t0
+        m = gguf.ResidentModel(f, stream=stream)
+        kmax = max(k for *_, k in LLAMA_LAYER)
+        nmax = max(n for _, _, n, _ in LLAMA_LAYER)
+        x = device.DeviceBuffer.from_host(synth.make_x(kmax, seed=5))
+        y = device.DeviceBuffer(4 * nmax)
+        for L in range(layers):
+            for name, q, n, k in LLAMA_LAYER:
+                w = m[gguf.translate_gguf_name(f"blk.{L}.{GGUF_PROJ[name]}.weight")]
+                device.gemv(q, w, x, y, n, k, stream=stream, w_bytes=w.nbytes)
+        device.synchronize()
+        finite = bool(np.isfinite(y.to_host(np.float32)).all())
+        out = {"layers": layers, "bytes": m.nbytes, "parse_ms": round(t_parse * 1e3, 2),
+               "load_ms": round(m.load_seconds * 1e3, 1), "load_gbs": round(m.load_gbs, 2),
+               "decode_step_outputs_finite": finite,
+               "note": "warm page cache; staging 2 x 64 MiB pinned, 4 host copy threads"}
+        x.free()
+        y.free()
+        m.close()
+        f.close()
     return out
 
 

@@ -63,16 +63,33 @@ def is_neon() -> bool:
 
 
 class DeviceWeight:
-    """Raw GGUF block bytes resident in device memory (uploaded once)."""
+    """Raw GGUF block bytes resident in device memory.
+
+    ``DeviceWeight(raw)`` uploads a copy it owns; :meth:`view` names a byte
+    range of an existing device buffer (a tensor of a
+    :class:`flatrun_amd.gguf.ResidentModel` arena), which it keeps alive but
+    does not free. ``qtype``, ``shape`` and ``name`` describe the tensor when
+    known (None otherwise)."""
 
     def __init__(self, raw: np.ndarray):
         from .device import DeviceBuffer
         raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1)
         self.nbytes = int(raw.size)
         self.buffer = DeviceBuffer.from_host(raw)
+        self.offset = 0
+        self.qtype = self.shape = self.name = None
+
+    @classmethod
+    def view(cls, buffer, offset: int, nbytes: int, *, qtype=None, shape=None, name=None) -> "DeviceWeight":
+        if offset < 0 or nbytes < 0 or offset + nbytes > buffer.nbytes:
+            raise ValueError(f"view [{offset}, {offset + nbytes}) outside a {buffer.nbytes}-byte buffer")
+        w = cls.__new__(cls)
+        w.buffer, w.offset, w.nbytes = buffer, int(offset), int(nbytes)
+        w.qtype, w.shape, w.name = qtype, shape, name
+        return w
 
     def data_ptr(self) -> int:
-        return self.buffer.ptr
+        return self.buffer.ptr + self.offset
 
 
 def _raw_bytes(weight) -> np.ndarray:
@@ -145,7 +162,7 @@ class NativeBackend:
             base = self._scratch.ptr
             if x_c.size:
                 _lib.check(_lib.lib().frq_memcpy_h2d(base, x_c.ctypes.data, x_c.nbytes))
-            device.gemv(qname, weight.buffer, base, base + xb, n, k, batch=seq, w_bytes=weight.nbytes)
+            device.gemv(qname, weight, base, base + xb, n, k, batch=seq, w_bytes=weight.nbytes)
             _lib.check(_lib.lib().frq_memcpy_d2h(out.ctypes.data, base + xb, out.nbytes))
         return out[0] if x_c.ndim == 1 else out
 
@@ -154,6 +171,14 @@ class NativeBackend:
         ``weight`` to any matmul to skip the per-call weight copy."""
         self._require()
         return DeviceWeight(_raw_bytes(weight))
+
+    def load_gguf(self, path, names=None, **kw):
+        """Every (or the named) tensor of a GGUF file resident in HBM:
+        returns a :class:`flatrun_amd.gguf.ResidentModel`; ``model[name]`` is
+        a DeviceWeight to pass as ``weight`` to any matmul."""
+        self._require()
+        from .gguf import ResidentModel
+        return ResidentModel(path, names, **kw)
 
     # ------------------------------------------------------------ matmuls
     def matmul_q4k(self, x, weight, n: int, k: int):
