@@ -377,6 +377,26 @@ def decode_sweep_resident(stream, steps: int, layers: int = 32) -> dict:
             for name, q, n, k in LLAMA_LAYER:
                 device.gemv(q, dev[L][name], x, y, n, k, stream=stream, w_bytes=host[name].nbytes)
 
+    spec = {name: (q, n) for name, q, n, _ in LLAMA_LAYER}
+    ycat = device.DeviceBuffer(4 * (2 * 14336 + 6144))
+
+    def group(L, names, k):
+        parts, off = [], 0
+        for nm in names:
+            q, n = spec[nm]
+            parts.append((q, dev[L][nm], n, ycat.ptr + 4 * off, host[nm].nbytes))
+            off += n
+        return parts, k
+
+    groups = [[group(L, ("q", "k", "v"), 4096), group(L, ("o",), 4096), group(L, ("gate", "up"), 4096),
+               group(L, ("down",), 14336)] for L in range(layers)]
+
+    def step_fused():
+        # the forwarder's launch pattern with shared-x fusion: q|k|v, o, gate|up, down
+        for L in range(layers):
+            for parts, k in groups[L]:
+                device.gemv_group(parts, x, k, stream=stream)
+
     def timed(run) -> float:
         run()
         device.synchronize()
@@ -393,12 +413,22 @@ def decode_sweep_resident(stream, steps: int, layers: int = 32) -> dict:
         step()
     ms = timed(lambda: cap.launch(stream))
     cap.destroy()
+    with device.Graph.capture(stream) as capf:
+        step_fused()
+    ms_f = timed(lambda: capf.launch(stream))
+    capf.destroy()
+    fused_ok = all(device.gemv_group_fusable([(p[0], p[1]) for p in parts], k)
+                   for parts, k in groups[0] if len(parts) > 1)
+    ycat.free()
     for d in dev:
         for b in d.values():
             b.free()
     return {"ms_per_step": round(ms, 4), "ms_per_step_eager": round(ms_eager, 4), "weight_bytes_per_step": total,
             "gemvs_per_step": layers * len(LLAMA_LAYER), "gbs": round(total / (ms / 1e3) / 1e9, 1),
-            "floor_ms_at_8TBs": round(total / 8e12 * 1e3, 4)}
+            "floor_ms_at_8TBs": round(total / 8e12 * 1e3, 4),
+            "fused_shared_x": {"ms_per_step": round(ms_f, 4), "launches_per_step": layers * 4,
+                               "gbs": round(total / (ms_f / 1e3) / 1e9, 1), "groups_fused": fused_ok,
+                               "note": "q|k|v and gate|up as one grouped launch each"}}
 
 
 def main() -> int:

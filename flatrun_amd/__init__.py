@@ -196,6 +196,65 @@ class NativeBackend:
     # the runtime backend's spelling (runtime/backend.py:111, 273)
     matmul_q6k = matmul_q6_k
 
+    def matmul_fused(self, x, parts, k: int):
+        """Several projections of the same x, concatenated along the output:
+        ``parts`` = [(quant, weight, n), ...] (1..4 entries, quant a GGML type
+        name, weight raw bytes or a DeviceWeight) returns
+        ``np.concatenate([W_0 x, W_1 x, ...], axis=-1)`` -- what the
+        forwarder builds from separate matmul calls for q/k/v
+        (model/qwen2.py:1510-1519) and gate/up (:1690-1702) -- from one
+        launch per x row when every weight is Q4_K or Q6_K (see
+        frq_dev_gemv_group). x (k,) -> (sum n,), x (seq, k) -> (seq, sum n);
+        the values equal the separate calls' bit for bit."""
+        self._require()
+        from . import device
+        x_c = np.ascontiguousarray(x, dtype=np.float32)
+        if x_c.ndim == 1:
+            if x_c.shape[0] != k:
+                raise ValueError(f"x.shape[0]={x_c.shape[0]} != k={k}")
+            seq = 1
+        elif x_c.ndim == 2:
+            if x_c.shape[1] != k:
+                raise FrqError(_lib.ERR_SHAPE, "fused matmul (batched): x.shape[1] != k")
+            seq = x_c.shape[0]
+        else:
+            raise ValueError(f"x must be 1-D or 2-D, got shape {x_c.shape}")
+        if not 1 <= len(parts) <= device.GROUP_MAX:
+            raise ValueError(f"matmul_fused takes 1..{device.GROUP_MAX} parts, got {len(parts)}")
+        ns = [int(n) for _, _, n in parts]
+        total = sum(ns)
+        out = np.empty((seq, total), dtype=np.float32)
+        temps = []
+        try:
+            ws = []
+            for q, wgt, n in parts:
+                if isinstance(wgt, DeviceWeight):
+                    ws.append(wgt)
+                else:
+                    raw = _raw_bytes(wgt).reshape(-1)
+                    dw = DeviceWeight(raw) if raw.size else None
+                    temps.append(dw)
+                    ws.append(dw)
+            if seq and total:
+                xb = (seq * k * 4 + 255) // 256 * 256
+                need = xb + seq * total * 4
+                if self._scratch is None or self._scratch.nbytes < need:
+                    self._scratch = device.DeviceBuffer(need)
+                base = self._scratch.ptr
+                if x_c.size:
+                    _lib.check(_lib.lib().frq_memcpy_h2d(base, x_c.ctypes.data, x_c.nbytes))
+                grp, off = [], 0
+                for (q, _, n), w in zip(parts, ws):
+                    grp.append((q, w if w is not None else 0, n, base + xb + 4 * off, w.nbytes if w is not None else 0))
+                    off += int(n)
+                device.gemv_group(grp, base, k, batch=seq, y_stride=total)
+                _lib.check(_lib.lib().frq_memcpy_d2h(out.ctypes.data, base + xb, out.nbytes))
+        finally:
+            for t in temps:
+                if t is not None:
+                    t.buffer.free()
+        return out[0] if x_c.ndim == 1 else out
+
     def matmul_q5_k(self, x, weight, n: int, k: int):
         """Fused Q5_K dequant + matvec (no native counterpart in the reference)."""
         return self._matmul("Q5_K", x, weight, n, k)

@@ -388,6 +388,45 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
     return FRQ_OK;
 }
 
+int frq_gemv_group_fusable(int count, const int* qtypes, const void* const* w, int64_t k) {
+    if (count < 1 || count > frq::kGemvGroupMax || !qtypes || !w) return 0;
+    return frq::gemv_group_fusable(count, qtypes, reinterpret_cast<const uint8_t* const*>(w), k) ? 1 : 0;
+}
+
+int frq_dev_gemv_group(int count, const int* qtypes, const void* const* w, const size_t* w_bytes, const int64_t* n,
+                       const float* x, int64_t k, float* const* y, int64_t batch, int64_t y_stride, void* stream) {
+    if (count < 1 || count > frq::kGemvGroupMax)
+        return fail(FRQ_ERR_INVALID, "gemv group: count %d outside [1, %d]", count, frq::kGemvGroupMax);
+    if (!qtypes || !w || !w_bytes || !n || !y) return fail(FRQ_ERR_INVALID, "gemv group: null argument array");
+    if (y_stride < 0) return fail(FRQ_ERR_SHAPE, "gemv group: negative y_stride");
+    Fmt f;
+    int64_t total = 0;
+    for (int i = 0; i < count; ++i) {
+        if (int rc = dev_gemv_checks(qtypes[i], w[i], w_bytes[i], x, y[i], n[i], k, batch, &f)) return rc;
+        total += n[i];
+    }
+    if (total == 0 || batch == 0) return FRQ_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t* wp[frq::kGemvGroupMax];
+    float* yb[frq::kGemvGroupMax];
+    for (int i = 0; i < count; ++i) wp[i] = static_cast<const uint8_t*>(w[i]);
+    const bool fused = k > 0 && frq::gemv_group_fusable(count, qtypes, wp, k);
+    for (int64_t b = 0; b < batch; ++b) {
+        for (int i = 0; i < count; ++i) yb[i] = y[i] + b * (y_stride ? y_stride : n[i]);
+        if (k == 0) {   // empty dot products are 0 (kernel fill: graph-capturable)
+            for (int i = 0; i < count; ++i)
+                if (n[i]) FRQ_HIP(frq::launch_fill(yb[i], 0.0f, n[i], s));
+        } else if (fused) {
+            FRQ_HIP(frq::launch_gemv_group(count, qtypes, wp, n, yb, x + b * k, k, s));
+        } else {
+            for (int i = 0; i < count; ++i)
+                if (n[i])
+                    if (int rc = gemv_device(qtypes[i], wp[i], x + b * k, yb[i], n[i], k, s)) return rc;
+        }
+    }
+    return FRQ_OK;
+}
+
 int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
                        frq_gemv_config* cfg, void* stream) {
     Fmt f;

@@ -95,20 +95,20 @@ __device__ __forceinline__ void finish_rows(int64_t row0, int64_t row_end, float
 // block's counter (device-scope atomic); the second to arrive reads the other
 // half's sums with system-scope loads (past the L2), writes y = a + b (the
 // same bits in either order) and returns the counter to zero.
+// Body of one workgroup; `wg` plays the role of blockIdx.x (the grouped
+// kernel below passes the index inside its segment).
 template <int CPL, int U, int R, int S = 1>
-__global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_waves_per_eu((CPL == 1 && U <= 3) ? 5 : 1))) gemv_q4_k_kernel(const uint8_t* __restrict__ w,
-                                                                         const float* __restrict__ x,
-                                                                         float* __restrict__ y, int64_t n,
-                                                                         int nb, float* __restrict__ part,
-                                                                         uint32_t* __restrict__ cnt) {
+__device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                               float* __restrict__ y, int64_t n, int nb, float* __restrict__ part,
+                                               uint32_t* __restrict__ cnt, int64_t wg) {
     static_assert(U <= R, "ring deeper than the row count");
     static_assert(S == 1 || S == 2, "one or two slices");
     __shared__ float red[R * 64];                           // [row][wave][DPP row]
     constexpr int LPB = 8 / CPL;
     constexpr int NE = 16 * CPL;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
-    const int slice = (S == 2) ? (int)(blockIdx.x & 1) : 0;
-    const int64_t rb = (S == 2) ? (int64_t)(blockIdx.x >> 1) : (int64_t)blockIdx.x;
+    const int slice = (S == 2) ? (int)(wg & 1) : 0;
+    const int64_t rb = (S == 2) ? (wg >> 1) : wg;
     const int nb0 = (S == 2) ? (nb + 1) / 2 : nb;           // blocks of the first slice
     const int blk_first = slice ? nb0 : 0, nbs = slice ? nb - nb0 : nb0;
     const int blk = tid / LPB, sub = tid % LPB;
@@ -253,6 +253,13 @@ __global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_w
             if (tid == 0) __hip_atomic_store(cnt + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+}
+
+template <int CPL, int U, int R, int S = 1>
+__global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_waves_per_eu((CPL == 1 && U <= 3) ? 5 : 1)))
+gemv_q4_k_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int64_t n, int nb,
+                 float* __restrict__ part, uint32_t* __restrict__ cnt) {
+    gemv_q4_k_body<CPL, U, R, S>(w, x, y, n, nb, part, cnt, blockIdx.x);
 }
 
 // ------------------------------------------------------------------ Q5_K
@@ -487,9 +494,8 @@ __device__ __forceinline__ void q6_quad(uint32_t src, uint32_t hsh, float (&f)[4
 }
 
 template <int U, int R>
-__global__ void __launch_bounds__(1024) gemv_q6_k_ring_kernel(const uint8_t* __restrict__ w,
-                                                              const float* __restrict__ x,
-                                                              float* __restrict__ y, int64_t n, int nb) {
+__device__ __forceinline__ void gemv_q6_k_ring_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                    float* __restrict__ y, int64_t n, int nb, int64_t wg) {
     static_assert(U <= R, "ring deeper than the row count");
     __shared__ float red[R * 64];                           // [row][wave][DPP row]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
@@ -501,7 +507,7 @@ __global__ void __launch_bounds__(1024) gemv_q6_k_ring_kernel(const uint8_t* __r
     const uint32_t sh = 8u * (uint32_t)mis;
     const int s = (sub & 3) >> 1;                  // l0 / 16
 
-    const int64_t row0 = (int64_t)blockIdx.x * R;
+    const int64_t row0 = wg * R;
     const int nrows = (int)(n - row0 < R ? n - row0 : R);
     const int64_t row_bytes = (int64_t)nb * kQ6KBytes;
     const uint32_t boff = (uint32_t)(blk * kQ6KBytes);
@@ -589,6 +595,35 @@ __global__ void __launch_bounds__(1024) gemv_q6_k_ring_kernel(const uint8_t* __r
         for (int w2 = 0; w2 < 4 * nwaves; ++w2) acc += red[r * 4 * nwaves + w2];
         y[row0 + r] = acc;
     }
+}
+
+template <int U, int R>
+__global__ void __launch_bounds__(1024) gemv_q6_k_ring_kernel(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ y, int64_t n, int nb) {
+    gemv_q6_k_ring_body<U, R>(w, x, y, n, nb, blockIdx.x);
+}
+
+// ------------------------------------------------------------------ grouped
+// One launch for several weight matrices that multiply the same x (q/k/v,
+// gate/up): segment i's rows go to y_i, and segment i owns workgroups
+// [wg_begin_i, wg_begin_{i+1}). Every segment has the same k, so one
+// workgroup shape (8 lanes per block, all of k) serves both row bodies; the
+// segment's format picks the body with a wave-uniform branch. Workgroups of
+// a segment do exactly what the single-matrix kernel's workgroups do, so the
+// outputs are bit-identical to separate launches.
+template <int R>
+__global__ void __launch_bounds__(1024) gemv_group_kernel(GemvGroup g, const float* __restrict__ x, int nb) {
+    const int64_t b = blockIdx.x;
+    int i = 0;
+#pragma unroll
+    for (int t = 1; t < kGemvGroupMax; ++t)
+        if (t < g.count && b >= g.wg_begin[t]) i = t;
+    const int64_t wg = b - g.wg_begin[i];
+    if (g.qtype[i] == kTypeQ4K)
+        gemv_q4_k_body<1, (R < 3 ? R : 3), R, 1>(g.w[i], x, g.y[i], g.n[i], nb, nullptr, nullptr, wg);
+    else
+        gemv_q6_k_ring_body<(R < 4 ? R : 4), R>(g.w[i], x, g.y[i], g.n[i], nb, wg);
 }
 
 // ------------------------------------------------------------------ Q8_0
@@ -1049,6 +1084,78 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
     if (p.unroll == 8)
         return launch_u<8>(qtype, p.cpl, w, x, y, n, (int)nb, p.rows_per_wg, p.waves, p.grid, stream);
     return launch_u<4>(qtype, p.cpl, w, x, y, n, (int)nb, p.rows_per_wg, p.waves, p.grid, stream);
+}
+
+bool gemv_group_fusable(int count, const int* qtypes, const uint8_t* const* w, int64_t k) {
+    if (count < 1 || count > kGemvGroupMax || k <= 0 || k % kQKElems) return false;
+    const int64_t nb = k / kQKElems;
+    if (nb * 8 > 1024) return false;
+    for (int i = 0; i < count; ++i) {
+        if (qtypes[i] == kTypeQ4K) {
+            if (reinterpret_cast<uintptr_t>(w[i]) & 15) return false;
+        } else if (qtypes[i] == kTypeQ6K) {
+            if (!q6k_ring_ok(w[i], nb)) return false;
+        } else {
+            return false;
+        }
+    }
+    return true;
+}
+
+template <int R>
+static void group_go(int64_t grid, int waves, const GemvGroup& g, const float* x, int nb, hipStream_t s) {
+    gemv_group_kernel<R><<<dim3((unsigned)grid), dim3((unsigned)(64 * waves)), 0, s>>>(g, x, nb);
+}
+
+hipError_t launch_gemv_group(int count, const int* qtypes, const uint8_t* const* w, const int64_t* n, float* const* y,
+                             const float* x, int64_t k, hipStream_t s, int* fused) {
+    if (fused) *fused = 0;
+    if (count < 1 || count > kGemvGroupMax) return hipErrorInvalidValue;
+    if (!gemv_group_fusable(count, qtypes, w, k)) {
+        for (int i = 0; i < count; ++i) {
+            GemvPlan p;
+            const hipError_t e = launch_gemv(qtypes[i], w[i], x, y[i], n[i], k, &p, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    const int64_t nb = k / kQKElems;
+    const int waves = (int)((nb * 8 + 63) / 64);
+    int64_t total = 0;
+    for (int i = 0; i < count; ++i) {
+        if (n[i] < 0) return hipErrorInvalidValue;
+        total += n[i];
+    }
+    if (total == 0) return hipSuccess;
+    // rows per workgroup for the whole group, by the single-matrix Q4_K rule
+    const int R = pick_rows_q4k(total, waves);
+    GemvGroup g{};
+    int64_t wg = 0;
+    int used = 0;
+    for (int i = 0; i < count; ++i) {
+        if (n[i] == 0) continue;                      // empty segment: no workgroups
+        g.w[used] = w[i];
+        g.y[used] = y[i];
+        g.n[used] = n[i];
+        g.qtype[used] = qtypes[i];
+        g.wg_begin[used] = wg;
+        wg += (n[i] + R - 1) / R;
+        ++used;
+    }
+    g.count = used;
+    if (wg > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    switch (R) {
+        case 1: group_go<1>(wg, waves, g, x, (int)nb, s); break;
+        case 2: group_go<2>(wg, waves, g, x, (int)nb, s); break;
+        case 4: group_go<4>(wg, waves, g, x, (int)nb, s); break;
+        case 7: group_go<7>(wg, waves, g, x, (int)nb, s); break;
+        case 8: group_go<8>(wg, waves, g, x, (int)nb, s); break;
+        case 14: group_go<14>(wg, waves, g, x, (int)nb, s); break;
+        case 16: group_go<16>(wg, waves, g, x, (int)nb, s); break;
+        default: return hipErrorInvalidConfiguration;
+    }
+    if (fused) *fused = 1;
+    return hipGetLastError();
 }
 
 }  // namespace frq

@@ -49,6 +49,25 @@ void gemv_split_scratch(int qtype, int64_t n, size_t* part_bytes, size_t* cnt_by
 // Checks that a GEMV of this shape can be planned; returns false with no launch otherwise.
 bool gemv_supported(int qtype, int64_t n, int64_t k);
 
+// Grouped GEMV: y_i[n_i] = W_i[n_i, k] . x[k] for up to kGemvGroupMax
+// matrices sharing x (q/k/v, gate/up), in ONE launch when every W_i is Q4_K
+// (16-byte aligned) or Q6_K (4-byte aligned, even block count) and 8 lanes
+// per block cover k (k <= 32768); otherwise one launch per matrix. Outputs
+// are bit-identical to separate launch_gemv calls either way. *fused tells
+// which path ran.
+constexpr int kGemvGroupMax = 4;
+struct GemvGroup {
+    const uint8_t* w[kGemvGroupMax];
+    float* y[kGemvGroupMax];
+    int64_t n[kGemvGroupMax];
+    int64_t wg_begin[kGemvGroupMax];   // first workgroup of each segment
+    int qtype[kGemvGroupMax];
+    int count;
+};
+bool gemv_group_fusable(int count, const int* qtypes, const uint8_t* const* w, int64_t k);
+hipError_t launch_gemv_group(int count, const int* qtypes, const uint8_t* const* w, const int64_t* n, float* const* y,
+                             const float* x, int64_t k, hipStream_t stream, int* fused = nullptr);
+
 // Split-K, software-pipelined GEMV (frq_gemv_sk.hip). Fields left <= 0 are
 // chosen by plan_gemv_sk.
 struct SplitKPlan {

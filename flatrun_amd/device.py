@@ -32,6 +32,8 @@ def _addr(obj) -> int:
 def _nbytes(obj) -> int:
     if isinstance(obj, DeviceBuffer):
         return obj.nbytes
+    if hasattr(obj, "data_ptr") and isinstance(getattr(obj, "nbytes", None), int):   # DeviceWeight
+        return obj.nbytes
     if hasattr(obj, "untyped_storage"):
         return int(obj.numel() * obj.element_size())
     raise TypeError(f"cannot size {type(obj).__name__}")
@@ -251,6 +253,39 @@ def gemv(qtype, w, x, y, n: int, k: int, batch: int = 1, stream=None, w_bytes: i
     q = qtype_id(qtype)
     wb = _nbytes(w) if w_bytes is None else int(w_bytes)
     check(lib().frq_dev_gemv(q, _addr(w), wb, _addr(x), _addr(y), int(n), int(k), int(batch), _stream(stream)))
+
+
+GROUP_MAX = 4
+
+
+def _group_arrays(parts):
+    if not 1 <= len(parts) <= GROUP_MAX:
+        raise ValueError(f"a GEMV group holds 1..{GROUP_MAX} matrices, got {len(parts)}")
+    qt = (ctypes.c_int * len(parts))(*[qtype_id(p[0]) for p in parts])
+    wp = (ctypes.c_void_p * len(parts))(*[_addr(p[1]) for p in parts])
+    return qt, wp
+
+
+def gemv_group(parts, x, k: int, batch: int = 1, y_stride: int = 0, stream=None) -> None:
+    """Matrices sharing x in one launch where possible (frq_dev_gemv_group).
+
+    ``parts``: up to 4 tuples ``(qtype, w, n, y[, w_bytes])``; ``y`` is the
+    device output of batch row 0 (an int address is accepted, e.g. an offset
+    into one concatenated buffer); row b of matrix i goes to
+    ``y_i + b * (y_stride or n_i)`` floats."""
+    qt, wp = _group_arrays(parts)
+    c = len(parts)
+    wb = (ctypes.c_size_t * c)(*[int(p[4]) if len(p) > 4 else _nbytes(p[1]) for p in parts])
+    nn = (ctypes.c_int64 * c)(*[int(p[2]) for p in parts])
+    yy = (ctypes.c_void_p * c)(*[_addr(p[3]) for p in parts])
+    check(lib().frq_dev_gemv_group(c, qt, wp, wb, nn, _addr(x), int(k), yy, int(batch), int(y_stride),
+                                   _stream(stream)))
+
+
+def gemv_group_fusable(parts, k: int) -> bool:
+    """True if ``parts`` ((qtype, w, ...) tuples) run as one launch."""
+    qt, wp = _group_arrays(parts)
+    return bool(lib().frq_gemv_group_fusable(len(parts), qt, wp, int(k)))
 
 
 def gemv_tuned(qtype, w, x, y, n: int, k: int, kernel: int = 0, cpl: int = 0, rows: int = 0, unroll: int = 0,

@@ -153,6 +153,25 @@ typedef struct {
     int64_t items;
 } frq_gemv_config;
 
+/* Several matrices that multiply the same x, with one launch where possible
+ * (replaces the forwarder's per-projection matmul calls followed by
+ * np.concatenate of their outputs: q/k/v model/qwen2.py:1510-1519, gate/up
+ * model/qwen2.py:1690-1702).
+ *   count        1 .. 4 matrices; qtypes[i], w[i], w_bytes[i], n[i] as for
+ *                frq_dev_gemv; all share k and x (batch rows of k floats)
+ *   y[i]         output base of matrix i for batch row 0; row b goes to
+ *                y[i] + b * (y_stride ? y_stride : n[i]) floats, so with
+ *                y[i] = out + (n[0] + .. + n[i-1]) and y_stride = sum of n
+ *                the result is the concatenation [W_0 x | W_1 x | ...]
+ * One launch per batch row when every matrix is Q4_K (16-byte aligned) or
+ * Q6_K (4-byte aligned, even block count per row) and k <= 32768
+ * (frq_gemv_group_fusable); otherwise one launch per matrix. The outputs are
+ * bit-identical to frq_dev_gemv on each matrix either way. */
+int frq_dev_gemv_group(int count, const int* qtypes, const void* const* w, const size_t* w_bytes, const int64_t* n,
+                       const float* x, int64_t k, float* const* y, int64_t batch, int64_t y_stride, void* stream);
+/* 1 if frq_dev_gemv_group would fuse these matrices into one launch, else 0. */
+int frq_gemv_group_fusable(int count, const int* qtypes, const void* const* w, int64_t k);
+
 /* frq_dev_gemv with an explicit launch geometry (batch 1). */
 int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
                        frq_gemv_config* cfg, void* stream);
