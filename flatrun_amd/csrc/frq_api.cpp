@@ -463,6 +463,10 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     p.rows_per_wg = cfg->rows;
     p.unroll = cfg->unroll;
     p.slices = cfg->slices;
+    if (cfg->kernel == FRQ_GEMV_ROWS_LDS) {
+        if (qtype != FRQ_Q4_K) return fail(FRQ_ERR_UNSUPPORTED, "the LDS row ring is a Q4_K kernel");
+        p.lds = cfg->unroll > 0 ? cfg->unroll : 4;
+    }
     float* part = nullptr;
     uint32_t* cnt = nullptr;
     if (p.slices == 2) {                       // the two-slice Q4_K kernel meets through scratch
@@ -473,7 +477,7 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     }
     hipError_t e = frq::launch_gemv(qtype, wp, x, y, n, k, &p, s, part, cnt);
     if (e != hipSuccess) return hip_fail(e, "launch_gemv");
-    cfg->kernel = FRQ_GEMV_ROWS;
+    cfg->kernel = p.lds > 0 ? FRQ_GEMV_ROWS_LDS : FRQ_GEMV_ROWS;
     cfg->cpl = p.cpl;
     cfg->rows = p.rows_per_wg;
     cfg->unroll = p.unroll;

@@ -255,6 +255,139 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
     }
 }
 
+// ------------------------------------------------------- Q4_K, LDS ring
+// The same per-lane work as gemv_q4_k_body with CPL = 1, fed through a ring
+// of D row slots in LDS instead of registers. Each wave owns blocks
+// [8w, 8w + 8) of every row (its lanes' blocks) and copies exactly those
+// 1152 bytes of row j + D into its own slot with two direct-to-LDS buffer
+// loads (64 x 16 B, then 32 x 4 B), contiguous like a plain streaming copy
+// and with no registers held while they are in flight. Nothing is shared
+// between waves, so no barrier is needed: a wave waits for its own loads
+// (vmcnt, counted at compile time), reads its lane's header and qs with two
+// ds_read_b128 and computes the row. Offsets past the row (the last wave's
+// missing blocks) read as zero through the row's buffer descriptor.
+constexpr int kQ4KLdsWaves = 16;      // slot storage sized for 1024-lane workgroups
+constexpr int kQ4KLdsWaveBytes = 1280;
+
+// Slot K of the ring: a variable of its own, so the compiler's LDS alias
+// scopes tell the slots apart and a read of slot K waits only for the loads
+// into slot K (one array indexed by slot makes every read wait for them all).
+template <int K>
+__device__ __forceinline__ uint8_t* q4k_lds_slot() {
+    __shared__ __attribute__((aligned(16))) uint8_t slot[kQ4KLdsWaves * kQ4KLdsWaveBytes];
+    return slot;
+}
+
+// s_waitcnt with vmcnt <= N and expcnt / lgkmcnt left unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int D, int R>
+__global__ void __launch_bounds__(1024) gemv_q4_k_lds_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                             float* __restrict__ y, int64_t n, int nb) {
+    static_assert(D >= 1 && D <= R, "ring depth");
+    __shared__ float red[R * 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const int blk = tid >> 3, sub = tid & 7;
+    const bool active = blk < nb;
+    const int gblk = active ? blk : 0;
+    const int g = sub >> 1, hh = sub & 1;
+    const PairDecode pdec(sub);
+    const bool own_hi = hh;
+    const float hfac = own_hi ? 0.0625f : 1.0f;
+    const uint32_t mask_a = own_hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu, mask_b = ~mask_a;
+
+    const int64_t row0 = (int64_t)blockIdx.x * R;
+    const int nrows = (int)(n - row0 < R ? n - row0 : R);
+    const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
+    const uint32_t wbase = (uint32_t)(wave * 8 * kQ4KBytes);          // the wave's bytes in a row
+    const uint32_t off_a = wbase + 16u * (uint32_t)lane;               // 64 x 16 B
+    const uint32_t off_b = wbase + 1024u + 4u * (uint32_t)(lane & 31); // 32 x 4 B (lanes 32..63 repeat)
+    // lane's block inside the wave's slot (inactive lanes read the wave's block 0)
+    const uint32_t lblk = active ? (uint32_t)((blk & 7) * kQ4KBytes) : 0u;
+    const uint32_t lq = lblk + 16 + 32 * g + 16 * hh;
+
+    auto issue = [&](auto jc) {                                        // row j -> slot j % D
+        constexpr int j = decltype(jc)::value;
+        const uint8_t* rp = w + (row0 + (j < nrows ? j : nrows - 1)) * row_bytes;
+        const auto rs = buffer_rsrc(rp, (uint32_t)row_bytes);
+        uint8_t* slot = q4k_lds_slot<j % D>() + wave * kQ4KLdsWaveBytes;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)slot, 16, off_a, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(slot + 1024), 4, off_b, 0,
+                                                 0, 0);
+    };
+
+    float xl[16], xh[16];
+    float sxl = 0.0f, sxh = 0.0f;
+    {
+        const float* xb = x + (int64_t)gblk * kQKElems + 64 * g + 16 * hh;
+        const float* xa = xb + (own_hi ? 32 : 0);
+        const float* xo = xb + (own_hi ? 0 : 32);
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(xa + i);
+            const float4 c = *reinterpret_cast<const float4*>(xo + i);
+            xl[i] = a.x; xl[i + 1] = a.y; xl[i + 2] = a.z; xl[i + 3] = a.w;
+            xh[i] = c.x; xh[i + 1] = c.y; xh[i + 2] = c.z; xh[i + 3] = c.w;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, D>([&](auto ic) { issue(ic); });
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        sxl += xl[i];
+        sxh += xh[i];
+    }
+    const float sxt = sxl + dpp_mov<0xB1>(sxh);
+
+    static_for<0, R>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        constexpr int newer = 2 * ((R - 1 - j) < (D - 1) ? (R - 1 - j) : (D - 1));
+        wait_vmcnt<newer>();                                           // this wave's copy of row j landed
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* slot = q4k_lds_slot<j % D>() + wave * kQ4KLdsWaveBytes;
+        const uint4 hd = *reinterpret_cast<const uint4*>(slot + lblk);
+        const uint4 q = *reinterpret_cast<const uint4*>(slot + lq);
+        const float d = f16_bits_to_f32(hd.x), dm = f16_bits_to_f32(hd.x >> 16);
+        uint32_t sc0, m0;
+        pdec(hd.y, hd.z, hd.w, sc0, m0);
+        float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+            float f[8];
+            nibbles8(qw[wd], f, mask_a, mask_b);
+            const int e = 4 * wd;
+            a0 = __builtin_fmaf(f[0], xl[e + 0], a0);
+            a1 = __builtin_fmaf(f[1], xl[e + 1], a1);
+            b0 = __builtin_fmaf(f[4], xh[e + 0], b0);
+            b1 = __builtin_fmaf(f[5], xh[e + 1], b1);
+            a0 = __builtin_fmaf(f[2], xl[e + 2], a0);
+            a1 = __builtin_fmaf(f[3], xl[e + 3], a1);
+            b0 = __builtin_fmaf(f[6], xh[e + 2], b0);
+            b1 = __builtin_fmaf(f[7], xh[e + 3], b1);
+        }
+        // the slot has been read into registers: refill it with row j + D
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (j + D < R) issue(Int<j + D>{});
+        const float so = (d * hfac) * (float)sc0, to = dm * (float)m0;
+        const float dot = (a0 + a1) + dpp_mov<0xB1>(b0 + b1);
+        const float pu = __builtin_fmaf(-to, sxt, so * dot);
+        const float v = row16_sum(active ? pu : 0.0f);
+        if ((lane & 15) == 15) red[j * 4 * nwaves + 4 * wave + (lane >> 4)] = v;
+    });
+    __syncthreads();
+    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+        float s = 0.0f;
+        for (int w2 = 0; w2 < 4 * nwaves; ++w2) s += red[r * 4 * nwaves + w2];
+        y[row0 + r] = s;
+    }
+}
+
 template <int CPL, int U, int R, int S = 1>
 __global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_waves_per_eu((CPL == 1 && U <= 3) ? 5 : 1)))
 gemv_q4_k_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int64_t n, int nb,
@@ -693,6 +826,105 @@ __global__ void __launch_bounds__(512) gemv_q8_0_kernel(const uint8_t* __restric
     finish_rows(row0, row_end, y, red, nwaves);
 }
 
+// Q8_0 register-ring kernel. Lane (block b = t / 2, half u = t % 2) owns
+// the 16 int8 at 34b + 2 + 16u (q8_0.h:36-51 element order). Blocks are 34
+// bytes, so with a 4-aligned row those bytes start at 0 or 2 mod 4: the lane
+// loads the aligned 20-byte window and funnel-shifts four dwords out of it.
+// Each int8 converts exactly with one sign-extending byte-select convert.
+// Rows as in the other ring kernels.
+__device__ __forceinline__ void sbytes8(uint32_t a, uint32_t b, float (&f)[8]) {
+    asm("v_cvt_f32_i32_sdwa %0, sext(%8) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f32_i32_sdwa %1, sext(%8) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f32_i32_sdwa %2, sext(%8) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f32_i32_sdwa %3, sext(%8) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+        "v_cvt_f32_i32_sdwa %4, sext(%9) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f32_i32_sdwa %5, sext(%9) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f32_i32_sdwa %6, sext(%9) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f32_i32_sdwa %7, sext(%9) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3"
+        : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]), "=&v"(f[7])
+        : "v"(a), "v"(b));
+}
+
+template <int U, int R>
+__global__ void __launch_bounds__(1024) gemv_q8_0_ring_kernel(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ y, int64_t n, int nb) {
+    static_assert(U <= R, "ring deeper than the row count");
+    __shared__ float red[R * 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const int blk_raw = tid >> 1, u = tid & 1;
+    const bool active = blk_raw < nb;
+    const int blk = active ? blk_raw : 0;
+    const uint32_t at = (uint32_t)(blk * kQ80Bytes + 2 + 16 * u);
+    const uint32_t o_win = at & ~3u, sh = 8u * (at & 3u), o_d = (uint32_t)(blk * kQ80Bytes);
+
+    const int64_t row0 = (int64_t)blockIdx.x * R;
+    const int nrows = (int)(n - row0 < R ? n - row0 : R);
+    const int64_t row_bytes = (int64_t)nb * kQ80Bytes;
+
+    struct Row {
+        uint4 q;
+        uint32_t q4, d;
+    };
+    auto load1 = [&](Row& t, int j) {
+        const uint8_t* rp = w + (row0 + (j < nrows ? j : nrows - 1)) * row_bytes;
+        const auto rs = buffer_rsrc(rp, (uint32_t)row_bytes);
+        t.q = bload_b128(rs, o_win);
+        t.q4 = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(o_win + 16), 0, 0);
+        t.d = bload_u16(rs, o_d);
+    };
+
+    float xv[16];
+    {
+        const float* xb = x + (int64_t)blk * kQ80Elems + 16 * u;
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(xb + i);
+            xv[i] = a.x; xv[i + 1] = a.y; xv[i + 2] = a.z; xv[i + 3] = a.w;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Row ring[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) load1(ring[i], i);
+    __builtin_amdgcn_sched_barrier(0);
+
+    static_for<0, R>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        Row& t = ring[j % U];
+        const uint32_t w5[5] = {t.q.x, t.q.y, t.q.z, t.q.w, t.q4};
+        uint32_t qd[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qd[c] = __builtin_amdgcn_alignbit(w5[c + 1], w5[c], sh);
+        const float d = f16_bits_to_f32(t.d);
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c += 2) {
+            float f[8];
+            sbytes8(qd[c], qd[c + 1], f);
+            a0 = __builtin_fmaf(f[0], xv[4 * c + 0], a0);
+            a1 = __builtin_fmaf(f[1], xv[4 * c + 1], a1);
+            a2 = __builtin_fmaf(f[2], xv[4 * c + 2], a2);
+            a3 = __builtin_fmaf(f[3], xv[4 * c + 3], a3);
+            a0 = __builtin_fmaf(f[4], xv[4 * c + 4], a0);
+            a1 = __builtin_fmaf(f[5], xv[4 * c + 5], a1);
+            a2 = __builtin_fmaf(f[6], xv[4 * c + 6], a2);
+            a3 = __builtin_fmaf(f[7], xv[4 * c + 7], a3);
+        }
+        if constexpr (j + U < R) load1(t, j + U);
+        __builtin_amdgcn_sched_barrier(0);
+        const float pu = d * ((a0 + a1) + (a2 + a3));
+        const float v = row16_sum(active ? pu : 0.0f);
+        if ((lane & 15) == 15) red[j * 4 * nwaves + 4 * wave + (lane >> 4)] = v;
+    });
+    __syncthreads();
+    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+        float acc = 0.0f;
+        for (int w2 = 0; w2 < 4 * nwaves; ++w2) acc += red[r * 4 * nwaves + w2];
+        y[row0 + r] = acc;
+    }
+}
+
 // ------------------------------------------------------------------ Q1_0
 // Work unit: 4*CPL bytes of sign bits (32*CPL elements, 4/CPL lanes per
 // block): sum_i (+-d) x_i = d * (2 * sum_{bit set} x_i - sum_i x_i).
@@ -766,6 +998,99 @@ __global__ void __launch_bounds__(512) gemv_q1_0_kernel(const uint8_t* __restric
         row_partials_out<U>(part, rb, row0, row_end, y, red, nwaves, wave, lane);
     }
     finish_rows(row0, row_end, y, red, nwaves);
+}
+
+// Q1_0 register-ring kernel. Lane (block b = t / 4, part u = t % 4) owns the
+// 4 sign-bit bytes 18b + 2 + 4u .. +3 (elements 32u .. 32u + 31 of block b;
+// element 8c + j is bit j of byte c, LSB first, gguf.py:266-299). Blocks
+// are 18 bytes, so with a 4-aligned row those bytes start at 0 or 2 mod 4:
+// the lane loads the aligned 8-byte window around them and funnel-shifts.
+// `bits & (0x01010101 << j)` leaves 2^j * bit in each byte: x is stored
+// pre-scaled by 2^-j (exact), so each element is one v_cvt_f32_ubyteN and
+// one FMA, and sum_i (+-d) x_i = d * (2 * sum_{bit set} x_i - sum_i x_i).
+// Rows as in the Q4_K / Q6_K ring kernels: fully unrolled over R, clamped
+// unconditional buffer loads, U rows in flight, 16-lane row sums in LDS.
+template <int U, int R>
+__global__ void __launch_bounds__(1024) gemv_q1_0_ring_kernel(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ y, int64_t n, int nb) {
+    static_assert(U <= R, "ring deeper than the row count");
+    __shared__ float red[R * 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const int blk_raw = tid >> 2, u = tid & 3;
+    const bool active = blk_raw < nb;
+    const int blk = active ? blk_raw : 0;
+    const uint32_t at = (uint32_t)(blk * kQ10Bytes + 2 + 4 * u);
+    const uint32_t o_win = at & ~3u, sh = 8u * (at & 3u), o_d = (uint32_t)(blk * kQ10Bytes);
+
+    const int64_t row0 = (int64_t)blockIdx.x * R;
+    const int nrows = (int)(n - row0 < R ? n - row0 : R);
+    const int64_t row_bytes = (int64_t)nb * kQ10Bytes;
+
+    struct Row {
+        uint32_t lo, hi, d;
+    };
+    auto load1 = [&](Row& t, int j) {
+        const uint8_t* rp = w + (row0 + (j < nrows ? j : nrows - 1)) * row_bytes;
+        const auto rs = buffer_rsrc(rp, (uint32_t)row_bytes);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)o_win, 0, 0);
+        t.lo = v[0];
+        t.hi = v[1];
+        t.d = bload_u16(rs, o_d);
+    };
+
+    float xv[32];
+    float sx = 0.0f;
+    {
+        const float* xb = x + (int64_t)blk * kQ10Elems + 32 * u;
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(xb + i);
+            xv[i] = a.x; xv[i + 1] = a.y; xv[i + 2] = a.z; xv[i + 3] = a.w;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Row ring[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) load1(ring[i], i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        sx += xv[i];
+        xv[i] *= 1.0f / (float)(1u << (i & 7));
+    }
+
+    static_for<0, R>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        Row& t = ring[j % U];
+        const uint32_t bits = __builtin_amdgcn_alignbit(t.hi, t.lo, sh);
+        const float d = f16_bits_to_f32(t.d);
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 8; b += 2) {
+            float f[8];                                             // bit planes b and b + 1
+            nibbles8(bits, f, 0x01010101u << b, 0x01010101u << (b + 1));
+            a0 = __builtin_fmaf(f[0], xv[b], a0);
+            a1 = __builtin_fmaf(f[4], xv[b + 1], a1);
+            a0 = __builtin_fmaf(f[1], xv[8 + b], a0);
+            a1 = __builtin_fmaf(f[5], xv[8 + b + 1], a1);
+            a0 = __builtin_fmaf(f[2], xv[16 + b], a0);
+            a1 = __builtin_fmaf(f[6], xv[16 + b + 1], a1);
+            a0 = __builtin_fmaf(f[3], xv[24 + b], a0);
+            a1 = __builtin_fmaf(f[7], xv[24 + b + 1], a1);
+        }
+        if constexpr (j + U < R) load1(t, j + U);
+        __builtin_amdgcn_sched_barrier(0);
+        const float pu = d * __builtin_fmaf(2.0f, a0 + a1, -sx);
+        const float v = row16_sum(active ? pu : 0.0f);
+        if ((lane & 15) == 15) red[j * 4 * nwaves + 4 * wave + (lane >> 4)] = v;
+    });
+    __syncthreads();
+    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+        float acc = 0.0f;
+        for (int w2 = 0; w2 < 4 * nwaves; ++w2) acc += red[r * 4 * nwaves + w2];
+        y[row0 + r] = acc;
+    }
 }
 
 // ------------------------------------------------------------------ planner
@@ -928,6 +1253,40 @@ bool q4k_rows(int rows, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const
     }
 }
 
+template <int D, int R>
+void q4k_lds_go(dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n, int nb) {
+    gemv_q4_k_lds_kernel<(D < R ? D : R), R><<<gd, bd, 0, s>>>(w, x, y, n, nb);
+}
+
+template <int D>
+bool q4k_lds_rows(int rows, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n,
+                  int nb) {
+    switch (rows) {
+        case 1: q4k_lds_go<D, 1>(gd, bd, s, w, x, y, n, nb); return true;
+        case 2: q4k_lds_go<D, 2>(gd, bd, s, w, x, y, n, nb); return true;
+        case 4: q4k_lds_go<D, 4>(gd, bd, s, w, x, y, n, nb); return true;
+        case 7: q4k_lds_go<D, 7>(gd, bd, s, w, x, y, n, nb); return true;
+        case 8: q4k_lds_go<D, 8>(gd, bd, s, w, x, y, n, nb); return true;
+        case 14: q4k_lds_go<D, 14>(gd, bd, s, w, x, y, n, nb); return true;
+        case 16: q4k_lds_go<D, 16>(gd, bd, s, w, x, y, n, nb); return true;
+        default: return false;
+    }
+}
+
+hipError_t launch_q4k_lds(int depth, int rows, int waves, int64_t grid, const uint8_t* w, const float* x, float* y,
+                          int64_t n, int nb, hipStream_t s) {
+    const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
+    bool ok = false;
+    if (depth >= 6)
+        ok = q4k_lds_rows<6>(rows, gd, bd, s, w, x, y, n, nb);
+    else if (depth >= 4)
+        ok = q4k_lds_rows<4>(rows, gd, bd, s, w, x, y, n, nb);
+    else
+        ok = q4k_lds_rows<2>(rows, gd, bd, s, w, x, y, n, nb);
+    if (!ok) return hipErrorInvalidConfiguration;
+    return hipGetLastError();
+}
+
 hipError_t launch_q4k(int cpl, int ring, int rows, int slices, int waves, int64_t grid, const uint8_t* w,
                       const float* x, float* y, int64_t n, int nb, float* part, uint32_t* cnt, hipStream_t s) {
     const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
@@ -985,6 +1344,64 @@ bool q6k_rows(int rows, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const
         case 16: q6k_go<U, 16>(gd, bd, s, w, x, y, n, nb); return true;
         default: return false;
     }
+}
+
+// Q8_0 ring kernel: work unit 8 in GemvPlan::cpl (2 lanes per block, 16 int8
+// each); needs a 4-byte aligned weight base and an even block count.
+constexpr int kQ80RingUnit = 8;
+
+bool q80_ring_ok(const uint8_t* w, int64_t nb) {
+    return (reinterpret_cast<uintptr_t>(w) & 3) == 0 && nb % 2 == 0 && nb * 2 <= 1024;
+}
+
+template <int U, int R>
+void q80_go(dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n, int nb) {
+    gemv_q8_0_ring_kernel<(U < R ? U : R), R><<<gd, bd, 0, s>>>(w, x, y, n, nb);
+}
+
+hipError_t launch_q80_ring(int rows, int waves, int64_t grid, const uint8_t* w, const float* x, float* y, int64_t n,
+                           int nb, hipStream_t s) {
+    const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
+    switch (rows) {
+        case 1: q80_go<4, 1>(gd, bd, s, w, x, y, n, nb); break;
+        case 2: q80_go<4, 2>(gd, bd, s, w, x, y, n, nb); break;
+        case 4: q80_go<4, 4>(gd, bd, s, w, x, y, n, nb); break;
+        case 7: q80_go<4, 7>(gd, bd, s, w, x, y, n, nb); break;
+        case 8: q80_go<4, 8>(gd, bd, s, w, x, y, n, nb); break;
+        case 14: q80_go<4, 14>(gd, bd, s, w, x, y, n, nb); break;
+        case 16: q80_go<4, 16>(gd, bd, s, w, x, y, n, nb); break;
+        default: return hipErrorInvalidConfiguration;
+    }
+    return hipGetLastError();
+}
+
+// Q1_0 ring kernel: work unit 8 in GemvPlan::cpl (4 lanes per block, 32
+// elements each); needs a 4-byte aligned weight base and an even block count.
+constexpr int kQ10RingUnit = 8;
+
+bool q10_ring_ok(const uint8_t* w, int64_t nb) {
+    return (reinterpret_cast<uintptr_t>(w) & 3) == 0 && nb % 2 == 0 && nb * 4 <= 1024;
+}
+
+template <int U, int R>
+void q10_go(dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n, int nb) {
+    gemv_q1_0_ring_kernel<(U < R ? U : R), R><<<gd, bd, 0, s>>>(w, x, y, n, nb);
+}
+
+hipError_t launch_q10_ring(int rows, int waves, int64_t grid, const uint8_t* w, const float* x, float* y, int64_t n,
+                           int nb, hipStream_t s) {
+    const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
+    switch (rows) {
+        case 1: q10_go<4, 1>(gd, bd, s, w, x, y, n, nb); break;
+        case 2: q10_go<4, 2>(gd, bd, s, w, x, y, n, nb); break;
+        case 4: q10_go<4, 4>(gd, bd, s, w, x, y, n, nb); break;
+        case 7: q10_go<4, 7>(gd, bd, s, w, x, y, n, nb); break;
+        case 8: q10_go<4, 8>(gd, bd, s, w, x, y, n, nb); break;
+        case 14: q10_go<4, 14>(gd, bd, s, w, x, y, n, nb); break;
+        case 16: q10_go<4, 16>(gd, bd, s, w, x, y, n, nb); break;
+        default: return hipErrorInvalidConfiguration;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_q6k_ring(int ring, int rows, int waves, int64_t grid, const uint8_t* w, const float* x, float* y,
@@ -1055,11 +1472,49 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
         return launch_q6k_ring(p.unroll, p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
     }
     if (qtype == kTypeQ6K && p.cpl == kQ6KRingUnit) return hipErrorInvalidValue;   // layout not eligible
+    if (qtype == kTypeQ10 && (p.cpl <= 0 || p.cpl == kQ10RingUnit) && q10_ring_ok(w, nb)) {
+        p.cpl = kQ10RingUnit;
+        p.waves = (int)((nb * 4 + 63) / 64);
+        if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q6k(n, p.waves);
+        if (!q4k_rows_ok(p.rows_per_wg)) return hipErrorInvalidConfiguration;
+        p.unroll = 4;
+        p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
+        if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+        if (plan) *plan = p;
+        return launch_q10_ring(p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
+    }
+    if (qtype == kTypeQ10 && p.cpl == kQ10RingUnit) return hipErrorInvalidValue;   // layout not eligible
+    if (qtype == kTypeQ80 && (p.cpl <= 0 || p.cpl == kQ80RingUnit) && q80_ring_ok(w, nb)) {
+        p.cpl = kQ80RingUnit;
+        p.waves = (int)((nb * 2 + 63) / 64);
+        if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q6k(n, p.waves);
+        if (!q4k_rows_ok(p.rows_per_wg)) return hipErrorInvalidConfiguration;
+        p.unroll = 4;
+        p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
+        if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+        if (plan) *plan = p;
+        return launch_q80_ring(p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
+    }
+    if (qtype == kTypeQ80 && p.cpl == kQ80RingUnit) return hipErrorInvalidValue;   // layout not eligible
     if (p.cpl <= 0) p.cpl = pick_cpl(qtype, nb);
     if (!cpl_valid(qtype, p.cpl)) return hipErrorInvalidValue;
     const int64_t lanes = nb * lanes_per_block(qtype, p.cpl);
     if (lanes > max_lanes(qtype, p.cpl)) return hipErrorInvalidConfiguration;
     p.waves = (int)((lanes + 63) / 64);
+    if (qtype == kTypeQ4K && p.lds > 0) {
+        if ((reinterpret_cast<uintptr_t>(w) & 15) || nb * 8 > 64 * kQ4KLdsWaves) return hipErrorInvalidConfiguration;
+        p.cpl = 1;
+        p.slices = 1;
+        p.waves = (int)((nb * 8 + 63) / 64);
+        if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q4k(n, p.waves);
+        if (!q4k_rows_ok(p.rows_per_wg)) return hipErrorInvalidConfiguration;
+        p.lds = p.lds >= 6 ? 6 : p.lds >= 4 ? 4 : 2;
+        p.unroll = p.lds < p.rows_per_wg ? p.lds : p.rows_per_wg;
+        p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
+        if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+        if (plan) *plan = p;
+        return launch_q4k_lds(p.lds, p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
+    }
     if (qtype == kTypeQ4K) {
         // one slice unless asked: two slices measured slower on every shape
         // tried (3584 x 18944: 13.1 vs 12.0 us), despite twice the waves

@@ -24,6 +24,7 @@ struct GemvPlan {
     int rows_per_wg = 0;    // output rows owned by one workgroup
     int unroll = 0;         // rows whose loads are issued together
     int slices = 0;         // Q4_K: 1, or 2 halves of every row (needs scratch); 0 = choose
+    int lds = 0;            // Q4_K: > 0 = row ring of that many rows in LDS instead of registers
     int64_t grid = 0;       // workgroups
 };
 

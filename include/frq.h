@@ -139,6 +139,8 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  *   kernel        FRQ_GEMV_AUTO, FRQ_GEMV_SPLITK (one wavefront per
  *                 (row block, K-slice) work item, deterministic split-K
  *                 fixup) or FRQ_GEMV_ROWS (one workgroup spans all of k)
+ *                 or FRQ_GEMV_ROWS_LDS (Q4_K: as ROWS, rows staged through
+ *                 an LDS ring of `unroll` rows by direct-to-LDS loads)
  *   cpl           work unit per lane (format specific)
  *   rows          rows per work item (SPLITK) / per workgroup (ROWS)
  *   unroll        rows per load batch
@@ -147,7 +149,7 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  *                 two halves, one workgroup each, combined through memory)
  *   waves_per_wg  wavefronts per workgroup (output)
  *   items         work items / workgroups launched (output)              */
-enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2 };
+enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2, FRQ_GEMV_ROWS_LDS = 3 };
 typedef struct {
     int32_t kernel, cpl, rows, unroll, slices, waves_per_wg;
     int64_t items;
