@@ -517,7 +517,10 @@ int frq_dev_gemm_bf16(int qtype, const void* w, size_t w_bytes, const uint16_t* 
     if ((qtype == FRQ_Q4_K ? (wa & 15) : (wa & 1)) || (reinterpret_cast<uintptr_t>(x) & 15))
         return fail(FRQ_ERR_ALIGN, "%s gemm: weight or x misaligned", f.name);
     if (reinterpret_cast<uintptr_t>(y) & 3) return fail(FRQ_ERR_ALIGN, "y must be 4-byte aligned");
-    FRQ_HIP(frq::launch_gemm_bf16(qtype, static_cast<const uint8_t*>(w), x, y, m, n, k, s));
+    float* part = nullptr;
+    uint32_t* cnt = nullptr;
+    if (int rc = sk_scratch(s, frq::gemm_bf16_scratch(m, n, k), 0, &part, &cnt)) return rc;   // split-K partials
+    FRQ_HIP(frq::launch_gemm_bf16(qtype, static_cast<const uint8_t*>(w), x, y, m, n, k, s, part));
     return FRQ_OK;
 }
 
@@ -541,7 +544,8 @@ int frq_gemm_bf16(int qtype, const uint16_t* x, const uint8_t* w, size_t w_bytes
     float* dy = reinterpret_cast<float*>(dw + wb + xb);
     FRQ_HIP(hipMemcpy(dw, w, w_bytes, hipMemcpyHostToDevice));
     FRQ_HIP(hipMemcpy(dx, x, (size_t)(m * k) * 2, hipMemcpyHostToDevice));
-    FRQ_HIP(frq::launch_gemm_bf16(qtype, dw, dx, dy, m, n, k, nullptr));
+    // the device entry point: same kernel plan (split-K scratch included) as resident weights
+    if (int rc = frq_dev_gemm_bf16(qtype, dw, w_bytes, dx, dy, m, n, k, nullptr)) return rc;
     FRQ_HIP(hipMemcpy(y, dy, (size_t)(m * n) * 4, hipMemcpyDeviceToHost));
     return FRQ_OK;
 }

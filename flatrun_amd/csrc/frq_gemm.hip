@@ -37,6 +37,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 // Native vector, not HIP's uint4 class: values of the class type held across
 // the K loop's barrier stay in scratch memory; native vectors go to registers.
@@ -132,42 +133,63 @@ struct WFmt<kTypeQ80> {
 template <>
 struct WFmt<kTypeQ6K> {
     static constexpr int kBytes = kQ6KBytes, kElems = kQKElems;
+    // ql and qh bytes of the quarter come from 20-byte windows aligned down to
+    // 4 bytes (the fields start at 0 or 2 mod 4; both windows share the
+    // misalignment, as their offsets differ by a multiple of 4) and are
+    // funnel-shifted into place; the windows stay inside the block.
     struct Raw {
-        uint32_t ql[4], qh[4];
-        uint32_t sc, d;
+        u32x4 ql;
+        u32x4 qh;
+        uint32_t ql4, qh4, sh, sc, d;
     };
     __device__ static void load(Raw& r, const uint8_t* wrow, int kb, int wq) {
         const uint8_t* bp = wrow + (int64_t)(kb >> 8) * kQ6KBytes;
         const int kt4 = (kb & 255) >> 6, h = kt4 >> 1, ks = 2 * (kt4 & 1) + (wq >> 1), l0 = 16 * (wq & 1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            r.ql[i] = ld_u32_a2(bp + 64 * h + 32 * (ks & 1) + l0 + 4 * i);
-            r.qh[i] = ld_u32_a2(bp + 128 + 32 * h + l0 + 4 * i);
-        }
+        const uint8_t* pl = bp + 64 * h + 32 * (ks & 1) + l0;
+        const uint8_t* ph = bp + 128 + 32 * h + l0;
+        const uintptr_t mis = reinterpret_cast<uintptr_t>(pl) & 3;
+        const uint8_t* al = pl - mis;
+        const uint8_t* ah = ph - mis;
+        r.ql = *reinterpret_cast<const u32x4*>(al);
+        r.ql4 = *reinterpret_cast<const uint32_t*>(al + 16);
+        r.qh = *reinterpret_cast<const u32x4*>(ah);
+        r.qh4 = *reinterpret_cast<const uint32_t*>(ah + 16);
+        r.sh = 8u * (uint32_t)mis;
         r.sc = bp[192 + 8 * h + (wq & 1) + 2 * ks];
         r.d = ld_u16(bp + 208);
     }
     __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq) {
         const int kt4 = (kb & 255) >> 6, ks = 2 * (kt4 & 1) + (wq >> 1);
         const float s = f16_bits_to_f32(r.d) * (float)(int)(int8_t)(r.sc & 0xFFu);
+        const float m = -32.0f * s;                         // exact: a power-of-two multiple
+        const uint32_t lw[5] = {r.ql[0], r.ql[1], r.ql[2], r.ql[3], r.ql4};
+        const uint32_t hw[5] = {r.qh[0], r.qh[1], r.qh[2], r.qh[3], r.qh4};
+        const uint32_t nsh = ks >= 2 ? 4u : 0u, hsh = 2u * (uint32_t)ks;
         uint32_t o[8];
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            const int i = p >> 1;
-            const uint32_t nib = (ks >= 2 ? (r.ql[i] >> 4) : r.ql[i]) & 0x0F0F0F0Fu;
-            const uint32_t q = nib | (((r.qh[i] >> (2 * ks)) & 0x03030303u) << 4);
-            const uint32_t v = q >> (16 * (p & 1));
-            o[p] = pack_bf16(s * (float)((int)(v & 0xFFu) - 32), s * (float)((int)((v >> 8) & 0xFFu) - 32));
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t l = __builtin_amdgcn_alignbit(lw[c + 1], lw[c], r.sh);
+            const uint32_t hb = __builtin_amdgcn_alignbit(hw[c + 1], hw[c], r.sh);
+            // q = low or high nibble of ql | bits 2ks, 2ks + 1 of qh << 4 (0 .. 63 per byte)
+            const uint32_t q = ((l >> nsh) & 0x0F0F0F0Fu) | (((hb >> hsh) & 0x03030303u) << 4);
+            // fl(s * (q - 32)) = fma(q, s, -32 s): the exact value, rounded once
+            o[2 * c] = pack_bf16(__builtin_fmaf(byte_f(q, 0), s, m), __builtin_fmaf(byte_f(q, 1), s, m));
+            o[2 * c + 1] = pack_bf16(__builtin_fmaf(byte_f(q, 2), s, m), __builtin_fmaf(byte_f(q, 3), s, m));
         }
         *reinterpret_cast<u32x4*>(dst + 16 * wq) = u32x4{o[0], o[1], o[2], o[3]};
         *reinterpret_cast<u32x4*>(dst + 16 * wq + 8) = u32x4{o[4], o[5], o[6], o[7]};
     }
 };
 
+// S > 1 splits K: split s of an output tile runs K-steps [s * K/(64S), +K/(64S))
+// and writes its fp32 partial tile to plane s of `part`; a second, small
+// kernel adds the planes in split order (deterministic, and the kernel
+// boundary makes every partial visible whichever XCD wrote it).
 template <int QT>
 __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restrict__ w,
                                                              const uint16_t* __restrict__ x,
-                                                             float* __restrict__ y, int M, int N, int K) {
+                                                             float* __restrict__ y, int M, int N, int K, int S,
+                                                             float* __restrict__ part) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[2][kBM * kLds];
     __shared__ __attribute__((aligned(16))) uint16_t ws[2][kBN * kLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -176,10 +198,13 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
     // so with 2 (or 4, 8) M-tiles each XCD only ever needs its own M-tile of X
     // (2 MB at M-tile 256, K 4096), which then stays in that XCD's L2.
     const int mtiles = (M + kBM - 1) / kBM;
-    const int n0 = (int)(blockIdx.x / mtiles) * kBN, m0 = (int)(blockIdx.x % mtiles) * kBM;
+    const int mt = (int)(blockIdx.x % mtiles), rest = (int)(blockIdx.x / mtiles);
+    const int split = rest % S, nt = rest / S;
+    const int n0 = nt * kBN, m0 = mt * kBM;
     using F = WFmt<QT>;
     const int64_t row_bytes = (int64_t)(K / F::kElems) * F::kBytes;
-    const int ksteps = K / kBK;
+    const int ksteps = K / kBK / S;                    // even (chosen by the host)
+    const int kbase = split * ksteps;
 
     // X staging: 8 threads per row (16 B each), rows xr + 64 j.
     const int xc = tid & 7, xr = tid >> 3;
@@ -193,7 +218,7 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
     };
     Stage st[2];
     auto load_tile = [&](Stage& sg, int kt) __attribute__((always_inline)) {
-        const int kb = kt * kBK;
+        const int kb = (kbase + kt) * kBK;
         static_for<0, 4>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             const int r = m0 + xr + 64 * j;
@@ -206,7 +231,7 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
             constexpr int j = decltype(jc)::value;
             *reinterpret_cast<u32x4*>(&xs[buf][(xr + 64 * j) * kLds + 8 * xc]) = sg.x[j];
         });
-        F::store(sg.w, &ws[buf][wr * kLds], kt * kBK, wq);
+        F::store(sg.w, &ws[buf][wr * kLds], (kbase + kt) * kBK, wq);
     };
 
     f32x16 acc[2][2];
@@ -260,6 +285,9 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
         });
     }
 
+    // S > 1: this split's partial tile goes to plane `split` of the scratch;
+    // gemm_split_reduce_kernel adds the planes after the kernel.
+    float* out = S == 1 ? y : part + (int64_t)split * M * N;
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -268,9 +296,27 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + 64 * wm + 32 * mi + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < M && n < N) y[(int64_t)m * N + n] = acc[mi][ni][r];
+                if (m < M && n < N) out[(int64_t)m * N + n] = acc[mi][ni][r];
             }
         }
+}
+
+// y[i] = part[0][i] + part[1][i] + ... + part[S-1][i], in that order (the
+// same bits however the splits were scheduled); 4 elements per thread.
+__global__ void __launch_bounds__(256) gemm_split_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
+                                                                int S, int64_t count) {
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i + 4 <= count) {
+        f32x4 v = *reinterpret_cast<const f32x4*>(part + i);
+        for (int q = 1; q < S; ++q) v += *reinterpret_cast<const f32x4*>(part + q * count + i);
+        *reinterpret_cast<f32x4*>(y + i) = v;
+    } else {
+        for (int64_t e = i; e < count; ++e) {
+            float v = part[e];
+            for (int q = 1; q < S; ++q) v += part[q * count + e];
+            y[e] = v;
+        }
+    }
 }
 
 }  // namespace
@@ -282,15 +328,51 @@ bool gemm_bf16_supported(int qtype, int64_t m, int64_t n, int64_t k) {
            k <= 0x7FFFFFFF && ((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM) <= 0x7FFFFFFF;
 }
 
+// K-splits for a GEMM shape: the largest S in {1, 2, 4, 8} that keeps the grid
+// within one round of 256 one-per-CU workgroups (tiles * S <= 256) and every
+// split at an even count of at least 4 K-steps. Shapes that fill the GPU are
+// not split: that would only trade tail balance for partial-sum traffic.
+// 512 x 14336 x 4096: 1; 512 x 4096 x 14336: 4; 512 x 1024 x 4096: 8.
+int gemm_bf16_splits(int64_t m, int64_t n, int64_t k) {
+    const int64_t kCUs = 256;
+    const int64_t tiles = ((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM);
+    const int64_t ksteps = k / kBK;
+    int best = 1;
+    for (int sp = 2; sp <= 8; sp *= 2) {
+        if (ksteps % (2 * sp) || ksteps / sp < 4 || tiles * sp > kCUs) break;
+        best = sp;
+    }
+    return best;
+}
+
+size_t gemm_bf16_scratch(int64_t m, int64_t n, int64_t k) {
+    const int sp = gemm_bf16_splits(m, n, k);
+    return sp > 1 ? (size_t)sp * (size_t)m * (size_t)n * sizeof(float) : 0;
+}
+
 hipError_t launch_gemm_bf16(int qtype, const uint8_t* w, const uint16_t* x, float* y, int64_t m, int64_t n, int64_t k,
-                            hipStream_t stream) {
+                            hipStream_t stream, float* part) {
     if (!gemm_bf16_supported(qtype, m, n, k)) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM))), block(512);
+    int sp = gemm_bf16_splits(m, n, k);
+    if (sp > 1 && !part) sp = 1;                           // no scratch: one split
+    const int64_t tiles = ((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM);
+    if (tiles * sp > 0x7FFFFFFF) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(tiles * sp)), block(512);
     switch (qtype) {
-        case kTypeQ4K: gemm_bf16_kernel<kTypeQ4K><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k); break;
-        case kTypeQ6K: gemm_bf16_kernel<kTypeQ6K><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k); break;
-        case kTypeQ80: gemm_bf16_kernel<kTypeQ80><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k); break;
+        case kTypeQ4K:
+            gemm_bf16_kernel<kTypeQ4K><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
+            break;
+        case kTypeQ6K:
+            gemm_bf16_kernel<kTypeQ6K><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
+            break;
+        case kTypeQ80:
+            gemm_bf16_kernel<kTypeQ80><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
+            break;
         default: return hipErrorInvalidValue;
+    }
+    if (sp > 1) {
+        const int64_t count = m * n, threads = (count + 3) / 4;
+        gemm_split_reduce_kernel<<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream>>>(part, y, sp, count);
     }
     return hipGetLastError();
 }

@@ -96,8 +96,15 @@ hipError_t launch_gemv_sk(int qtype, const uint8_t* w, const float* x, float* y,
 // bits, row-major) . W[n, k]^T (raw Q4_K, Q6_K or Q8_0 blocks) with W rounded
 // to bf16 and fp32 accumulation. x 16-byte aligned; w 16-byte aligned for
 // Q4_K, 2-byte for the others; k a multiple of 256 (Q4_K, Q6_K) or 128 (Q8_0).
+// Shapes with too few 256 x 128 output tiles to fill the GPU split K
+// (gemm_bf16_splits): each split writes an fp32 partial plane of `part`
+// (gemm_bf16_scratch bytes) and a second kernel adds the planes in split
+// order. Launches sharing `part` must be ordered (one stream). With null
+// scratch the GEMM runs unsplit.
 bool gemm_bf16_supported(int qtype, int64_t m, int64_t n, int64_t k);
+int gemm_bf16_splits(int64_t m, int64_t n, int64_t k);
+size_t gemm_bf16_scratch(int64_t m, int64_t n, int64_t k);
 hipError_t launch_gemm_bf16(int qtype, const uint8_t* w, const uint16_t* x, float* y, int64_t m, int64_t n, int64_t k,
-                            hipStream_t stream);
+                            hipStream_t stream, float* part = nullptr);
 
 }  // namespace frq

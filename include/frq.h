@@ -193,7 +193,10 @@ int frq_gemm_q4_k_bf16(const uint16_t* x_bf16, const uint8_t* w, size_t w_bytes,
 /* The same GEMM for any of Q4_K, Q6_K, Q8_0 (qtype); k a multiple of 256
  * (Q4_K, Q6_K) or 128 (Q8_0); w 16-byte aligned (Q4_K) or 2-byte aligned.
  * Replaces, for bf16 activations, matmul_q6_k_batched (_C.cpp:244-283) and
- * matmul_q8_0_batched (_C.cpp:199-242) as well. */
+ * matmul_q8_0_batched (_C.cpp:199-242) as well. Shapes with too few output
+ * tiles to fill the GPU (e.g. n = 1024 or 4096 at m = 512) split K over
+ * several workgroups and add the partials in a fixed order (deterministic);
+ * the partials live in scratch grown once per (device, stream). */
 int frq_dev_gemm_bf16(int qtype, const void* w, size_t w_bytes, const uint16_t* x_bf16, float* y, int64_t m,
                       int64_t n, int64_t k, void* stream);
 int frq_gemm_bf16(int qtype, const uint16_t* x_bf16, const uint8_t* w, size_t w_bytes, int64_t m, int64_t n,
@@ -233,8 +236,9 @@ int frq_device_synchronize(void);
  * step issues one GEMV per weight (224 for a 32-layer Llama block stack),
  * and replay removes the per-launch host cost. Capture runs on a stream made
  * by frq_stream_create (not the null stream), in thread-local mode. Entry
- * points that allocate on first use (the split-K scratch of very long rows,
- * the host workspace) must have run once for the shape before capture.
+ * points that allocate on first use (the split-K scratch of very long rows
+ * and of split GEMMs, the host workspace) must have run once for the shape
+ * before capture.
  * Captured work records kernels only (no memset nodes). No reference
  * counterpart: the reference calls its matmuls one by one from Python.     */
 int frq_stream_begin_capture(void* stream);

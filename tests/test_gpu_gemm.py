@@ -121,3 +121,44 @@ def test_gemm_edges_and_errors(frq):
     with pytest.raises(RuntimeError):
         _C.matmul_q4_k_bf16(np.zeros((2, 256), np.float32), np.zeros(100, np.uint8), 1, 256)
     assert _lib.lib().frq_dev_gemm_q4_k_bf16(None, 144, None, None, 1, 1, 256, None) != 0
+
+
+def test_gemm_split_k_deterministic_and_shared_scratch(frq):
+    """Shapes with few output tiles split K (512 x 1024 x 4096: 8 splits);
+    the partial planes are added in split order, so repeated calls give the
+    same bits, also when other split GEMMs, graph replays and split-K GEMVs
+    (which share the scratch) run in between."""
+    from flatrun_amd import device
+
+    m, n, k = 512, 1024, 4096
+    raw, xb = make_case(m, n, k, seed=21)
+    y0 = _C.matmul_q4_k_bf16(xb, raw, n, k)
+    check(y0, raw, xb, n, k)
+    raw2, xb2 = make_case(300, 200, 1024, seed=22, q="Q6_K")
+    wg = synth.make_blocks("Q4_K", 8, 65536, seed=23)               # split-K GEMV (rows beyond one workgroup)
+    xg = synth.make_x(65536, seed=24)
+    for _ in range(3):
+        assert bits_equal(_C.matmul_q4_k_bf16(xb, raw, n, k), y0)
+        check(_C.matmul_bf16("Q6_K", xb2, raw2, 200, 1024), raw2, xb2, 200, 1024, q="Q6_K")
+        _C.matmul_q4_k(xg, wg, 8, 65536)
+    w = device.DeviceBuffer.from_host(raw)
+    xd = device.DeviceBuffer.from_host(_C.to_bf16_bits(xb))
+    yd = device.DeviceBuffer(m * n * 4)
+    s = device.Stream()
+    try:
+        device.gemm_bf16("Q4_K", w, xd, yd, m, n, k, stream=s, w_bytes=raw.nbytes)
+        s.synchronize()
+        assert bits_equal(yd.to_host(np.float32).reshape(m, n), y0)
+        with device.Graph.capture(s) as cap:
+            device.gemm_bf16("Q4_K", w, xd, yd, m, n, k, stream=s, w_bytes=raw.nbytes)
+        for _ in range(3):
+            _lib.check(_lib.lib().frq_memcpy_h2d(yd.ptr, np.full(m * n, np.nan, np.float32).ctypes.data, m * n * 4))
+            cap.launch(s)
+            s.synchronize()
+            assert bits_equal(yd.to_host(np.float32).reshape(m, n), y0)
+        cap.destroy()
+    finally:
+        w.free()
+        xd.free()
+        yd.free()
+        s.destroy()
