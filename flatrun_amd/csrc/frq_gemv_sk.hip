@@ -9,11 +9,10 @@
 //     b is computed (two register sets, unrolled), so HBM reads overlap the
 //     dequant arithmetic inside every wave.
 //   * Each row's lane partials are summed with DPP. With one slice the sum
-//     is y[row]; with S > 1 slices it goes to a partial buffer, and the last
-//     wave of a row block to finish (agent-scope counter, release/acquire
-//     fences, so the partials of waves on other XCDs are visible) sums the S
-//     partials in slice order -- a deterministic result -- and resets the
-//     counter to zero for the next launch.
+//     is y[row]; with S > 1 slices it goes to a partial buffer, and a second
+//     kernel sums the S partials of every row in slice order -- a
+//     deterministic result, with the kernel boundary making the partials of
+//     waves on other XCDs visible (no cache flushes inside the kernel).
 //
 // Q4_K work unit (CPL=2): one 32-byte qs group g of a block: 64 elements,
 // sub-blocks 2g (low nibbles) and 2g+1 (high nibbles); CPL=1: half a group
@@ -25,22 +24,16 @@ namespace frq {
 
 namespace {
 
-// Sums the S slice partials of a finished row block (last wave only).
-__device__ __forceinline__ void splitk_fixup(float* __restrict__ y, float* __restrict__ part,
-                                             uint32_t* __restrict__ cnt, int64_t n, int S, int64_t rblk,
-                                             int64_t r0, int64_t r1, int lane) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    uint32_t prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(&cnt[rblk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __builtin_amdgcn_readfirstlane(prev);
-    if (prev != (uint32_t)(S - 1)) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    for (int64_t r = r0 + lane; r < r1; r += 64) {
-        float acc = 0.0f;
-        for (int s = 0; s < S; ++s) acc += part[(int64_t)s * n + r];
-        y[r] = acc;
-    }
-    if (lane == 0) __hip_atomic_store(&cnt[rblk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// y[r] = part[0][r] + part[1][r] + ... + part[S-1][r], in slice order (the
+// same bits however the slices were scheduled). Runs after the split-K
+// kernel, whose boundary makes every slice's partials visible.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
+                                                            int64_t n, int S) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    float acc = part[r];
+    for (int s = 1; s < S; ++s) acc += part[(int64_t)s * n + r];
+    y[r] = acc;
 }
 
 }  // namespace
@@ -48,7 +41,7 @@ __device__ __forceinline__ void splitk_fixup(float* __restrict__ y, float* __res
 template <int CPL, int U>
 __global__ void __launch_bounds__(256) gemv_q4_k_sk_kernel(const uint8_t* __restrict__ w,
                                                            const float* __restrict__ x, float* __restrict__ y,
-                                                           float* __restrict__ part, uint32_t* __restrict__ cnt,
+                                                           float* __restrict__ part,
                                                            int64_t n, int nb, int S, int ubase, int urem, int R,
                                                            int64_t items) {
     constexpr int UPB = 8 / CPL;   // work units per block
@@ -156,7 +149,6 @@ __global__ void __launch_bounds__(256) gemv_q4_k_sk_kernel(const uint8_t* __rest
         load(A, r + 2 * U);
         compute(B, r + U);
     }
-    if (S > 1) splitk_fixup(y, part, cnt, n, S, rblk, r0, r1, lane);
 }
 
 // ------------------------------------------------------------------ planner
@@ -219,17 +211,18 @@ bool plan_gemv_sk(int qtype, int64_t n, int64_t k, SplitKPlan* p) {
 
 void gemv_sk_scratch(const SplitKPlan& p, int64_t n, size_t* partial_bytes, size_t* counter_bytes) {
     *partial_bytes = p.slices > 1 ? (size_t)n * p.slices * 4 : 0;
-    *counter_bytes = p.slices > 1 ? (size_t)p.row_blocks * 4 : 0;
+    *counter_bytes = 0;
 }
 
 hipError_t launch_gemv_sk(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k,
                           const SplitKPlan& p, float* part, uint32_t* cnt, hipStream_t stream) {
     if (p.items <= 0) return hipSuccess;
-    if (p.slices > 1 && (!part || !cnt)) return hipErrorInvalidValue;
+    if (p.slices > 1 && !part) return hipErrorInvalidValue;
+    (void)cnt;
     const int nb = (int)(k / sk_block_elems(qtype));
     const int wpg = p.items >= 4 ? 4 : (int)p.items;      // independent waves per workgroup
     const dim3 bd(64 * wpg), gd((unsigned)((p.items + wpg - 1) / wpg));
-#define FRQ_SK_ARGS w, x, y, part, cnt, n, nb, p.slices, p.unit_base, p.unit_rem, p.rows, p.items
+#define FRQ_SK_ARGS w, x, y, part, n, nb, p.slices, p.unit_base, p.unit_rem, p.rows, p.items
     switch (qtype) {
         case kTypeQ4K:
             if (p.cpl == 2) {
@@ -243,6 +236,8 @@ hipError_t launch_gemv_sk(int qtype, const uint8_t* w, const float* x, float* y,
         default: return hipErrorInvalidValue;
     }
 #undef FRQ_SK_ARGS
+    if (p.slices > 1)
+        splitk_reduce_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream>>>(part, y, n, p.slices);
     return hipGetLastError();
 }
 
