@@ -206,6 +206,7 @@ def run_suite(stream, steps: int, only: set | None = None) -> dict:
              ("llama3_8b_decode_streamed", lambda: decode_sweep_streamed(stream)),
              ("prefill_gemm_q4_k_bf16_512x14336x4096", lambda: prefill_gemm(stream)),
              ("llama3_8b_prefill_layer_512", lambda: prefill_layer(stream)),
+             ("dequant", lambda: dequant_suite(stream)),
              ("copy_ceiling", lambda: copy_ceiling(stream)),
              ("gguf_load_llama3_8b_4_layers", lambda: gguf_load(stream)),
              ("host_path_q4_k_3584x18944", host_path_rate)]
@@ -366,6 +367,43 @@ def prefill_layer(stream, m: int = 512, reps: int = 5) -> dict:
     return {"us_per_layer": round(us, 1), "tflops": round(flop / us / 1e6, 1), "flop": flop, "gemms": len(LLAMA_LAYER),
             "frac_bf16_peak": round(flop / us / 1e6 / BF16_PEAK_TFLOPS, 4),
             "note": "X 512 tokens (bf16); W resident raw blocks; the reference re-dequantizes W per token"}
+
+
+DEQUANT_SUITE = [("Q8_0", 4864, 896), ("Q4_K", 18944, 3584), ("Q5_K", 18944, 3584), ("Q6_K", 152064, 3584),
+                 ("Q8_0", 18944, 3584), ("Q1_0", 18944, 3584), ("Q4_0", 18944, 3584), ("Q5_0", 18944, 3584),
+                 ("Q5_1", 18944, 3584)]
+
+
+def dequant_suite(stream, reps: int = 20) -> dict:
+    """Block dequant to fp32 at the workload shapes, and every format at
+    18944 x 3584 (271 MB of fp32 out, past the 256 MB last-level cache, so
+    the formats compare on HBM): algorithmic bytes = raw blocks read +
+    4 n k written, timed as a graph of `reps` launches over 2 weight copies."""
+    out = {}
+    for q, n, k in DEQUANT_SUITE:
+        raw = synth.make_blocks(q, n, k, seed=50)
+        ws = [device.DeviceBuffer.from_host(raw) for _ in range(2)]
+        y = device.DeviceBuffer(4 * n * k)
+        with device.Graph.capture(stream) as cap:
+            for i in range(reps):
+                device.dequant(q, ws[i % 2], y, n * k, stream=stream, w_bytes=raw.nbytes)
+        cap.launch(stream)
+        device.synchronize()
+        e0, e1 = device.Event(), device.Event()
+        e0.record(stream)
+        cap.launch(stream)
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) / reps * 1e3
+        cap.destroy()
+        for b in ws:
+            b.free()
+        y.free()
+        nbytes = raw.nbytes + 4 * n * k
+        out[f"{q.lower()}_{n}x{k}"] = {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
+                                       "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                                       "algorithmic_bytes": nbytes}
+    return out
 
 
 def copy_ceiling(stream, mib: int = 512, reps: int = 20) -> dict:

@@ -16,9 +16,10 @@
 // products above is fused into the following add.
 //
 // Work mapping: one thread writes four consecutive outputs (one dwordx4
-// store), so a wavefront writes 1 KiB of contiguous fp32 and the stores are
-// fully coalesced; the kernel is bound by the 4 B/element write stream. The
-// four outputs always share one scale, so each thread decodes one scale pair.
+// store; eight, in two stores, for Q4_K and Q5_K), so a wavefront writes 1-2
+// KiB of contiguous fp32; the kernel is bound by the 4 B/element write
+// stream. A thread's outputs always share one scale, so it decodes one scale
+// pair.
 // A ragged last block (element count not a multiple of the block) is decoded
 // and the tail trimmed, as the reference's _finish does (gguf.py:61-73).
 #include "frq_common.h"
@@ -40,9 +41,12 @@ __device__ __forceinline__ void store4(float* __restrict__ y, int64_t e0, int64_
 
 __device__ __forceinline__ float ub(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
 
+// Q4_K and Q5_K: eight outputs per thread (two dwordx4 stores), all in one
+// 32-element sub-block, so the block header is read and the scale pair
+// decoded once per eight outputs.
 __global__ void __launch_bounds__(256) dequant_q4_k_kernel(const uint8_t* __restrict__ w,
                                                            float* __restrict__ y, int64_t n) {
-    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    const int64_t e0 = 8 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
     if (e0 >= n) return;
     const int64_t b = e0 / kQKElems;
     const int o = (int)(e0 % kQKElems);
@@ -53,15 +57,16 @@ __global__ void __launch_bounds__(256) dequant_q4_k_kernel(const uint8_t* __rest
     k4_scale_min(hd.y, hd.z, hd.w, j, sc, m);
     const float s = f16_bits_to_f32(hd.x) * (float)sc;
     const float t = f16_bits_to_f32(hd.x >> 16) * (float)m;
-    uint32_t q = *reinterpret_cast<const uint32_t*>(blk + 16 + 32 * g + i);
-    q = (j & 1) ? (q >> 4) : q;
-    q &= 0x0F0F0F0Fu;
-    store4(y, e0, n, s * ub(q, 0) - t, s * ub(q, 1) - t, s * ub(q, 2) - t, s * ub(q, 3) - t);
+    const uint2 qq = *reinterpret_cast<const uint2*>(blk + 16 + 32 * g + i);
+    const uint32_t sh = (j & 1) ? 4u : 0u;
+    const uint32_t q0 = (qq.x >> sh) & 0x0F0F0F0Fu, q1 = (qq.y >> sh) & 0x0F0F0F0Fu;
+    store4(y, e0, n, s * ub(q0, 0) - t, s * ub(q0, 1) - t, s * ub(q0, 2) - t, s * ub(q0, 3) - t);
+    store4(y, e0 + 4, n, s * ub(q1, 0) - t, s * ub(q1, 1) - t, s * ub(q1, 2) - t, s * ub(q1, 3) - t);
 }
 
 __global__ void __launch_bounds__(256) dequant_q5_k_kernel(const uint8_t* __restrict__ w,
                                                            float* __restrict__ y, int64_t n) {
-    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    const int64_t e0 = 8 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
     if (e0 >= n) return;
     const int64_t b = e0 / kQKElems;
     const int o = (int)(e0 % kQKElems);
@@ -72,14 +77,19 @@ __global__ void __launch_bounds__(256) dequant_q5_k_kernel(const uint8_t* __rest
     k4_scale_min(hd.y, hd.z, hd.w, j, sc, m);
     const double s = (double)(f16_bits_to_f32(hd.x) * (float)sc);   // fl32(d*sc), widened exactly
     const double t = (double)(f16_bits_to_f32(hd.x >> 16) * (float)m);
-    uint32_t q = *reinterpret_cast<const uint32_t*>(blk + 48 + 32 * g + i);
-    q = ((j & 1) ? (q >> 4) : q) & 0x0F0F0F0Fu;
-    const uint32_t h = (*reinterpret_cast<const uint32_t*>(blk + 16 + i) >> j) & 0x01010101u;
-    q |= h << 4;                                                         // v = q4 + 16*bit, exact
-    float v[4];
+    const uint2 qq = *reinterpret_cast<const uint2*>(blk + 48 + 32 * g + i);
+    const uint2 hh = *reinterpret_cast<const uint2*>(blk + 16 + i);
+    const uint32_t sh = (j & 1) ? 4u : 0u;
+    const uint32_t qw[2] = {qq.x, qq.y}, hw[2] = {hh.x, hh.y};
+    float v[8];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) v[c] = (float)(s * (double)((q >> (8 * c)) & 0xFFu) - t);
+    for (int p = 0; p < 2; ++p) {
+        const uint32_t q = ((qw[p] >> sh) & 0x0F0F0F0Fu) | (((hw[p] >> j) & 0x01010101u) << 4);   // q4 + 16*bit
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[4 * p + c] = (float)(s * (double)((q >> (8 * c)) & 0xFFu) - t);
+    }
     store4(y, e0, n, v[0], v[1], v[2], v[3]);
+    store4(y, e0 + 4, n, v[4], v[5], v[6], v[7]);
 }
 
 __global__ void __launch_bounds__(256) dequant_q6_k_kernel(const uint8_t* __restrict__ w,
@@ -196,9 +206,10 @@ hipError_t launch_dequant(int qtype, const uint8_t* w, float* y, int64_t n, hipS
     const int64_t threads = (n + 3) / 4;
     const dim3 block(256);
     const dim3 grid((unsigned)((threads + 255) / 256));
+    const dim3 grid8((unsigned)(((n + 7) / 8 + 255) / 256));   // Q4_K, Q5_K: eight outputs per thread
     switch (qtype) {
-        case kTypeQ4K: dequant_q4_k_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
-        case kTypeQ5K: dequant_q5_k_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
+        case kTypeQ4K: dequant_q4_k_kernel<<<grid8, block, 0, stream>>>(w, y, n); break;
+        case kTypeQ5K: dequant_q5_k_kernel<<<grid8, block, 0, stream>>>(w, y, n); break;
         case kTypeQ6K: dequant_q6_k_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
         case kTypeQ80: dequant_q8_0_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
         case kTypeQ10: dequant_q1_0_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
