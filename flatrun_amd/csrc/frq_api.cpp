@@ -146,9 +146,13 @@ int sk_scratch(hipStream_t stream, size_t part_bytes, size_t cnt_bytes, float** 
     return FRQ_OK;
 }
 
-// One GEMV on device buffers: the whole-row kernel when a row fits one
-// workgroup, else the split-K kernel.
+// One GEMV on device buffers: the matrix-core Q4_K kernel where eligible,
+// else the whole-row kernel when a row fits one workgroup, else split-K.
 int gemv_device(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s) {
+    if (frq::gemv_mx_eligible(qtype, w, x, n, k)) {
+        FRQ_HIP(frq::launch_gemv_mx(w, x, y, n, k, 0, s));
+        return FRQ_OK;
+    }
     if (frq::gemv_supported(qtype, n, k)) {   // whole-row kernel, one slice: no scratch
         FRQ_HIP(frq::launch_gemv(qtype, w, x, y, n, k, nullptr, s));
         return FRQ_OK;
@@ -435,6 +439,21 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     if (n == 0 || k == 0) return fail(FRQ_ERR_SHAPE, "tuned gemv needs n > 0 and k > 0");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const uint8_t* wp = static_cast<const uint8_t*>(w);
+    if (cfg->kernel == FRQ_GEMV_MX || (cfg->kernel == FRQ_GEMV_AUTO && frq::gemv_mx_eligible(qtype, wp, x, n, k))) {
+        if (qtype != FRQ_Q4_K) return fail(FRQ_ERR_UNSUPPORTED, "the matrix-core GEMV is a Q4_K kernel");
+        int used = 0;
+        hipError_t e = frq::launch_gemv_mx(wp, x, y, n, k, cfg->rows, s, &used);
+        if (e != hipSuccess) return hip_fail(e, "launch_gemv_mx");
+        const int64_t nb = k / 256, L = (nb + 15) / 16;
+        cfg->kernel = FRQ_GEMV_MX;
+        cfg->cpl = 0;
+        cfg->rows = used;
+        cfg->unroll = (int32_t)L;
+        cfg->slices = 1;
+        cfg->waves_per_wg = (int32_t)((nb + L - 1) / L);
+        cfg->items = (n + used - 1) / used;
+        return FRQ_OK;
+    }
     if (cfg->kernel == FRQ_GEMV_SPLITK ||
         (cfg->kernel == FRQ_GEMV_AUTO && !frq::gemv_supported(qtype, n, k) && frq::gemv_sk_supported(qtype))) {
         frq::SplitKPlan p;

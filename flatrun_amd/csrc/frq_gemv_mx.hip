@@ -1,0 +1,248 @@
+// Q4_K GEMV, batch 1, with the products on the matrix cores
+// (v_mfma_i32_16x16x64_i8): y[i] = sum_j w[i, j] x[j], the reference's
+// matmul_q4_k (q4_k.h:427-449) over rows of 256-element blocks
+// [d f16][dmin f16][scales 12][qs 128] (gguf.py:192-219).
+//
+// Arithmetic. Within a 32-element sub-block s of a block, w = d*sc_s*q - dmin*m_s
+// with q in 0..15, so a row's block contributes
+//     d*sc_s * sum(q x) - dmin*m_s * sum(x)
+// per sub-block. x is split once per sub-block into an exponent e (the
+// sub-block's max |x| < 2^e) and integers m = trunc(x * 2^(30-e)), |m| < 2^30,
+// written as four balanced base-256 digits (int8). The matrix cores form
+// sum(q * digit) exactly in int32 for each digit; the epilogue recombines the
+// four sums (two exact 24-bit halves, one fp32 rounding), scales by 2^(e-30)
+// (exact) and d*sc_s, and subtracts dmin*m_s * sum(x) (sum(x) in fp32, fixed
+// order). x enters with 30 bits relative to its sub-block maximum; every
+// product q*digit is exact, so the result stays within the fp32 accumulation
+// tolerance of the element-wise kernels without matching their bits.
+//
+// Work mapping. A workgroup owns TR <= 16 output rows and the whole row
+// length; wave w owns blocks [w L, w L + L) of every row. Per wave:
+//   1. the x of its blocks is loaded first, then 3 x 16 B of every row's
+//      block per lane: lane (c = l & 15, g = l >> 4) takes row c's header and
+//      qs bytes 32g .. 32g+31, whose low nibbles are sub-block 2g and high
+//      nibbles sub-block 2g+1;
+//   2. the x digits go to a wave-private LDS table (lane t splits x[4t..4t+3]
+//      of each block; eight lanes share a sub-block's max and sum via DPP);
+//   3. four MFMAs per block: A = the digits, block-diagonal (row group g of A
+//      is nonzero only in k-group g, so lane (c, g) receives the digit sums of
+//      its own 16-byte groups), B = the nibbles as int8; the per-row epilogue
+//      applies the scales;
+//   4. one LDS reduction over waves and k-groups, in a fixed order.
+// No barrier separates the waves between the loads and the reduction: the
+// only shared LDS data (a zero block that the inactive A lanes read) is
+// written and fenced before the first load.
+#include "frq_common.h"
+#include "frq_kernels.h"
+
+namespace frq {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMxMaxL = 5;              // blocks per wave: k <= 16 waves x 5 blocks x 256
+constexpr int kMxLimbBlock = 1024;      // digit bytes per block: 256 x 4
+constexpr int kMxTabBlock = 16;         // per block: 8 sub-blocks x (exponent, sum x)
+
+__device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
+    return __builtin_amdgcn_perm(s0, s1, sel);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+
+template <int LMAX>
+__global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __restrict__ w,
+                                                            const float* __restrict__ x, float* __restrict__ y,
+                                                            int64_t n, int nb, int L, int TR) {
+    constexpr int kWaveLimb = LMAX * kMxLimbBlock;
+    constexpr int kLimbAll = 16 * kWaveLimb;
+    constexpr int kZero = LMAX * kMxLimbBlock;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLimbAll + kZero];
+    __shared__ __attribute__((aligned(16))) float tab[16 * LMAX * kMxTabBlock];
+    __shared__ float red[16 * 64];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const int b0 = wave * L;
+    const int lw = (nb - b0 < L) ? nb - b0 : L;   // >= 1: the launch gives every wave a block
+    const int64_t row0 = (int64_t)blockIdx.x * TR;
+    const int nrows = (int)((n - row0 < TR) ? n - row0 : TR);
+    const int c = lane & 15, g = lane >> 4;
+    const uint32_t row_bytes = (uint32_t)nb * kQ4KBytes;
+    const auto rs = buffer_rsrc(w + row0 * (int64_t)row_bytes, (uint32_t)nrows * row_bytes);
+    const uint32_t roff = (uint32_t)(c < nrows ? c : nrows - 1) * row_bytes;   // extra lanes re-read the last row
+
+    for (int i = tid; i < kZero / 16; i += blockDim.x)
+        reinterpret_cast<uint4*>(lds + kLimbAll)[i] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+
+    // x first (small, cache-resident): the digit split then waits for x only,
+    // while every weight load is still in flight. Blocks past the wave's
+    // slice (last wave only) re-read its last block; their sums are dropped.
+    float4 xv[LMAX];
+#pragma unroll
+    for (int j = 0; j < LMAX; ++j) {
+        const int jj = j < lw ? j : lw - 1;
+        xv[j] = *reinterpret_cast<const float4*>(x + (int64_t)(b0 + jj) * kQKElems + 4 * lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 hd[LMAX], q0[LMAX], q1[LMAX];
+#pragma unroll
+    for (int j = 0; j < LMAX; ++j) {
+        const int jj = j < lw ? j : lw - 1;
+        const uint32_t off = roff + (uint32_t)(b0 + jj) * kQ4KBytes;
+        hd[j] = bload_b128(rs, off);
+        q0[j] = bload_b128(rs, off + 16 + 32 * g);
+        q1[j] = bload_b128(rs, off + 32 + 32 * g);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- x -> digits. Lane t: x[4t .. 4t+3] of the block = sub-block s = t / 8,
+    // half h = (t / 4) % 2, bytes 4 (t % 4) .. +3 of the 16-element group.
+    // Table entry (hi, h, g) (hi = s % 2, g = s / 2) holds 4 digits x 16 bytes.
+    {
+        const int s = lane >> 3, hi = s & 1, gg = s >> 1, h = (lane >> 2) & 1;
+        uint8_t* wl = lds + wave * kWaveLimb + ((hi * 2 + h) * 4 + gg) * 64 + 4 * (lane & 3);
+        float* wt = tab + wave * LMAX * kMxTabBlock + 2 * s;
+#pragma unroll
+        for (int j = 0; j < LMAX; ++j) {
+            const float4 v = xv[j];
+            const uint32_t a0 = __float_as_uint(v.x) & 0x7FFFFFFFu, a1 = __float_as_uint(v.y) & 0x7FFFFFFFu;
+            const uint32_t a2 = __float_as_uint(v.z) & 0x7FFFFFFFu, a3 = __float_as_uint(v.w) & 0x7FFFFFFFu;
+            uint32_t mx = max(max(a0, a1), max(a2, a3));   // |x| bit patterns order like |x|
+            mx = max(mx, dpp_u<0xB1>(mx));                 // quad_perm [1,0,3,2]
+            mx = max(mx, dpp_u<0x4E>(mx));                 // quad_perm [2,3,0,1]
+            mx = max(mx, dpp_u<0x141>(mx));                // row_half_mirror: max over the 8 lanes
+            float sx = (v.x + v.y) + (v.z + v.w);
+            sx += dpp_mov<0xB1>(sx);
+            sx += dpp_mov<0x4E>(sx);
+            sx += dpp_mov<0x141>(sx);                      // same fp32 sum in all 8 lanes
+            const int e = __builtin_amdgcn_frexp_expf(__uint_as_float(mx));   // max |x| < 2^e (0 for 0)
+            const int sh = 30 - e;
+            const int m0 = (int)__builtin_ldexpf(v.x, sh), m1 = (int)__builtin_ldexpf(v.y, sh);
+            const int m2 = (int)__builtin_ldexpf(v.z, sh), m3 = (int)__builtin_ldexpf(v.w, sh);
+            // m = sum_i digit_i 256^i with digit_i = byte_i(m + 0x808080) - 128
+            // (i < 3) and digit_3 = byte_3(m + 0x808080) as a signed byte
+            const uint32_t u0 = (uint32_t)m0 + 0x808080u, u1 = (uint32_t)m1 + 0x808080u;
+            const uint32_t u2 = (uint32_t)m2 + 0x808080u, u3 = (uint32_t)m3 + 0x808080u;
+            const uint32_t ab_e = perm(u1, u0, 0x06020400u), ab_o = perm(u1, u0, 0x07030501u);
+            const uint32_t cd_e = perm(u3, u2, 0x06020400u), cd_o = perm(u3, u2, 0x07030501u);
+            uint8_t* p = wl + j * kMxLimbBlock;
+            *reinterpret_cast<uint32_t*>(p + 0) = perm(cd_e, ab_e, 0x05040100u) ^ 0x80808080u;
+            *reinterpret_cast<uint32_t*>(p + 16) = perm(cd_o, ab_o, 0x05040100u) ^ 0x80808080u;
+            *reinterpret_cast<uint32_t*>(p + 32) = perm(cd_e, ab_e, 0x07060302u) ^ 0x80808080u;
+            *reinterpret_cast<uint32_t*>(p + 48) = perm(cd_o, ab_o, 0x07060302u);
+            *reinterpret_cast<float2*>(wt + j * kMxTabBlock) = make_float2(__int_as_float(e - 30), sx);
+        }
+    }
+
+    // ---- products. A lane of the A operand (row r = l & 15 of A, k-group
+    // l >> 4) carries digit r % 4 of k-group r / 4 when r / 4 == l >> 4, and
+    // zeros otherwise; the digit table and the zero block are read at the
+    // same per-MFMA offsets.
+    const bool act = ((lane & 15) >> 2) == (lane >> 4);
+    const uint8_t* abase = act ? lds + wave * kWaveLimb + (lane >> 4) * 64 + (lane & 3) * 16 : lds + kLimbAll;
+    const float* tb = tab + wave * LMAX * kMxTabBlock + 4 * g;
+    // scale pairs 2g, 2g+1 (get_scale_min_k4, gguf.py:135-163): bytes o, o+1
+    // of scales[0..3] / [4..7] (g < 2), plus the low / high nibbles of
+    // scales[8 + o], [9 + o] (g >= 2), o = 2 (g % 2)
+    const uint32_t o = 2u * (uint32_t)(g & 1);
+    const uint32_t selp = o | ((o + 1) << 8) | ((o + 4) << 16) | ((o + 5) << 24);
+    const uint32_t selq = o | ((o + 1) << 8) | (o << 16) | ((o + 1) << 24);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < LMAX; ++j) {
+        const uint8_t* ab = abase + j * kMxLimbBlock;
+        const i32x4 A00 = *reinterpret_cast<const i32x4*>(ab + 0);     // low nibbles, bytes 0..15
+        const i32x4 A01 = *reinterpret_cast<const i32x4*>(ab + 256);   // low nibbles, bytes 16..31
+        const i32x4 A10 = *reinterpret_cast<const i32x4*>(ab + 512);   // high nibbles, bytes 0..15
+        const i32x4 A11 = *reinterpret_cast<const i32x4*>(ab + 768);   // high nibbles, bytes 16..31
+        const uint4 a = q0[j], b = q1[j];
+        const i32x4 lo0 = {(int)(a.x & 0x0F0F0F0Fu), (int)(a.y & 0x0F0F0F0Fu), (int)(a.z & 0x0F0F0F0Fu),
+                           (int)(a.w & 0x0F0F0F0Fu)};
+        const i32x4 lo1 = {(int)(b.x & 0x0F0F0F0Fu), (int)(b.y & 0x0F0F0F0Fu), (int)(b.z & 0x0F0F0F0Fu),
+                           (int)(b.w & 0x0F0F0F0Fu)};
+        const i32x4 hi0 = {(int)((a.x >> 4) & 0x0F0F0F0Fu), (int)((a.y >> 4) & 0x0F0F0F0Fu),
+                           (int)((a.z >> 4) & 0x0F0F0F0Fu), (int)((a.w >> 4) & 0x0F0F0F0Fu)};
+        const i32x4 hi1 = {(int)((b.x >> 4) & 0x0F0F0F0Fu), (int)((b.y >> 4) & 0x0F0F0F0Fu),
+                           (int)((b.z >> 4) & 0x0F0F0F0Fu), (int)((b.w >> 4) & 0x0F0F0F0Fu)};
+        const i32x4 z = {0, 0, 0, 0};
+        i32x4 sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A00, lo0, z, 0, 0, 0);
+        sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A01, lo1, sl, 0, 0, 0);
+        i32x4 sh = __builtin_amdgcn_mfma_i32_16x16x64_i8(A10, hi0, z, 0, 0, 0);
+        sh = __builtin_amdgcn_mfma_i32_16x16x64_i8(A11, hi1, sh, 0, 0, 0);
+
+        const uint4 hdj = hd[j];
+        const float d = f16_bits_to_f32(hdj.x), dm = f16_bits_to_f32(hdj.x >> 16);
+        const uint32_t P = perm(hdj.z, hdj.y, selp), Q = perm(hdj.w, hdj.w, selq);
+        const uint32_t lo4 = (Q & 0x00000F0Fu) | ((Q >> 4) & 0x0F0F0000u);
+        const uint32_t scm = (g < 2) ? (P & 0x3F3F3F3Fu) : (lo4 | ((P >> 2) & 0x30303030u));
+        const float sc0 = (float)(scm & 0xFF), sc1 = (float)((scm >> 8) & 0xFF);
+        const float mn0 = (float)((scm >> 16) & 0xFF), mn1 = (float)(scm >> 24);
+        const float4 t = *reinterpret_cast<const float4*>(tb + j * kMxTabBlock);   // e0-30, sum0, e1-30, sum1
+        // sum(q m) = (S3 * 256 + S2) * 65536 + (S1 * 256 + S0): both halves exact in fp32
+        const float vl = __builtin_fmaf((float)((sl[3] << 8) + sl[2]), 65536.0f, (float)((sl[1] << 8) + sl[0]));
+        const float vh = __builtin_fmaf((float)((sh[3] << 8) + sh[2]), 65536.0f, (float)((sh[1] << 8) + sh[0]));
+        float part = __builtin_ldexpf(vl, __float_as_int(t.x)) * (d * sc0);
+        part = __builtin_fmaf(-(dm * mn0), t.y, part);
+        part = __builtin_fmaf(__builtin_ldexpf(vh, __float_as_int(t.z)), d * sc1, part);
+        part = __builtin_fmaf(-(dm * mn1), t.w, part);
+        acc += (j < lw) ? part : 0.0f;
+    }
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (tid < nrows) {
+        float s = 0.0f;
+        for (int wv = 0; wv < nwaves; ++wv)
+            s += (red[wv * 64 + tid] + red[wv * 64 + 16 + tid]) + (red[wv * 64 + 32 + tid] + red[wv * 64 + 48 + tid]);
+        y[row0 + tid] = s;
+    }
+}
+
+}  // namespace
+
+int gemv_mx_rows(int64_t n) {
+    // Rows per workgroup: fill the 256 CUs in whole rounds. r rounds of 256
+    // workgroups, r = ceil(n / 4096), each of ceil(n / (256 r)) <= 16 rows.
+    if (n <= 0) return 0;
+    const int64_t r = (n + 4095) / 4096;
+    return (int)((n + 256 * r - 1) / (256 * r));
+}
+
+bool gemv_mx_eligible(int qtype, const uint8_t* w, const float* x, int64_t n, int64_t k) {
+    if (qtype != kTypeQ4K || n <= 0 || k <= 0 || k % kQKElems) return false;
+    if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15) return false;
+    const int64_t nb = k / kQKElems;
+    if (nb > 16 * kMxMaxL) return false;
+    return gemv_mx_rows(n) >= kMxMinRows;
+}
+
+hipError_t launch_gemv_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int rows,
+                          hipStream_t stream, int* rows_used) {
+    if (n <= 0) return hipSuccess;
+    if (k <= 0 || k % kQKElems) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15) return hipErrorInvalidValue;
+    const int64_t nb64 = k / kQKElems;
+    if (nb64 > 16 * kMxMaxL) return hipErrorInvalidConfiguration;
+    const int nb = (int)nb64;
+    if (rows <= 0) rows = gemv_mx_rows(n);
+    if (rows < 1 || rows > 16) return hipErrorInvalidConfiguration;
+    const int L = (nb + 15) / 16;
+    const int nw = (nb + L - 1) / L;   // every wave gets >= 1 block: (nw - 1) L < nb
+    const int64_t grid = (n + rows - 1) / rows;
+    if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    if (rows_used) *rows_used = rows;
+    const dim3 g((unsigned)grid), b(64 * nw);
+    switch (L) {
+        case 1: gemv_q4_k_mx_kernel<1><<<g, b, 0, stream>>>(w, x, y, n, nb, L, rows); break;
+        case 2: gemv_q4_k_mx_kernel<2><<<g, b, 0, stream>>>(w, x, y, n, nb, L, rows); break;
+        case 3: gemv_q4_k_mx_kernel<3><<<g, b, 0, stream>>>(w, x, y, n, nb, L, rows); break;
+        case 4: gemv_q4_k_mx_kernel<4><<<g, b, 0, stream>>>(w, x, y, n, nb, L, rows); break;
+        default: gemv_q4_k_mx_kernel<5><<<g, b, 0, stream>>>(w, x, y, n, nb, L, rows); break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace frq

@@ -130,7 +130,12 @@ int frq_matmul(int qtype, const float* x, size_t seq, const uint8_t* weight, siz
 int frq_dev_dequant(int qtype, const void* w, size_t w_bytes, int64_t n_elems, float* y, void* stream);
 
 /* y[b, n] = W[n, k] . x[b, k] for b < batch: the decode matvec of
- * matmul_<q> / matmul_<q>_batched (_C.cpp:99-283) on device buffers. */
+ * matmul_<q> / matmul_<q>_batched (_C.cpp:99-283) on device buffers.
+ * Q4_K rows with k <= 20480 and n > 1280 (w and x 16-byte aligned) run on
+ * the matrix cores (int8 MFMA on the nibbles and on x split into four
+ * 8-bit digits per 32-element sub-block, exact integer dot products); the
+ * other shapes and formats on the element-wise kernels. Both stay within the
+ * fp32 accumulation tolerance of the fp64 result; their bits differ. */
 int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
                  int64_t batch, void* stream);
 
@@ -141,6 +146,10 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  *                 fixup) or FRQ_GEMV_ROWS (one workgroup spans all of k)
  *                 or FRQ_GEMV_ROWS_LDS (Q4_K: as ROWS, rows staged through
  *                 an LDS ring of `unroll` rows by direct-to-LDS loads)
+ *                 or FRQ_GEMV_MX (Q4_K, k <= 20480: the matrix-core kernel;
+ *                 `rows` = output rows per workgroup, 1..16, 0 = choose;
+ *                 on return `unroll` = blocks per wavefront). AUTO takes
+ *                 the kernel frq_dev_gemv takes.
  *   cpl           work unit per lane (format specific)
  *   rows          rows per work item (SPLITK) / per workgroup (ROWS)
  *   unroll        rows per load batch
@@ -149,7 +158,7 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  *                 two halves, one workgroup each, combined through memory)
  *   waves_per_wg  wavefronts per workgroup (output)
  *   items         work items / workgroups launched (output)              */
-enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2, FRQ_GEMV_ROWS_LDS = 3 };
+enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2, FRQ_GEMV_ROWS_LDS = 3, FRQ_GEMV_MX = 4 };
 typedef struct {
     int32_t kernel, cpl, rows, unroll, slices, waves_per_wg;
     int64_t items;
@@ -166,9 +175,10 @@ typedef struct {
  *                y[i] = out + (n[0] + .. + n[i-1]) and y_stride = sum of n
  *                the result is the concatenation [W_0 x | W_1 x | ...]
  * One launch per batch row when every matrix is Q4_K (16-byte aligned) or
- * Q6_K (4-byte aligned, even block count per row) and k <= 32768
- * (frq_gemv_group_fusable); otherwise one launch per matrix. The outputs are
- * bit-identical to frq_dev_gemv on each matrix either way. */
+ * Q6_K (4-byte aligned, even block count per row), k <= 32768 and no matrix
+ * takes frq_dev_gemv's matrix-core path (frq_gemv_group_fusable); otherwise
+ * one launch per matrix. The outputs are bit-identical to frq_dev_gemv on
+ * each matrix either way. */
 int frq_dev_gemv_group(int count, const int* qtypes, const void* const* w, const size_t* w_bytes, const int64_t* n,
                        const float* x, int64_t k, float* const* y, int64_t batch, int64_t y_stride, void* stream);
 /* 1 if frq_dev_gemv_group would fuse these matrices into one launch, else 0. */
