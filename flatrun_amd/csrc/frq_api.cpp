@@ -150,7 +150,7 @@ int sk_scratch(hipStream_t stream, size_t part_bytes, size_t cnt_bytes, float** 
 // else the whole-row kernel when a row fits one workgroup, else split-K.
 int gemv_device(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s) {
     if (frq::gemv_mx_eligible(qtype, w, x, n, k)) {
-        FRQ_HIP(frq::launch_gemv_mx(w, x, y, n, k, 0, s));
+        FRQ_HIP(frq::launch_gemv_mx(qtype, w, x, y, n, k, 0, s));
         return FRQ_OK;
     }
     if (frq::gemv_supported(qtype, n, k)) {   // whole-row kernel, one slice: no scratch
@@ -440,9 +440,10 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     hipStream_t s = static_cast<hipStream_t>(stream);
     const uint8_t* wp = static_cast<const uint8_t*>(w);
     if (cfg->kernel == FRQ_GEMV_MX || (cfg->kernel == FRQ_GEMV_AUTO && frq::gemv_mx_eligible(qtype, wp, x, n, k))) {
-        if (qtype != FRQ_Q4_K) return fail(FRQ_ERR_UNSUPPORTED, "the matrix-core GEMV is a Q4_K kernel");
+        if (qtype != FRQ_Q4_K && qtype != FRQ_Q6_K)
+            return fail(FRQ_ERR_UNSUPPORTED, "the matrix-core GEMV takes Q4_K and Q6_K");
         int used = 0;
-        hipError_t e = frq::launch_gemv_mx(wp, x, y, n, k, cfg->rows, s, &used);
+        hipError_t e = frq::launch_gemv_mx(qtype, wp, x, y, n, k, cfg->rows, s, &used);
         if (e != hipSuccess) return hip_fail(e, "launch_gemv_mx");
         const int64_t nb = k / 256, L = (nb + 15) / 16;
         cfg->kernel = FRQ_GEMV_MX;

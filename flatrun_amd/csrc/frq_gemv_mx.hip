@@ -32,6 +32,9 @@
 // No barrier separates the waves between the loads and the reduction: the
 // only shared LDS data (a zero block that the inactive A lanes read) is
 // written and fenced before the first load.
+//
+// A Q6_K kernel of the same design follows; frq_dev_gemv does not route to it
+// (slower than the element-wise Q6_K ring, see gemv_mx_eligible).
 #include "frq_common.h"
 #include "frq_kernels.h"
 
@@ -40,7 +43,8 @@ namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kMxMaxL = 5;              // blocks per wave: k <= 16 waves x 5 blocks x 256
+constexpr int kMxMaxL = 5;              // Q4_K blocks per wave: k <= 16 waves x 5 blocks x 256
+constexpr int kMxMaxLQ6 = 4;            // Q6_K (21 weight VGPRs per block)
 constexpr int kMxLimbBlock = 1024;      // digit bytes per block: 256 x 4
 constexpr int kMxTabBlock = 16;         // per block: 8 sub-blocks x (exponent, sum x)
 
@@ -51,6 +55,55 @@ __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel)
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+
+// x[4t .. 4t+3] of one 256-element block (lane t of a wave) as digits: d[i]
+// packs digit i of the four values in element order; eo = e - 30 for the
+// lane's 32-element sub-block (max |x| < 2^e); s16 / s32 = sum of x over the
+// lane's 16- / 32-element group, the same fp32 bits in every lane of it.
+struct XDigits {
+    uint32_t d[4];
+    int eo;
+    float s16, s32;
+};
+__device__ __forceinline__ XDigits x_digits(float4 v) {
+    XDigits r;
+    const uint32_t a0 = __float_as_uint(v.x) & 0x7FFFFFFFu, a1 = __float_as_uint(v.y) & 0x7FFFFFFFu;
+    const uint32_t a2 = __float_as_uint(v.z) & 0x7FFFFFFFu, a3 = __float_as_uint(v.w) & 0x7FFFFFFFu;
+    uint32_t mx = max(max(a0, a1), max(a2, a3));   // |x| bit patterns order like |x|
+    mx = max(mx, dpp_u<0xB1>(mx));                 // quad_perm [1,0,3,2]
+    mx = max(mx, dpp_u<0x4E>(mx));                 // quad_perm [2,3,0,1]
+    mx = max(mx, dpp_u<0x141>(mx));                // row_half_mirror: max over the 8 lanes
+    float sx = (v.x + v.y) + (v.z + v.w);
+    sx += dpp_mov<0xB1>(sx);
+    sx += dpp_mov<0x4E>(sx);
+    r.s16 = sx;                                    // 4 lanes = 16 elements
+    r.s32 = sx + dpp_mov<0x141>(sx);               // 8 lanes = 32 elements
+    const int e = __builtin_amdgcn_frexp_expf(__uint_as_float(mx));   // max |x| < 2^e (0 for 0)
+    const int sh = 30 - e;
+    const int m0 = (int)__builtin_ldexpf(v.x, sh), m1 = (int)__builtin_ldexpf(v.y, sh);
+    const int m2 = (int)__builtin_ldexpf(v.z, sh), m3 = (int)__builtin_ldexpf(v.w, sh);
+    // m = sum_i digit_i 256^i with digit_i = byte_i(m + 0x808080) - 128
+    // (i < 3) and digit_3 = byte_3(m + 0x808080) as a signed byte
+    const uint32_t u0 = (uint32_t)m0 + 0x808080u, u1 = (uint32_t)m1 + 0x808080u;
+    const uint32_t u2 = (uint32_t)m2 + 0x808080u, u3 = (uint32_t)m3 + 0x808080u;
+    const uint32_t ab_e = perm(u1, u0, 0x06020400u), ab_o = perm(u1, u0, 0x07030501u);
+    const uint32_t cd_e = perm(u3, u2, 0x06020400u), cd_o = perm(u3, u2, 0x07030501u);
+    r.d[0] = perm(cd_e, ab_e, 0x05040100u) ^ 0x80808080u;
+    r.d[1] = perm(cd_o, ab_o, 0x05040100u) ^ 0x80808080u;
+    r.d[2] = perm(cd_e, ab_e, 0x07060302u) ^ 0x80808080u;
+    r.d[3] = perm(cd_o, ab_o, 0x07060302u);
+    r.eo = e - 30;
+    return r;
+}
+
+// sum(q m) from the four int32 digit sums: (S3 * 256 + S2) * 65536 + (S1 * 256 + S0).
+// Q4_K (32 elements, q <= 15): |S_i| <= 61440, both halves exact in fp32.
+// Q6_K (16 elements, q <= 63): |S_i| <= 129024, |S3| <= 64512, so the high
+// half is exact and the low half (< 2^25) rounds at most once, by 2^(e-29)
+// in x units: the order of the digit truncation itself.
+__device__ __forceinline__ float digit_sum(i32x4 s) {
+    return __builtin_fmaf((float)((s[3] << 8) + s[2]), 65536.0f, (float)((s[1] << 8) + s[0]));
 }
 
 template <int LMAX>
@@ -108,33 +161,13 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
         float* wt = tab + wave * LMAX * kMxTabBlock + 2 * s;
 #pragma unroll
         for (int j = 0; j < LMAX; ++j) {
-            const float4 v = xv[j];
-            const uint32_t a0 = __float_as_uint(v.x) & 0x7FFFFFFFu, a1 = __float_as_uint(v.y) & 0x7FFFFFFFu;
-            const uint32_t a2 = __float_as_uint(v.z) & 0x7FFFFFFFu, a3 = __float_as_uint(v.w) & 0x7FFFFFFFu;
-            uint32_t mx = max(max(a0, a1), max(a2, a3));   // |x| bit patterns order like |x|
-            mx = max(mx, dpp_u<0xB1>(mx));                 // quad_perm [1,0,3,2]
-            mx = max(mx, dpp_u<0x4E>(mx));                 // quad_perm [2,3,0,1]
-            mx = max(mx, dpp_u<0x141>(mx));                // row_half_mirror: max over the 8 lanes
-            float sx = (v.x + v.y) + (v.z + v.w);
-            sx += dpp_mov<0xB1>(sx);
-            sx += dpp_mov<0x4E>(sx);
-            sx += dpp_mov<0x141>(sx);                      // same fp32 sum in all 8 lanes
-            const int e = __builtin_amdgcn_frexp_expf(__uint_as_float(mx));   // max |x| < 2^e (0 for 0)
-            const int sh = 30 - e;
-            const int m0 = (int)__builtin_ldexpf(v.x, sh), m1 = (int)__builtin_ldexpf(v.y, sh);
-            const int m2 = (int)__builtin_ldexpf(v.z, sh), m3 = (int)__builtin_ldexpf(v.w, sh);
-            // m = sum_i digit_i 256^i with digit_i = byte_i(m + 0x808080) - 128
-            // (i < 3) and digit_3 = byte_3(m + 0x808080) as a signed byte
-            const uint32_t u0 = (uint32_t)m0 + 0x808080u, u1 = (uint32_t)m1 + 0x808080u;
-            const uint32_t u2 = (uint32_t)m2 + 0x808080u, u3 = (uint32_t)m3 + 0x808080u;
-            const uint32_t ab_e = perm(u1, u0, 0x06020400u), ab_o = perm(u1, u0, 0x07030501u);
-            const uint32_t cd_e = perm(u3, u2, 0x06020400u), cd_o = perm(u3, u2, 0x07030501u);
+            const XDigits dg = x_digits(xv[j]);
             uint8_t* p = wl + j * kMxLimbBlock;
-            *reinterpret_cast<uint32_t*>(p + 0) = perm(cd_e, ab_e, 0x05040100u) ^ 0x80808080u;
-            *reinterpret_cast<uint32_t*>(p + 16) = perm(cd_o, ab_o, 0x05040100u) ^ 0x80808080u;
-            *reinterpret_cast<uint32_t*>(p + 32) = perm(cd_e, ab_e, 0x07060302u) ^ 0x80808080u;
-            *reinterpret_cast<uint32_t*>(p + 48) = perm(cd_o, ab_o, 0x07060302u);
-            *reinterpret_cast<float2*>(wt + j * kMxTabBlock) = make_float2(__int_as_float(e - 30), sx);
+            *reinterpret_cast<uint32_t*>(p + 0) = dg.d[0];
+            *reinterpret_cast<uint32_t*>(p + 16) = dg.d[1];
+            *reinterpret_cast<uint32_t*>(p + 32) = dg.d[2];
+            *reinterpret_cast<uint32_t*>(p + 48) = dg.d[3];
+            *reinterpret_cast<float2*>(wt + j * kMxTabBlock) = make_float2(__int_as_float(dg.eo), dg.s32);
         }
     }
 
@@ -182,9 +215,7 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
         const float sc0 = (float)(scm & 0xFF), sc1 = (float)((scm >> 8) & 0xFF);
         const float mn0 = (float)((scm >> 16) & 0xFF), mn1 = (float)(scm >> 24);
         const float4 t = *reinterpret_cast<const float4*>(tb + j * kMxTabBlock);   // e0-30, sum0, e1-30, sum1
-        // sum(q m) = (S3 * 256 + S2) * 65536 + (S1 * 256 + S0): both halves exact in fp32
-        const float vl = __builtin_fmaf((float)((sl[3] << 8) + sl[2]), 65536.0f, (float)((sl[1] << 8) + sl[0]));
-        const float vh = __builtin_fmaf((float)((sh[3] << 8) + sh[2]), 65536.0f, (float)((sh[1] << 8) + sh[0]));
+        const float vl = digit_sum(sl), vh = digit_sum(sh);
         float part = __builtin_ldexpf(vl, __float_as_int(t.x)) * (d * sc0);
         part = __builtin_fmaf(-(dm * mn0), t.y, part);
         part = __builtin_fmaf(__builtin_ldexpf(vh, __float_as_int(t.z)), d * sc1, part);
@@ -201,7 +232,139 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
     }
 }
 
+
+// Q6_K: blocks [ql 128][qh 64][scales int8 x16][d f16] (210 B, so only 2-byte
+// aligned; the buffer loads below are unaligned, which gfx950 serves exactly).
+// Element 128h + 32k + l (h < 2, k < 4, l < 32) is
+//     q = (ql[64h + 32 (k & 1) + l] >> 4 (k >> 1)) & 15 | ((qh[32h + l] >> 2k) & 3) << 4
+// with scale sc[8h + 2k + l / 16] and w = d * sc * (q - 32) (gguf.py:365-420,
+// matmul_q6_k q6_k.h). Lane (c, g) takes ql[64h + 16g .. +16) and
+// qh[32h + 16 (g & 1) .. +16) of row c for h = 0, 1: the low nibbles are the
+// 16-element sub-block 8h + g, the high nibbles 8h + 4 + g, i.e. element
+// chunk 4m + g for MFMA m = 2h + (high). One MFMA per sub-block (16 values of
+// q in 0..63 as int8), then d * sc * (sum(q x) - 32 sum(x)).
+template <int LMAX>
+__global__ void __launch_bounds__(1024) gemv_q6_k_mx_kernel(const uint8_t* __restrict__ w,
+                                                            const float* __restrict__ x, float* __restrict__ y,
+                                                            int64_t n, int nb, int L, int TR) {
+    constexpr int kTab = 32;   // per block: 16 chunks x (exponent, sum x), ordered [g][m]
+    constexpr int kWaveLimb = LMAX * kMxLimbBlock;
+    constexpr int kLimbAll = 16 * kWaveLimb;
+    constexpr int kZero = LMAX * kMxLimbBlock;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLimbAll + kZero];
+    __shared__ __attribute__((aligned(16))) float tab[16 * LMAX * kTab];
+    __shared__ float red[16 * 64];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    const int b0 = wave * L;
+    const int lw = (nb - b0 < L) ? nb - b0 : L;
+    const int64_t row0 = (int64_t)blockIdx.x * TR;
+    const int nrows = (int)((n - row0 < TR) ? n - row0 : TR);
+    const int c = lane & 15, g = lane >> 4;
+    const uint32_t row_bytes = (uint32_t)nb * kQ6KBytes;
+    const auto rs = buffer_rsrc(w + row0 * (int64_t)row_bytes, (uint32_t)nrows * row_bytes);
+    const uint32_t roff = (uint32_t)(c < nrows ? c : nrows - 1) * row_bytes;
+
+    for (int i = tid; i < kZero / 16; i += blockDim.x)
+        reinterpret_cast<uint4*>(lds + kLimbAll)[i] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+
+    float4 xv[LMAX];
+#pragma unroll
+    for (int j = 0; j < LMAX; ++j) {
+        const int jj = j < lw ? j : lw - 1;
+        xv[j] = *reinterpret_cast<const float4*>(x + (int64_t)(b0 + jj) * kQKElems + 4 * lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 ql0[LMAX], ql1[LMAX], qh0[LMAX], qh1[LMAX], scv[LMAX];
+    uint32_t dd[LMAX];
+#pragma unroll
+    for (int j = 0; j < LMAX; ++j) {
+        const int jj = j < lw ? j : lw - 1;
+        const uint32_t off = roff + (uint32_t)(b0 + jj) * kQ6KBytes;
+        ql0[j] = bload_b128(rs, off + 16 * g);
+        ql1[j] = bload_b128(rs, off + 64 + 16 * g);
+        qh0[j] = bload_b128(rs, off + 128 + 16 * (g & 1));
+        qh1[j] = bload_b128(rs, off + 160 + 16 * (g & 1));
+        scv[j] = bload_b128(rs, off + 192);
+        dd[j] = bload_u16(rs, off + 208);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    {   // x -> digits, in element order: lane t owns chunk t / 4, bytes 4 (t % 4) .. +3
+        const int ch = lane >> 2;
+        uint8_t* wl = lds + wave * kWaveLimb + ch * 64 + 4 * (lane & 3);
+        float* wt = tab + wave * LMAX * kTab + 2 * ((ch & 3) * 4 + (ch >> 2));
+#pragma unroll
+        for (int j = 0; j < LMAX; ++j) {
+            const XDigits dg = x_digits(xv[j]);
+            uint8_t* p = wl + j * kMxLimbBlock;
+            *reinterpret_cast<uint32_t*>(p + 0) = dg.d[0];
+            *reinterpret_cast<uint32_t*>(p + 16) = dg.d[1];
+            *reinterpret_cast<uint32_t*>(p + 32) = dg.d[2];
+            *reinterpret_cast<uint32_t*>(p + 48) = dg.d[3];
+            *reinterpret_cast<float2*>(wt + j * kTab) = make_float2(__int_as_float(dg.eo), dg.s16);
+        }
+    }
+
+    const bool act = ((lane & 15) >> 2) == (lane >> 4);
+    const uint8_t* abase = act ? lds + wave * kWaveLimb + (lane >> 4) * 64 + (lane & 3) * 16 : lds + kLimbAll;
+    const float* tb = tab + wave * LMAX * kTab + 8 * g;
+    // ((qh >> s) & 3) << 4 = rotr(qh, s - 4) & 0x30303030: s = 2 (g >> 1) for the
+    // low nibbles (k = g >> 1), 4 + 2 (g >> 1) for the high nibbles (k = 2 + (g >> 1))
+    const uint32_t rlo = (28u + 2u * (uint32_t)(g >> 1)) & 31u, rhi = 2u * (uint32_t)(g >> 1);
+    const uint32_t scsh = 8u * (uint32_t)g;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < LMAX; ++j) {
+        const uint8_t* ab = abase + j * kMxLimbBlock;
+        i32x4 bl[2], bh[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint4 ql = h ? ql1[j] : ql0[j], qh = h ? qh1[j] : qh0[j];
+            const uint32_t qv[4] = {ql.x, ql.y, ql.z, ql.w}, hv[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo_hi = __builtin_amdgcn_alignbit(hv[i], hv[i], rlo) & 0x30303030u;
+                const uint32_t hi_hi = __builtin_amdgcn_alignbit(hv[i], hv[i], rhi) & 0x30303030u;
+                bl[h][i] = (int)((qv[i] & 0x0F0F0F0Fu) | lo_hi);
+                bh[h][i] = (int)(((qv[i] >> 4) & 0x0F0F0F0Fu) | hi_hi);
+            }
+        }
+        const i32x4 z = {0, 0, 0, 0};
+        const i32x4 s0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(*reinterpret_cast<const i32x4*>(ab + 0), bl[0], z, 0, 0, 0);
+        const i32x4 s1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(*reinterpret_cast<const i32x4*>(ab + 256), bh[0], z, 0, 0, 0);
+        const i32x4 s2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(*reinterpret_cast<const i32x4*>(ab + 512), bl[1], z, 0, 0, 0);
+        const i32x4 s3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(*reinterpret_cast<const i32x4*>(ab + 768), bh[1], z, 0, 0, 0);
+
+        const float d = f16_bits_to_f32(dd[j]);
+        const uint4 sv = scv[j];   // sub-block 4m + g: byte g of dword m
+        // signed byte g of each dword (the builtin's result type is unsigned: cast before converting)
+        const float sc0 = (float)(int)__builtin_amdgcn_sbfe(sv.x, scsh, 8);
+        const float sc1 = (float)(int)__builtin_amdgcn_sbfe(sv.y, scsh, 8);
+        const float sc2 = (float)(int)__builtin_amdgcn_sbfe(sv.z, scsh, 8);
+        const float sc3 = (float)(int)__builtin_amdgcn_sbfe(sv.w, scsh, 8);
+        const float4 ta = *reinterpret_cast<const float4*>(tb + j * kTab);       // m = 0, 1: (e - 30, sum x)
+        const float4 tc = *reinterpret_cast<const float4*>(tb + j * kTab + 4);   // m = 2, 3
+        float part = (d * sc0) * __builtin_fmaf(-32.0f, ta.y, __builtin_ldexpf(digit_sum(s0), __float_as_int(ta.x)));
+        part = __builtin_fmaf(d * sc1, __builtin_fmaf(-32.0f, ta.w, __builtin_ldexpf(digit_sum(s1), __float_as_int(ta.z))), part);
+        part = __builtin_fmaf(d * sc2, __builtin_fmaf(-32.0f, tc.y, __builtin_ldexpf(digit_sum(s2), __float_as_int(tc.x))), part);
+        part = __builtin_fmaf(d * sc3, __builtin_fmaf(-32.0f, tc.w, __builtin_ldexpf(digit_sum(s3), __float_as_int(tc.z))), part);
+        acc += (j < lw) ? part : 0.0f;
+    }
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (tid < nrows) {
+        float s = 0.0f;
+        for (int wv = 0; wv < nwaves; ++wv)
+            s += (red[wv * 64 + tid] + red[wv * 64 + 16 + tid]) + (red[wv * 64 + 32 + tid] + red[wv * 64 + 48 + tid]);
+        y[row0 + tid] = s;
+    }
+}
+
 }  // namespace
+
+int mx_max_blocks(int qtype) { return qtype == kTypeQ6K ? kMxMaxLQ6 : kMxMaxL; }
 
 int gemv_mx_rows(int64_t n) {
     // Rows per workgroup: fill the 256 CUs in whole rounds. r rounds of 256
@@ -212,20 +375,26 @@ int gemv_mx_rows(int64_t n) {
 }
 
 bool gemv_mx_eligible(int qtype, const uint8_t* w, const float* x, int64_t n, int64_t k) {
+    // Q4_K only: the Q6_K matrix-core kernel measured slower than the
+    // element-wise ring on every shape tried (lm_head 152064 x 3584: 166 vs
+    // 109 us; 4096 x 14336: 18.3 vs 14.0 us). Its 210-byte blocks make half of
+    // its 16-byte loads unaligned, and a lane fetches 82 bytes per block for
+    // 52.5 used (qh and scales are shared by several lanes); the ring reads
+    // aligned windows once. It stays reachable through the tuned entry.
     if (qtype != kTypeQ4K || n <= 0 || k <= 0 || k % kQKElems) return false;
     if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15) return false;
-    const int64_t nb = k / kQKElems;
-    if (nb > 16 * kMxMaxL) return false;
+    if (k / kQKElems > 16 * mx_max_blocks(qtype)) return false;
     return gemv_mx_rows(n) >= kMxMinRows;
 }
 
-hipError_t launch_gemv_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int rows,
+hipError_t launch_gemv_mx(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int rows,
                           hipStream_t stream, int* rows_used) {
     if (n <= 0) return hipSuccess;
-    if (k <= 0 || k % kQKElems) return hipErrorInvalidValue;
-    if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15) return hipErrorInvalidValue;
+    if ((qtype != kTypeQ4K && qtype != kTypeQ6K) || k <= 0 || k % kQKElems) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(x) & 15) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(w) & (qtype == kTypeQ4K ? 15 : 1)) return hipErrorInvalidValue;
     const int64_t nb64 = k / kQKElems;
-    if (nb64 > 16 * kMxMaxL) return hipErrorInvalidConfiguration;
+    if (nb64 > 16 * mx_max_blocks(qtype)) return hipErrorInvalidConfiguration;
     const int nb = (int)nb64;
     if (rows <= 0) rows = gemv_mx_rows(n);
     if (rows < 1 || rows > 16) return hipErrorInvalidConfiguration;
@@ -235,6 +404,15 @@ hipError_t launch_gemv_mx(const uint8_t* w, const float* x, float* y, int64_t n,
     if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
     if (rows_used) *rows_used = rows;
     const dim3 g((unsigned)grid), b(64 * nw);
+    if (qtype == kTypeQ6K) {
+        switch (L) {
+            case 1: gemv_q6_k_mx_kernel<1><<<g, b, 0, stream>>>(w, x, y, n, nb, L, rows); break;
+            case 2: gemv_q6_k_mx_kernel<2><<<g, b, 0, stream>>>(w, x, y, n, nb, L, rows); break;
+            case 3: gemv_q6_k_mx_kernel<3><<<g, b, 0, stream>>>(w, x, y, n, nb, L, rows); break;
+            default: gemv_q6_k_mx_kernel<4><<<g, b, 0, stream>>>(w, x, y, n, nb, L, rows); break;
+        }
+        return hipGetLastError();
+    }
     switch (L) {
         case 1: gemv_q4_k_mx_kernel<1><<<g, b, 0, stream>>>(w, x, y, n, nb, L, rows); break;
         case 2: gemv_q4_k_mx_kernel<2><<<g, b, 0, stream>>>(w, x, y, n, nb, L, rows); break;

@@ -50,14 +50,17 @@ void gemv_split_scratch(int qtype, int64_t n, size_t* part_bytes, size_t* cnt_by
 // Checks that a GEMV of this shape can be planned; returns false with no launch otherwise.
 bool gemv_supported(int qtype, int64_t n, int64_t k);
 
-// Q4_K GEMV on the matrix cores (frq_gemv_mx.hip), batch 1. Eligible when
-// k is a multiple of 256 up to 20480, w and x are 16-byte aligned and the
-// row rule gives >= kMxMinRows rows per workgroup (n > 1280).
+// Q4_K / Q6_K GEMV on the matrix cores (frq_gemv_mx.hip), batch 1: k a
+// multiple of 256 up to 16 * mx_max_blocks(qtype) blocks (Q4_K 20480, Q6_K
+// 16384), x 16-byte aligned, w 16-byte (Q4_K) / 2-byte (Q6_K) aligned. The
+// default path takes it (gemv_mx_eligible) for Q4_K when the row rule gives
+// >= kMxMinRows rows per workgroup (n > 1280); Q6_K only through the tuned entry.
 constexpr int kMxMinRows = 6;
+int mx_max_blocks(int qtype);
 int gemv_mx_rows(int64_t n);
 bool gemv_mx_eligible(int qtype, const uint8_t* w, const float* x, int64_t n, int64_t k);
 // rows = output rows per workgroup (1..16; <= 0: gemv_mx_rows(n)); *rows_used gets what ran.
-hipError_t launch_gemv_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int rows,
+hipError_t launch_gemv_mx(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int rows,
                           hipStream_t stream, int* rows_used = nullptr);
 
 // Grouped GEMV: y_i[n_i] = W_i[n_i, k] . x[k] for up to kGemvGroupMax

@@ -146,10 +146,11 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  *                 fixup) or FRQ_GEMV_ROWS (one workgroup spans all of k)
  *                 or FRQ_GEMV_ROWS_LDS (Q4_K: as ROWS, rows staged through
  *                 an LDS ring of `unroll` rows by direct-to-LDS loads)
- *                 or FRQ_GEMV_MX (Q4_K, k <= 20480: the matrix-core kernel;
- *                 `rows` = output rows per workgroup, 1..16, 0 = choose;
- *                 on return `unroll` = blocks per wavefront). AUTO takes
- *                 the kernel frq_dev_gemv takes.
+ *                 or FRQ_GEMV_MX (the matrix-core kernel: Q4_K, k <= 20480,
+ *                 or Q6_K, k <= 16384; `rows` = output rows per workgroup,
+ *                 1..16, 0 = choose; on return `unroll` = blocks per
+ *                 wavefront). AUTO takes the kernel frq_dev_gemv takes
+ *                 (the matrix cores for Q4_K only).
  *   cpl           work unit per lane (format specific)
  *   rows          rows per work item (SPLITK) / per workgroup (ROWS)
  *   unroll        rows per load batch

@@ -1,12 +1,14 @@
-"""The matrix-core Q4_K GEMV (int8 MFMA; frq_gemv_mx.hip) against the oracle.
+"""The matrix-core Q4_K / Q6_K GEMVs (int8 MFMA; frq_gemv_mx.hip) against the oracle.
 
 Contract: the north-star matvec tolerance (1e-5 normwise and componentwise
 against the fp64 oracle); bits independent of the rows-per-workgroup choice
 and of launch order (fixed per-row summation order); the default device path
-takes it for Q4_K with k <= 20480 and n > 1280. x is split into four 8-bit
-digits per 32-element sub-block relative to the sub-block's max |x|, so the
-cases below include x spread over many binades inside a sub-block, tiny and
-huge x, zeros, and a lone outlier.
+takes the Q4_K kernel for n > 1280 and k <= 20480 (the Q6_K kernel, k <=
+16384, only through the tuned entry: slower than the Q6_K ring). x is split
+into four 8-bit digits per 32-element sub-block relative to the sub-block's
+max |x|, so the cases below include x spread over many binades inside a
+sub-block, tiny and huge x, zeros, and a lone outlier. Q6_K blocks are 210 B:
+odd block counts and a 2-byte weight offset exercise the unaligned loads.
 """
 
 from __future__ import annotations
@@ -21,13 +23,15 @@ from oracle import gguf_np as G
 pytestmark = pytest.mark.gpu
 
 
-def run_mx(raw, x, n, k, rows=0):
-    w = device.DeviceBuffer.from_host(raw)
+def run_mx(raw, x, n, k, rows=0, q="Q4_K", w_offset=0):
+    """One forced matrix-core launch; the weights sit w_offset bytes into their buffer."""
+    w = device.DeviceBuffer.from_host(np.concatenate([np.zeros(w_offset, np.uint8), raw]))
     xd = device.DeviceBuffer.from_host(x)
     yd = device.DeviceBuffer(max(4, 4 * n))
     try:
         _lib.check(_lib.lib().frq_memcpy_h2d(yd.ptr, np.full(n, np.nan, np.float32).ctypes.data, 4 * n))
-        cfg = device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_lib.GEMV_MX, rows=rows)
+        cfg = device.gemv_tuned(q, w.ptr + w_offset, xd, yd, n, k, kernel=_lib.GEMV_MX, rows=rows,
+                                w_bytes=raw.nbytes)
         device.synchronize()
         return yd.to_host(np.float32)[:n], cfg
     finally:
@@ -36,43 +40,60 @@ def run_mx(raw, x, n, k, rows=0):
         yd.free()
 
 
-def oracle_check(y, raw, x, n, k, what):
-    assert_matvec_close(y, G.matmul_f64("Q4_K", x, raw, n, k), G.abs_matmul_f64("Q4_K", x, raw, n, k), what=what)
+def oracle_check(y, raw, x, n, k, what, q="Q4_K"):
+    assert_matvec_close(y, G.matmul_f64(q, x, raw, n, k), G.abs_matmul_f64(q, x, raw, n, k), what=what)
 
 
-# nb = 1 .. 80 blocks: 1 .. 5 blocks per wave, ragged last waves (nb = 37, 74, 79)
-@pytest.mark.parametrize("n,k", [(1, 256), (5, 512), (16, 1024), (17, 1280), (33, 3584), (40, 4096), (7, 9472),
-                                 (100, 14336), (29, 18944), (64, 20224), (50, 20480)])
-def test_mx_shapes_and_rows(frq, n, k):
-    raw = synth.make_blocks("Q4_K", n, k, seed=n * 7 + k)
+# Q4_K: nb = 1 .. 80 blocks (1 .. 5 per wave); Q6_K: nb = 1 .. 64 (1 .. 4 per
+# wave), odd counts putting every other block at 2 mod 4; ragged last waves
+@pytest.mark.parametrize("q,n,k", [("Q4_K", 1, 256), ("Q4_K", 5, 512), ("Q4_K", 16, 1024), ("Q4_K", 17, 1280),
+                                   ("Q4_K", 33, 3584), ("Q4_K", 40, 4096), ("Q4_K", 7, 9472), ("Q4_K", 100, 14336),
+                                   ("Q4_K", 29, 18944), ("Q4_K", 64, 20224), ("Q4_K", 50, 20480),
+                                   ("Q6_K", 1, 256), ("Q6_K", 9, 768), ("Q6_K", 16, 1280), ("Q6_K", 33, 3584),
+                                   ("Q6_K", 21, 4352), ("Q6_K", 40, 9472), ("Q6_K", 70, 14336), ("Q6_K", 19, 16384)])
+def test_mx_shapes_and_rows(frq, q, n, k):
+    raw = synth.make_blocks(q, n, k, seed=n * 7 + k)
     x = synth.make_x(k, seed=k + 1)
     ref = None
     for rows in (16, 1, 3, 8, 14):
-        y, cfg = run_mx(raw, x, n, k, rows)
+        y, cfg = run_mx(raw, x, n, k, rows, q=q)
         assert cfg["kernel"] == _lib.GEMV_MX and cfg["rows"] == rows
         assert cfg["items"] == -(-n // rows)
         if ref is None:
-            oracle_check(y, raw, x, n, k, f"mx {n}x{k}")
+            oracle_check(y, raw, x, n, k, f"mx {q} {n}x{k}", q=q)
             ref = y
         else:
             assert bits_equal(y, ref), rows      # the row tiling never changes a row's sums
 
 
-@pytest.mark.parametrize("n,k", [(3584, 18944), (18944, 3584), (4096, 4096), (1536, 8960), (2000, 2048)])
-def test_mx_default_path_full_size(frq, n, k):
+def test_mx_q6_k_unaligned_weights(frq):
+    """Q6_K weights 2 bytes into their buffer (every block at 2 mod 4 or 0 mod 4
+    in turn, no 16-byte alignment anywhere): same bits as the aligned copy."""
+    q, n, k = "Q6_K", 37, 3328
+    raw = synth.make_blocks(q, n, k, seed=8)
+    x = synth.make_x(k, seed=9)
+    y0, _ = run_mx(raw, x, n, k, q=q)
+    y2, _ = run_mx(raw, x, n, k, q=q, w_offset=2)
+    oracle_check(y0, raw, x, n, k, "Q6_K aligned", q=q)
+    assert bits_equal(y0, y2)
+
+
+@pytest.mark.parametrize("q,n,k", [("Q4_K", 3584, 18944), ("Q4_K", 18944, 3584), ("Q4_K", 4096, 4096),
+                                   ("Q4_K", 1536, 8960), ("Q4_K", 2000, 2048)])
+def test_mx_default_path_full_size(frq, q, n, k):
     """frq_dev_gemv takes the matrix-core kernel for these shapes; the tuned
     entry's AUTO mode reports it and gives the same bits."""
-    raw = synth.make_blocks("Q4_K", n, k, seed=n ^ k)
+    raw = synth.make_blocks(q, n, k, seed=n ^ k)
     x = synth.make_x(k, seed=k + 7)
     w = device.DeviceBuffer.from_host(raw)
     xd = device.DeviceBuffer.from_host(x)
     yd = device.DeviceBuffer(4 * n)
     try:
-        device.gemv("Q4_K", w, xd, yd, n, k)
+        device.gemv(q, w, xd, yd, n, k)
         device.synchronize()
         y = yd.to_host(np.float32)
-        oracle_check(y, raw, x, n, k, f"default {n}x{k}")
-        cfg = device.gemv_tuned("Q4_K", w, xd, yd, n, k)
+        oracle_check(y, raw, x, n, k, f"default {q} {n}x{k}", q=q)
+        cfg = device.gemv_tuned(q, w, xd, yd, n, k)
         device.synchronize()
         assert cfg["kernel"] == _lib.GEMV_MX and 6 <= cfg["rows"] <= 16
         assert bits_equal(yd.to_host(np.float32), y)
@@ -100,34 +121,46 @@ def _x_cases(k, rng):
     }
 
 
-def test_mx_x_ranges(frq):
+@pytest.mark.parametrize("q", ["Q4_K", "Q6_K"])
+def test_mx_x_ranges(frq, q):
     n, k = 48, 4096
-    raw = synth.make_blocks("Q4_K", n, k, seed=11)
+    raw = synth.make_blocks(q, n, k, seed=11)
     rng = np.random.default_rng(5)
     for name, x in _x_cases(k, rng).items():
-        y, _ = run_mx(raw, x, n, k)
+        y, _ = run_mx(raw, x, n, k, q=q)
         if name == "zeros":
             assert np.array_equal(y, np.zeros(n, np.float32))
             continue
         if name == "subnormal":
             # products and sums of ~1e-40 sit in the fp32 subnormal range for
             # every kernel; the check is that the scale round-trips (no zeroing)
-            y64 = G.matmul_f64("Q4_K", x, raw, n, k)
+            y64 = G.matmul_f64(q, x, raw, n, k)
             assert np.all(np.isfinite(y)) and np.max(np.abs(y - y64)) <= 1e-3 * np.max(np.abs(y64))
             continue
-        oracle_check(y, raw, x, n, k, f"x {name}")
+        oracle_check(y, raw, x, n, k, f"{q} x {name}", q=q)
 
 
-def test_mx_nonfinite_x_gives_nonfinite_y(frq):
+@pytest.mark.parametrize("q", ["Q4_K", "Q6_K"])
+def test_mx_nonfinite_x_gives_nonfinite_y(frq, q):
     """Outside the contract (finite inputs); documented behaviour: every row
     whose dot product meets an inf or NaN comes out inf or NaN."""
     n, k = 20, 1024
-    raw = synth.make_blocks("Q4_K", n, k, seed=2)
+    raw = synth.make_blocks(q, n, k, seed=2)
     for bad in (np.inf, -np.inf, np.nan):
         x = synth.make_x(k, seed=4)
         x[300] = bad
-        y, _ = run_mx(raw, x, n, k)
+        y, _ = run_mx(raw, x, n, k, q=q)
         assert not np.any(np.isfinite(y)), bad
+
+
+@pytest.mark.parametrize("n,k", [(4096, 14336), (3584, 3584)])
+def test_mx_q6_k_full_size_forced(frq, n, k):
+    """The Q6_K matrix-core kernel at the Llama down / Qwen q shapes, forced."""
+    raw = synth.make_blocks("Q6_K", n, k, seed=n + k)
+    x = synth.make_x(k, seed=k + 5)
+    y, cfg = run_mx(raw, x, n, k, q="Q6_K")
+    assert cfg["kernel"] == _lib.GEMV_MX
+    oracle_check(y, raw, x, n, k, f"Q6_K {n}x{k}", q="Q6_K")
 
 
 def test_mx_repeat_and_graph_replay(frq):
@@ -190,17 +223,21 @@ def test_mx_rejects(frq):
     w = device.DeviceBuffer.from_host(raw)
     xd = device.DeviceBuffer(4 * 256 * 81)
     yd = device.DeviceBuffer(64)
-    q6 = device.DeviceBuffer.from_host(synth.make_blocks("Q6_K", 4, 512, seed=1))
+    q5 = device.DeviceBuffer.from_host(synth.make_blocks("Q5_K", 4, 512, seed=1))
+    q6 = device.DeviceBuffer.from_host(synth.make_blocks("Q6_K", 4, 256 * 65, seed=1))
     try:
         with pytest.raises(RuntimeError):                      # 81 blocks: beyond 16 waves x 5 blocks
             device.gemv_tuned("Q4_K", w, xd, yd, 4, 256 * 81, kernel=_lib.GEMV_MX)
+        with pytest.raises(RuntimeError):                      # Q6_K: 65 blocks, beyond 16 waves x 4 blocks
+            device.gemv_tuned("Q6_K", q6, xd, yd, 4, 256 * 65, kernel=_lib.GEMV_MX)
         with pytest.raises(RuntimeError):                      # rows per workgroup above 16
             device.gemv_tuned("Q4_K", w, xd, yd, 4, 256, kernel=_lib.GEMV_MX, rows=17, w_bytes=4 * 144)
-        with pytest.raises(RuntimeError):                      # Q4_K only
-            device.gemv_tuned("Q6_K", q6, xd, yd, 4, 512, kernel=_lib.GEMV_MX)
-        # the default path still serves k beyond the matrix-core limit
+        with pytest.raises(RuntimeError):                      # Q4_K and Q6_K only
+            device.gemv_tuned("Q5_K", q5, xd, yd, 4, 512, kernel=_lib.GEMV_MX)
+        # the default path still serves k beyond the matrix-core limits
         device.gemv("Q4_K", w, xd, yd, 4, 256 * 81)
+        device.gemv("Q6_K", q6, xd, yd, 4, 256 * 65)
         device.synchronize()
     finally:
-        for b in (w, xd, yd, q6):
+        for b in (w, xd, yd, q5, q6):
             b.free()
