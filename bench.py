@@ -67,8 +67,9 @@ def effective_bytes(q: str, n: int, k: int, batch: int = 1) -> int:
 class GemvWorkload:
     """Rotating device copies of one seeded weight, x and y resident in HBM."""
 
-    def __init__(self, q: str, n: int, k: int, seed: int, stream, rotate_bytes: int = ROTATE_BYTES):
-        self.q, self.n, self.k = q, n, k
+    def __init__(self, q: str, n: int, k: int, seed: int, stream, rotate_bytes: int = ROTATE_BYTES,
+                 kernel: int | None = None):
+        self.q, self.n, self.k, self.kernel = q, n, k, kernel
         self.raw = synth.make_blocks(q, n, k, seed=seed)
         self.ncopies = max(2, math.ceil(rotate_bytes / self.raw.nbytes))
         self.w = [device.DeviceBuffer.from_host(self.raw) for _ in range(self.ncopies)]
@@ -81,8 +82,12 @@ class GemvWorkload:
         device.synchronize()
 
     def launch(self, i: int) -> None:
-        device.gemv(self.q, self.w[i % self.ncopies], self.x, self.y, self.n, self.k, stream=self.stream,
-                    w_bytes=self.raw.nbytes)
+        if self.kernel is None:
+            device.gemv(self.q, self.w[i % self.ncopies], self.x, self.y, self.n, self.k, stream=self.stream,
+                        w_bytes=self.raw.nbytes)
+        else:
+            device.gemv_tuned(self.q, self.w[i % self.ncopies], self.x, self.y, self.n, self.k, kernel=self.kernel,
+                              stream=self.stream, w_bytes=self.raw.nbytes)
 
     def result(self) -> np.ndarray:
         device.synchronize()
@@ -170,12 +175,16 @@ def cpu_baseline(work: GemvWorkload, y_gpu: np.ndarray, seconds: float) -> dict:
     }
 
 
+# (name, quant, out, in, kernel): kernel None = the default device path;
+# GEMV_ROWS forces the element-wise fp32 kernel (dequant and dot in one pass)
 SUITE = [
-    ("q8_0_4864x896", "Q8_0", 4864, 896),
-    ("q4_k_18944x3584", "Q4_K", 18944, 3584),
-    ("q4_k_3584x18944", "Q4_K", 3584, 18944),
-    ("q6_k_152064x3584", "Q6_K", 152064, 3584),
-    ("q1_0_4096x4096", "Q1_0", 4096, 4096),
+    ("q8_0_4864x896", "Q8_0", 4864, 896, None),
+    ("q4_k_18944x3584", "Q4_K", 18944, 3584, None),
+    ("q4_k_3584x18944", "Q4_K", 3584, 18944, None),
+    ("q4_k_3584x18944_elementwise", "Q4_K", 3584, 18944, _lib.GEMV_ROWS),
+    ("q4_k_18944x3584_elementwise", "Q4_K", 18944, 3584, _lib.GEMV_ROWS),
+    ("q6_k_152064x3584", "Q6_K", 152064, 3584, None),
+    ("q1_0_4096x4096", "Q1_0", 4096, 4096, None),
 ]
 
 # Llama-3-8B Q4_K_M projection mix: (name, quant, out, in)
@@ -191,10 +200,10 @@ def run_suite(stream, steps: int, only: set | None = None) -> dict:
     def want(name: str) -> bool:
         return not only or name in only
 
-    for idx, (name, q, n, k) in enumerate(SUITE):
+    for idx, (name, q, n, k, kernel) in enumerate(SUITE):
         if not want(name):
             continue
-        w = GemvWorkload(q, n, k, seed=100 + idx, stream=stream)
+        w = GemvWorkload(q, n, k, seed=100 + idx, stream=stream, kernel=kernel)
         t = w.time_throughput(steps, warmup=10)
         te = w.time_eager(min(steps, 200))
         tk = t / steps
