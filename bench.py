@@ -539,7 +539,7 @@ def main() -> int:
                          "(reference traffic for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU (the matvec path is single-device); "
+        print("bench.py: measures one GPU (the matvec path is single-device); "
               f"--gpus {a.gpus} is not supported", file=sys.stderr)
         return 2
     _lib.lib()

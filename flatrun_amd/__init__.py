@@ -58,7 +58,7 @@ def version() -> str:
 
 
 def is_neon() -> bool:
-    """Always False: this build targets gfx950, not ARM NEON."""
+    """Always False: the library targets gfx950, not ARM NEON."""
     return False
 
 

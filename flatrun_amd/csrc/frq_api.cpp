@@ -195,7 +195,7 @@ int host_matmul(int qtype, const float* x, size_t seq, const uint8_t* weight, si
     }
     if (int rc = have_device()) return rc;
     if (!frq::gemv_sk_supported(qtype) && !frq::gemv_supported(qtype, (int64_t)n, (int64_t)k))
-        return fail(FRQ_ERR_UNSUPPORTED, "matmul: k=%zu is beyond the single-workgroup row limit of this build", k);
+        return fail(FRQ_ERR_UNSUPPORTED, "matmul: k=%zu is beyond the single-workgroup row limit of this library", k);
     std::lock_guard<std::mutex> lk(g_ws.mu);
     const size_t wb = align256(weight_bytes), xb = align256(seq * k * 4), yb = align256(seq * n * 4);
     void* base = nullptr;
@@ -372,7 +372,7 @@ static int dev_gemv_checks(int qtype, const void* w, size_t w_bytes, const float
     if (!w || !x || !y) return fail(FRQ_ERR_INVALID, "null buffer");
     if (int rc = check_dev_ptrs(qtype, w, x, y)) return rc;
     if (k > 0 && !frq::gemv_sk_supported(qtype) && !frq::gemv_supported(qtype, n, k))
-        return fail(FRQ_ERR_UNSUPPORTED, "%s matmul: k=%lld is beyond the single-workgroup row limit of this build",
+        return fail(FRQ_ERR_UNSUPPORTED, "%s matmul: k=%lld is beyond the single-workgroup row limit of this library",
                     f->name, (long long)k);
     return FRQ_OK;
 }
@@ -517,7 +517,7 @@ static int gemm_checks(int qtype, size_t w_bytes, int64_t m, int64_t n, int64_t 
     if ((int64_t)w_bytes != n * (k / f->belems) * f->bbytes)
         return fail(FRQ_ERR_SIZE, "%s gemm: weight byte size mismatch", f->name);
     if (m > 0 && n > 0 && k > 0 && !frq::gemm_bf16_supported(qtype, m, n, k))
-        return fail(FRQ_ERR_UNSUPPORTED, "%s gemm: shape beyond this build's limits", f->name);
+        return fail(FRQ_ERR_UNSUPPORTED, "%s gemm: shape beyond this library's limits", f->name);
     return FRQ_OK;
 }
 

@@ -4,8 +4,7 @@
  * Plain pointers and sizes only; no exceptions cross this boundary. Every
  * entry point returns an frq_status; on failure frq_last_error() returns a
  * thread-local message. Python reaches the library through ctypes
- * (flatrun_amd/_lib.py); the binding a reference maintainer would add is in
- * INTEGRATION.md.
+ * (flatrun_amd/_lib.py).
  *
  * Two families:
  *
@@ -51,7 +50,7 @@ typedef enum {
     FRQ_ERR_INVALID = 1,      /* bad argument (null pointer, unknown type, ...) */
     FRQ_ERR_SHAPE = 2,        /* shape / ndim rule of _C.cpp violated          */
     FRQ_ERR_SIZE = 3,         /* weight byte count does not match (n, k)       */
-    FRQ_ERR_UNSUPPORTED = 4,  /* valid request this build does not plan         */
+    FRQ_ERR_UNSUPPORTED = 4,  /* valid request this library does not plan       */
     FRQ_ERR_NO_DEVICE = 5,    /* no HIP device visible                          */
     FRQ_ERR_HIP = 6,          /* HIP runtime error                              */
     FRQ_ERR_ALIGN = 7         /* device pointer misaligned for its format       */
@@ -65,7 +64,7 @@ enum { FRQ_Q4_0 = 2, FRQ_Q5_0 = 6, FRQ_Q5_1 = 7, FRQ_Q8_0 = 8, FRQ_Q4_K = 12, FR
 /* Build identifier. Replaces _C.version (_C.cpp:449-451). */
 const char* frq_version(void);
 
-/* Always 0: this build has no NEON path. Replaces _C.is_neon (_C.cpp:441-447). */
+/* Always 0: this library has no NEON path. Replaces _C.is_neon (_C.cpp:441-447). */
 int frq_is_neon(void);
 
 /* Message of the last failed call on this thread ("" if none). */

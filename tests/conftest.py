@@ -19,7 +19,7 @@ if str(ROOT) not in sys.path:
 
 GOLDEN = ROOT / "tests" / "golden"
 
-# Matvec tolerance of the north-star contract: max relative error 1e-5 with
+# Matvec tolerance of the contract: max relative error 1e-5 with
 # fp32 accumulation, measured normwise (max|dy| / max|y|) and componentwise
 # (|dy_i| / sum_j |w_ij x_j|) against the fp64 oracle and the NumPy matvec.
 MATVEC_RTOL = 1e-5

@@ -1,6 +1,6 @@
 """The matrix-core Q4_K / Q6_K GEMVs (int8 MFMA; frq_gemv_mx.hip) against the oracle.
 
-Contract: the north-star matvec tolerance (1e-5 normwise and componentwise
+Contract: the matvec tolerance (1e-5 normwise and componentwise
 against the fp64 oracle); bits independent of the rows-per-workgroup choice
 and of launch order (fixed per-row summation order); the default device path
 takes the Q4_K kernel for n > 1280 and k <= 20480 (the Q6_K kernel, k <=
