@@ -51,6 +51,18 @@ ROTATE_BYTES = 1 << 30         # >= 1 GiB of distinct copies per workload
 TRAFFIC_FILE = ROOT / "profiles" / "q4_k_gemv_3584x18944.traffic.json"
 
 
+GEMM_COUNTERS_FILE = ROOT / "profiles" / "q4_k_gemm_bf16_512x14336x4096.counters.json"
+
+
+def measured_mfma_util() -> float | None:
+    """MFMA busy percentage of the prefill GEMM, from the committed rocprofv3
+    SQ_VALU_MFMA_BUSY_CYCLES / GRBM_GUI_ACTIVE summary, if present."""
+    try:
+        return round(float(json.loads(GEMM_COUNTERS_FILE.read_text())["derived"]["mfma_util_pct"]), 1)
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def measured_traffic() -> int | None:
     """HBM bytes per launch of the headline kernel, from the committed
     rocprofv3 FETCH_SIZE + WRITE_SIZE summary (copy-calibrated), if present."""
@@ -332,7 +344,8 @@ def prefill_gemm(stream, m: int = 512, n: int = 14336, k: int = 4096, reps: int 
     yd.free()
     flop = 2 * m * n * k
     return {"us": round(us, 2), "tflops": round(flop / us / 1e6, 1), "flop": flop,
-            "frac_bf16_peak": round(flop / us / 1e6 / BF16_PEAK_TFLOPS, 4), "peak_tflops": BF16_PEAK_TFLOPS}
+            "frac_bf16_peak": round(flop / us / 1e6 / BF16_PEAK_TFLOPS, 4), "peak_tflops": BF16_PEAK_TFLOPS,
+            "mfma_busy_pct_profiled": measured_mfma_util()}
 
 
 def prefill_layer(stream, m: int = 512, reps: int = 5) -> dict:

@@ -1,11 +1,20 @@
 """Summaries of rocprofv3 output for the GEMV kernels.
 
     python -m flatrun_amd.profiling trace  <results.db> [--match SUBSTR]
+    python -m flatrun_amd.profiling counters <results.db> [--match SUBSTR]
     python -m flatrun_amd.profiling traffic --fetch <fetch.db> --write <write.db>
             --match SUBSTR [--copy-bytes N]
 
 ``trace`` reads a ``rocprofv3 --kernel-trace`` database and prints, per
 kernel, the dispatch count and the mean / median / min duration.
+
+``counters`` reads one ``rocprofv3 --pmc`` database of SQ / GRBM counters and
+prints, per matched kernel, the mean counters per dispatch and the derived
+figures rocprofv3 defines for them: MFMA utilization
+(``SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * SIMDs)``), bf16 MFMA FLOPs
+(``SQ_INSTS_VALU_MFMA_MOPS_BF16 * 512``), LDS utilization and bank-conflict
+share (per CU), and mean waves per CU. GRBM counters are reduced by max over
+their instances (XCDs), SQ counters by sum, as those definitions do.
 
 ``traffic`` reads two ``rocprofv3 --pmc`` databases (one collected with
 ``FETCH_SIZE``, one with ``WRITE_SIZE``; both in KiB per dispatch, summed over
@@ -62,6 +71,44 @@ def pmc_means(db: str) -> dict[str, dict[str, float]]:
     return {k: {c: statistics.fmean(v) for c, v in d.items()} for k, d in acc.items()}
 
 
+CU_NUM, SIMD_NUM = 256, 1024          # MI355X
+
+
+def pmc_reduced(db: str) -> dict[str, dict[str, float]]:
+    """Kernel name -> {counter: mean per dispatch}, instances summed (SQ) or
+    reduced by max (GRBM)."""
+    con = sqlite3.connect(db)
+    disp = _dispatches(con)
+    counters = {r[0]: r[1] for r in con.execute("select id, name from rocpd_info_pmc")}
+    per_event: dict[int, dict[str, float]] = collections.defaultdict(dict)
+    for eid, pid, val in con.execute("select event_id, pmc_id, value from rocpd_pmc_event"):
+        c = counters.get(pid, str(pid))
+        d = per_event[eid]
+        d[c] = max(d.get(c, val), val) if c.startswith("GRBM_") else d.get(c, 0.0) + val
+    acc: dict[str, dict[str, list[float]]] = collections.defaultdict(lambda: collections.defaultdict(list))
+    for eid, (name, _) in disp.items():
+        for c, v in per_event.get(eid, {}).items():
+            acc[name][c].append(v)
+    return {k: {c: statistics.fmean(v) for c, v in d.items()} for k, d in acc.items()}
+
+
+def derived(c: dict[str, float]) -> dict[str, float]:
+    out = {}
+    gui = c.get("GRBM_GUI_ACTIVE")
+    if gui:
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+            out["mfma_util_pct"] = 100.0 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui * SIMD_NUM)
+        if "SQ_LDS_IDX_ACTIVE" in c:
+            out["lds_util_pct"] = 100.0 * c["SQ_LDS_IDX_ACTIVE"] / (gui * CU_NUM)
+        if "SQ_LDS_BANK_CONFLICT" in c:
+            out["lds_bank_conflict_pct"] = 100.0 * c["SQ_LDS_BANK_CONFLICT"] / (gui * CU_NUM)
+        if "SQ_WAVE_CYCLES" in c:
+            out["waves_per_cu"] = 4.0 * c["SQ_WAVE_CYCLES"] / (gui * CU_NUM)
+    if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in c:
+        out["mfma_bf16_flop"] = c["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0
+    return out
+
+
 def _pick(table: dict, match: str) -> str:
     hits = [k for k in table if match in k]
     if len(hits) != 1:
@@ -90,6 +137,9 @@ def main(argv=None) -> int:
     t = sub.add_parser("trace")
     t.add_argument("db")
     t.add_argument("--match", default="")
+    cn = sub.add_parser("counters")
+    cn.add_argument("db")
+    cn.add_argument("--match", default="")
     tr = sub.add_parser("traffic")
     tr.add_argument("--fetch", required=True)
     tr.add_argument("--write", required=True)
@@ -104,6 +154,10 @@ def main(argv=None) -> int:
         print(f"{'kernel':72s} {'n':>6s} {'mean_us':>9s} {'median_us':>9s} {'min_us':>8s}")
         for mean, name, d in sorted(rows, reverse=True):
             print(f"{name[:72]:72s} {len(d):6d} {mean:9.3f} {statistics.median(d):9.3f} {min(d):8.3f}")
+    elif a.cmd == "counters":
+        table = pmc_reduced(a.db)
+        out = {name: {"counters": c, "derived": derived(c)} for name, c in table.items() if a.match in name}
+        print(json.dumps(out, indent=1))
     else:
         print(json.dumps(traffic(a.fetch, a.write, a.match, a.copy_bytes), indent=1))
     return 0
