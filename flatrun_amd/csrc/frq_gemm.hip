@@ -45,6 +45,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBM = 256, kBN = 128, kBK = 64;
+constexpr int kGemmValuPerMfma = 5;   // dequant VALU ops placed after each MFMA of a K-step
 constexpr int kLds = kBK + 8;   // bf16 per LDS row
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
@@ -76,12 +77,20 @@ struct WFmt<kTypeQ4K> {
     }
     __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq) {
         const int g = (kb >> 6) & 3;
-        uint32_t sc0, mn0, sc1, mn1;
-        k4_scale_min(r.h[1], r.h[2], r.h[3], 2 * g, sc0, mn0);
-        k4_scale_min(r.h[1], r.h[2], r.h[3], 2 * g + 1, sc1, mn1);
+        // scale/min pairs 2g, 2g+1 (get_scale_min_k4, gguf.py:135-163) without a
+        // branch, so the K-step stays one block the scheduler can interleave:
+        // bytes o, o+1 of scales[0..3] and [4..7] (g < 2), or the nibbles of
+        // scales[8 + o], [9 + o] with their high bits (g >= 2), o = 2 (g % 2)
+        const uint32_t o = 2u * (uint32_t)(g & 1);
+        const uint32_t P = __builtin_amdgcn_perm(r.h[2], r.h[1], o | ((o + 1) << 8) | ((o + 4) << 16) | ((o + 5) << 24));
+        const uint32_t Q = __builtin_amdgcn_perm(r.h[3], r.h[3], o | ((o + 1) << 8) | (o << 16) | ((o + 1) << 24));
+        const uint32_t lo4 = (Q & 0x00000F0Fu) | ((Q >> 4) & 0x0F0F0000u);
+        const uint32_t lowsel = 0u - (uint32_t)(g < 2);   // all ones for g < 2: a blend, not a branch
+        const uint32_t scm = ((P & 0x3F3F3F3Fu) & lowsel) |
+                             ((lo4 | ((P >> 2) & 0x30303030u)) & ~lowsel);
         const float d = f16_bits_to_f32(r.h[0]), dmin = f16_bits_to_f32(r.h[0] >> 16);
-        const float s0 = d * (float)sc0, t0 = dmin * (float)mn0;
-        const float s1 = d * (float)sc1, t1 = dmin * (float)mn1;
+        const float s0 = d * byte_f(scm, 0), t0 = dmin * byte_f(scm, 2);
+        const float s1 = d * byte_f(scm, 1), t1 = dmin * byte_f(scm, 3);
         const uint32_t qw[2] = {r.q[0], r.q[1]};
         uint32_t lo[4], hi[4];
 #pragma unroll
@@ -281,6 +290,27 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
             load_tile(st[j], kt + 2 < last ? kt + 2 : last);
             compute(j);
             store_tile(st[j ^ 1], j ^ 1, kt + 1 < last ? kt + 1 : last);
+            // Order for the scheduler: the loads for t + 2 first, then this
+            // step's 16 MFMAs with the next step's dequant arithmetic between
+            // them (the wave's other SIMD partner is in the same phase, so
+            // only this interleave keeps the matrix core and the VALU both
+            // busy), the fragment reads of each 16-k slice ahead of its
+            // MFMAs, and the LDS writes of step t + 1 last.
+            __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);   // global loads
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // fragments of k-slice 0
+            static_for<0, kBK / 16>([&](auto kc) {
+                constexpr int kk = decltype(kc)::value;
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kGemmValuPerMfma, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kGemmValuPerMfma, 0);
+                if constexpr (kk + 1 < kBK / 16) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kGemmValuPerMfma, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kGemmValuPerMfma, 0);
+            });
+            __builtin_amdgcn_sched_group_barrier(0x200, 6, 0);   // LDS writes for t + 1
             __syncthreads();
         });
     }
