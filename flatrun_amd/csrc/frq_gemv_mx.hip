@@ -81,8 +81,11 @@ __device__ __forceinline__ XDigits x_digits(float4 v) {
     r.s32 = sx + dpp_mov<0x141>(sx);               // 8 lanes = 32 elements
     const int e = __builtin_amdgcn_frexp_expf(__uint_as_float(mx));   // max |x| < 2^e (0 for 0)
     const int sh = 30 - e;
-    const int m0 = (int)__builtin_ldexpf(v.x, sh), m1 = (int)__builtin_ldexpf(v.y, sh);
-    const int m2 = (int)__builtin_ldexpf(v.z, sh), m3 = (int)__builtin_ldexpf(v.w, sh);
+    // |x| 2^(30-e) < 2^30 for finite x; the clamp (one v_med3) only keeps the
+    // conversion defined for inf / NaN, whose sums already make y non-finite
+    constexpr float kLim = 1073741824.0f;
+    auto digit_int = [&](float a) { return (int)__builtin_amdgcn_fmed3f(__builtin_ldexpf(a, sh), -kLim, kLim); };
+    const int m0 = digit_int(v.x), m1 = digit_int(v.y), m2 = digit_int(v.z), m3 = digit_int(v.w);
     // m = sum_i digit_i 256^i with digit_i = byte_i(m + 0x808080) - 128
     // (i < 3) and digit_3 = byte_3(m + 0x808080) as a signed byte
     const uint32_t u0 = (uint32_t)m0 + 0x808080u, u1 = (uint32_t)m1 + 0x808080u;
