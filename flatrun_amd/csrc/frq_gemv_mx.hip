@@ -20,14 +20,17 @@
 // length; wave w owns blocks [w L, w L + L) of every row. Per wave:
 //   1. the x of its blocks is loaded first, then 3 x 16 B of every row's
 //      block per lane: lane (c = l & 15, g = l >> 4) takes row c's header and
-//      qs bytes 32g .. 32g+31, whose low nibbles are sub-block 2g and high
-//      nibbles sub-block 2g+1;
+//      qs bytes 16g .. 16g+15 and 64+16g .. 64+16g+15, so that each load
+//      instruction reads 64 contiguous bytes of each of its 16 rows;
 //   2. the x digits go to a wave-private LDS table (lane t splits x[4t..4t+3]
 //      of each block; eight lanes share a sub-block's max and sum via DPP);
-//   3. four MFMAs per block: A = the digits, block-diagonal (row group g of A
-//      is nonzero only in k-group g, so lane (c, g) receives the digit sums of
-//      its own 16-byte groups), B = the nibbles as int8; the per-row epilogue
-//      applies the scales;
+//   3. four MFMAs per block, chained in pairs: A = the digits, B = the nibbles
+//      as int8. qs bytes 32p .. 32p+31 hold sub-block 2p in their low and
+//      2p+1 in their high nibbles, so k-groups 0, 1 of the first load carry
+//      sub-blocks 0 (low) and 1 (high), k-groups 2, 3 sub-blocks 2 and 3. A
+//      row r of A is nonzero only in the two k-groups of sub-block r / 4, so
+//      lane (c, g) receives the digit sums of sub-block g (first pair) and
+//      4 + g (second pair); the per-row epilogue applies the scales;
 //   4. one LDS reduction over waves and k-groups, in a fixed order.
 // No barrier separates the waves between the loads and the reduction: the
 // only shared LDS data (a zero block that the inactive A lanes read) is
@@ -150,18 +153,21 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
         const int jj = j < lw ? j : lw - 1;
         const uint32_t off = roff + (uint32_t)(b0 + jj) * kQ4KBytes;
         hd[j] = bload_b128(rs, off);
-        q0[j] = bload_b128(rs, off + 16 + 32 * g);
-        q1[j] = bload_b128(rs, off + 32 + 32 * g);
+        q0[j] = bload_b128(rs, off + 16 + 16 * g);
+        q1[j] = bload_b128(rs, off + 80 + 16 * g);
     }
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- x -> digits. Lane t: x[4t .. 4t+3] of the block = sub-block s = t / 8,
     // half h = (t / 4) % 2, bytes 4 (t % 4) .. +3 of the 16-element group.
-    // Table entry (hi, h, g) (hi = s % 2, g = s / 2) holds 4 digits x 16 bytes.
+    // MFMA m = 2 (s / 4) + s % 2 (load s / 4, low or high nibbles) reads the
+    // group in k-group kk = 2 ((s / 2) % 2) + h; table entry (m, kk) holds
+    // 4 digits x 16 bytes. The (exponent, sum) table is ordered [s % 4][s / 4].
     {
-        const int s = lane >> 3, hi = s & 1, gg = s >> 1, h = (lane >> 2) & 1;
-        uint8_t* wl = lds + wave * kWaveLimb + ((hi * 2 + h) * 4 + gg) * 64 + 4 * (lane & 3);
-        float* wt = tab + wave * LMAX * kMxTabBlock + 2 * s;
+        const int s = lane >> 3, h = (lane >> 2) & 1;
+        const int m = 2 * (s >> 2) + (s & 1), kk = 2 * ((s >> 1) & 1) + h;
+        uint8_t* wl = lds + wave * kWaveLimb + (m * 4 + kk) * 64 + 4 * (lane & 3);
+        float* wt = tab + wave * LMAX * kMxTabBlock + 4 * (s & 3) + 2 * (s >> 2);
 #pragma unroll
         for (int j = 0; j < LMAX; ++j) {
             const XDigits dg = x_digits(xv[j]);
@@ -175,26 +181,28 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
     }
 
     // ---- products. A lane of the A operand (row r = l & 15 of A, k-group
-    // l >> 4) carries digit r % 4 of k-group r / 4 when r / 4 == l >> 4, and
-    // zeros otherwise; the digit table and the zero block are read at the
-    // same per-MFMA offsets.
-    const bool act = ((lane & 15) >> 2) == (lane >> 4);
-    const uint8_t* abase = act ? lds + wave * kWaveLimb + (lane >> 4) * 64 + (lane & 3) * 16 : lds + kLimbAll;
+    // kk = l >> 4) of MFMA m carries digit r % 4 of its k-group when
+    // r / 4 == 2 (kk / 2) + m % 2, and zeros otherwise; the digit table and
+    // the zero block are read at the same per-MFMA offsets.
+    const int ar = lane & 15, akk = lane >> 4;
+    const uint8_t* atab = lds + wave * kWaveLimb + akk * 64 + (ar & 3) * 16;
+    const uint8_t* abase_lo = ((ar >> 2) == 2 * (akk >> 1)) ? atab : lds + kLimbAll;       // m = 0, 2
+    const uint8_t* abase_hi = ((ar >> 2) == 2 * (akk >> 1) + 1) ? atab : lds + kLimbAll;   // m = 1, 3
     const float* tb = tab + wave * LMAX * kMxTabBlock + 4 * g;
-    // scale pairs 2g, 2g+1 (get_scale_min_k4, gguf.py:135-163): bytes o, o+1
-    // of scales[0..3] / [4..7] (g < 2), plus the low / high nibbles of
-    // scales[8 + o], [9 + o] (g >= 2), o = 2 (g % 2)
-    const uint32_t o = 2u * (uint32_t)(g & 1);
-    const uint32_t selp = o | ((o + 1) << 8) | ((o + 4) << 16) | ((o + 5) << 24);
-    const uint32_t selq = o | ((o + 1) << 8) | (o << 16) | ((o + 1) << 24);
+    // sub-blocks g and 4 + g (get_scale_min_k4, gguf.py:135-163): with
+    // y, z, w = scales[g], scales[4 + g], scales[8 + g],
+    // sc_g = y & 63, m_g = z & 63, sc_4+g = (w & 15) | (y >> 6) << 4,
+    // m_4+g = (w >> 4) | (z >> 6) << 4
+    const uint32_t sh8 = 8u * (uint32_t)g;
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < LMAX; ++j) {
-        const uint8_t* ab = abase + j * kMxLimbBlock;
-        const i32x4 A00 = *reinterpret_cast<const i32x4*>(ab + 0);     // low nibbles, bytes 0..15
-        const i32x4 A01 = *reinterpret_cast<const i32x4*>(ab + 256);   // low nibbles, bytes 16..31
-        const i32x4 A10 = *reinterpret_cast<const i32x4*>(ab + 512);   // high nibbles, bytes 0..15
-        const i32x4 A11 = *reinterpret_cast<const i32x4*>(ab + 768);   // high nibbles, bytes 16..31
+        const uint8_t* alo = abase_lo + j * kMxLimbBlock;
+        const uint8_t* ahi = abase_hi + j * kMxLimbBlock;
+        const i32x4 A0 = *reinterpret_cast<const i32x4*>(alo + 0);     // first load, low nibbles
+        const i32x4 A1 = *reinterpret_cast<const i32x4*>(ahi + 256);   // first load, high nibbles
+        const i32x4 A2 = *reinterpret_cast<const i32x4*>(alo + 512);   // second load, low nibbles
+        const i32x4 A3 = *reinterpret_cast<const i32x4*>(ahi + 768);   // second load, high nibbles
         const uint4 a = q0[j], b = q1[j];
         const i32x4 lo0 = {(int)(a.x & 0x0F0F0F0Fu), (int)(a.y & 0x0F0F0F0Fu), (int)(a.z & 0x0F0F0F0Fu),
                            (int)(a.w & 0x0F0F0F0Fu)};
@@ -205,19 +213,17 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
         const i32x4 hi1 = {(int)((b.x >> 4) & 0x0F0F0F0Fu), (int)((b.y >> 4) & 0x0F0F0F0Fu),
                            (int)((b.z >> 4) & 0x0F0F0F0Fu), (int)((b.w >> 4) & 0x0F0F0F0Fu)};
         const i32x4 z = {0, 0, 0, 0};
-        i32x4 sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A00, lo0, z, 0, 0, 0);
-        sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A01, lo1, sl, 0, 0, 0);
-        i32x4 sh = __builtin_amdgcn_mfma_i32_16x16x64_i8(A10, hi0, z, 0, 0, 0);
-        sh = __builtin_amdgcn_mfma_i32_16x16x64_i8(A11, hi1, sh, 0, 0, 0);
+        i32x4 sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, lo0, z, 0, 0, 0);
+        sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, hi0, sl, 0, 0, 0);    // sub-block g
+        i32x4 sh = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, lo1, z, 0, 0, 0);
+        sh = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, hi1, sh, 0, 0, 0);    // sub-block 4 + g
 
         const uint4 hdj = hd[j];
         const float d = f16_bits_to_f32(hdj.x), dm = f16_bits_to_f32(hdj.x >> 16);
-        const uint32_t P = perm(hdj.z, hdj.y, selp), Q = perm(hdj.w, hdj.w, selq);
-        const uint32_t lo4 = (Q & 0x00000F0Fu) | ((Q >> 4) & 0x0F0F0000u);
-        const uint32_t scm = (g < 2) ? (P & 0x3F3F3F3Fu) : (lo4 | ((P >> 2) & 0x30303030u));
-        const float sc0 = (float)(scm & 0xFF), sc1 = (float)((scm >> 8) & 0xFF);
-        const float mn0 = (float)((scm >> 16) & 0xFF), mn1 = (float)(scm >> 24);
-        const float4 t = *reinterpret_cast<const float4*>(tb + j * kMxTabBlock);   // e0-30, sum0, e1-30, sum1
+        const uint32_t yb = (hdj.y >> sh8) & 0xFFu, zb = (hdj.z >> sh8) & 0xFFu, wb = (hdj.w >> sh8) & 0xFFu;
+        const float sc0 = (float)(yb & 63u), mn0 = (float)(zb & 63u);
+        const float sc1 = (float)((wb & 15u) | ((yb >> 6) << 4)), mn1 = (float)((wb >> 4) | ((zb >> 6) << 4));
+        const float4 t = *reinterpret_cast<const float4*>(tb + j * kMxTabBlock);   // sub-blocks g, 4+g: (e - 30, sum x)
         const float vl = digit_sum(sl), vh = digit_sum(sh);
         float part = __builtin_ldexpf(vl, __float_as_int(t.x)) * (d * sc0);
         part = __builtin_fmaf(-(dm * mn0), t.y, part);
