@@ -17,13 +17,17 @@ Printed: ONE JSON line with
              per launch / mean launch duration over the same timed region;
   eager_launch_us  mean time per launch when each launch is issued from
              Python one by one (host-bound for kernels this short);
+  read_ceiling  the same weight copies read by the library's plain streaming
+             read kernel, graph-replayed the same way: the time any kernel
+             that reads those bytes once per launch needs here, and the
+             GEMV's time over it;
   cpu_baseline  the reference's native scalar matmul (its own _C module built
              from its sources, 1 thread) on the same bytes, timed on the host
              for a bounded number of full-shape repetitions; plus the NumPy path;
   configs    every other benchmark workload (GB/s, mean kernel us, fraction of
              HBM peak), the Llama-3-8B decode-step weight sweep (ms/step,
              graph replay and eager; resident and streamed), the prefill
-             GEMM, the copy ceiling, and a GGUF file -> HBM load.
+             GEMM, the copy and read ceilings, and a GGUF file -> HBM load.
 """
 
 from __future__ import annotations
@@ -229,6 +233,7 @@ def run_suite(stream, steps: int, only: set | None = None) -> dict:
              ("llama3_8b_prefill_layer_512", lambda: prefill_layer(stream)),
              ("dequant", lambda: dequant_suite(stream)),
              ("copy_ceiling", lambda: copy_ceiling(stream)),
+             ("read_ceiling_447MB", lambda: read_ceiling(stream, synth.nbytes("Q6_K", 152064, 3584), reps=50)),
              ("gguf_load_llama3_8b_4_layers", lambda: gguf_load(stream)),
              ("host_path_q4_k_3584x18944", host_path_rate)]
     for name, fn in extra:
@@ -451,6 +456,37 @@ def copy_ceiling(stream, mib: int = 512, reps: int = 20) -> dict:
     return {"bytes_moved": 2 * nbytes, "us": round(ms * 1e3, 2), "gbs": round(2 * nbytes / (ms / 1e3) / 1e9, 1)}
 
 
+def read_ceiling(stream, nbytes: int, reps: int = 200, bufs=None) -> dict:
+    """The library's plain streaming read (16 B per lane, XOR-folded, one word
+    written per workgroup) of `nbytes`, one distinct buffer per launch out of
+    >= 1 GiB (`bufs`, or fresh ones), replayed from a graph like the GEMV:
+    the practical ceiling for a kernel that reads `nbytes` once per launch."""
+    nbytes = nbytes // 16 * 16
+    own = bufs is None
+    if own:
+        bufs = [device.DeviceBuffer(nbytes) for _ in range(max(2, math.ceil(ROTATE_BYTES / nbytes)))]
+    out = device.DeviceBuffer(4 * device.READ_XOR_WORDS)
+    reps = max(reps, len(bufs))
+    with device.Graph.capture(stream) as cap:
+        for i in range(reps):
+            device.read_xor(bufs[i % len(bufs)], nbytes, out, stream=stream)
+    cap.launch(stream)
+    device.synchronize()
+    e0, e1 = device.Event(), device.Event()
+    e0.record(stream)
+    cap.launch(stream)
+    e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) * 1e3 / reps
+    cap.destroy()
+    out.free()
+    if own:
+        for b in bufs:
+            b.free()
+    return {"bytes": nbytes, "buffers_rotated": len(bufs), "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
+            "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
 def host_path_rate(reps: int = 20) -> dict:
     """The reference-shaped host entry point (_C.matmul_q4_k: numpy in, numpy
     out, weight and x copied host -> device on every call): PCIe-inclusive."""
@@ -593,6 +629,11 @@ def main() -> int:
                      "kernel_us": round(t_kernel * 1e6, 3)},
         "eager_launch_us": round(t_eager * 1e6, 3),
     }
+    # the same weight copies read by a plain streaming kernel: what any kernel
+    # reading these bytes once per launch can reach on this part
+    rc = read_ceiling(stream, work.raw.nbytes, reps=min(a.steps, 1000), bufs=work.w)
+    rc["gemv_time_over_read_time"] = round(t_kernel * 1e6 / rc["us"], 3)
+    rec["read_ceiling"] = rc
     if a.copy_calibration > 0:
         nbytes = a.copy_calibration << 20
         src, dst = device.DeviceBuffer(nbytes), device.DeviceBuffer(nbytes)

@@ -590,6 +590,16 @@ int frq_dev_copy(void* dst, const void* src, size_t bytes, void* stream) {
     return FRQ_OK;
 }
 
+int frq_dev_read_xor(const void* src, size_t bytes, uint32_t* out, void* stream) {
+    static_assert(FRQ_READ_XOR_WORDS == frq::kReadXorWords, "read_xor word count");
+    if (bytes % 16) return fail(FRQ_ERR_INVALID, "read size must be a multiple of 16 bytes");
+    if ((reinterpret_cast<uintptr_t>(src) & 15) != 0) return fail(FRQ_ERR_ALIGN, "read buffer must be 16-byte aligned");
+    if (!out || (reinterpret_cast<uintptr_t>(out) & 3) != 0) return fail(FRQ_ERR_INVALID, "null or unaligned output words");
+    if (bytes != 0 && !src) return fail(FRQ_ERR_INVALID, "null buffer");
+    FRQ_HIP(frq::launch_read_xor(src, (int64_t)bytes, out, static_cast<hipStream_t>(stream)));
+    return FRQ_OK;
+}
+
 int frq_set_device(int device) { FRQ_HIP(hipSetDevice(device)); return FRQ_OK; }
 int frq_malloc(void** ptr, size_t bytes) {
     if (!ptr) return fail(FRQ_ERR_INVALID, "null ptr");

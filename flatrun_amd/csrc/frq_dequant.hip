@@ -201,6 +201,46 @@ hipError_t launch_copy(void* dst, const void* src, int64_t bytes, hipStream_t st
     return hipGetLastError();
 }
 
+// Plain streaming read: a contiguous slice per workgroup, 16 B per lane and
+// eight loads in flight per lane, folded into a 32-bit XOR; workgroup b
+// stores its XOR in out[b] (no atomics) and workgroup 0 zeroes the words past
+// the grid. The read-only reference point beside copy16: a GEMV reads its
+// weights once and writes almost nothing.
+constexpr int kReadUnroll = 8;
+__global__ void __launch_bounds__(256) read_xor_kernel(const uint4* __restrict__ src, int64_t n16,
+                                                       uint32_t* __restrict__ out) {
+    __shared__ uint32_t red[4];
+    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const int64_t b = (int64_t)blockIdx.x * per;
+    const int64_t e = b + per < n16 ? b + per : n16;
+    uint32_t r = 0;
+    for (int64_t i = b + threadIdx.x; i < e; i += 256 * kReadUnroll) {
+        uint4 v[kReadUnroll];
+#pragma unroll
+        for (int u = 0; u < kReadUnroll; ++u) {
+            const int64_t j = i + 256 * u;
+            v[u] = j < e ? src[j] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < kReadUnroll; ++u) r ^= (v[u].x ^ v[u].y) ^ (v[u].z ^ v[u].w);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) r ^= (uint32_t)__shfl_xor((int)r, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = r;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = (red[0] ^ red[1]) ^ (red[2] ^ red[3]);
+    if (blockIdx.x == 0)
+        for (int i = (int)gridDim.x + (int)threadIdx.x; i < kReadXorWords; i += 256) out[i] = 0;
+}
+
+hipError_t launch_read_xor(const void* src, int64_t bytes, uint32_t* out, hipStream_t stream) {
+    const int64_t n16 = bytes > 0 ? bytes / 16 : 0;
+    const int64_t blocks = n16 > 0 ? (n16 + 255) / 256 : 1;
+    read_xor_kernel<<<dim3((unsigned)(blocks < kReadXorWords ? blocks : kReadXorWords)), dim3(256), 0, stream>>>(
+        static_cast<const uint4*>(src), n16, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_dequant(int qtype, const uint8_t* w, float* y, int64_t n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     const int64_t threads = (n + 3) / 4;

@@ -34,6 +34,12 @@ hipError_t launch_fill(float* y, float value, int64_t n, hipStream_t stream);
 // dst[0, bytes) = src[0, bytes); bytes a multiple of 16, both 16-byte aligned.
 hipError_t launch_copy(void* dst, const void* src, int64_t bytes, hipStream_t stream);
 
+// out[0, kReadXorWords) = per-workgroup XORs of the 32-bit words of
+// src[0, bytes) (zeros past the grid): the XOR of all of out is the XOR of
+// all of src. bytes a multiple of 16, src 16-byte aligned.
+constexpr int kReadXorWords = 2048;
+hipError_t launch_read_xor(const void* src, int64_t bytes, uint32_t* out, hipStream_t stream);
+
 hipError_t launch_dequant(int qtype, const uint8_t* w, float* y, int64_t n_elems, hipStream_t stream);
 
 // y[n] = W[n, k] . x[k] with fp32 accumulation. `plan` may be pre-filled

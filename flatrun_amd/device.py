@@ -323,6 +323,16 @@ def copy(dst, src, nbytes: int, stream=None) -> None:
     check(lib().frq_dev_copy(_addr(dst), _addr(src), int(nbytes), _stream(stream)))
 
 
+READ_XOR_WORDS = 2048
+
+
+def read_xor(src, nbytes: int, out, stream=None) -> None:
+    """Read src[:nbytes] with the library's streaming read kernel (enqueued):
+    out (READ_XOR_WORDS device words) receives per-workgroup XORs of its
+    32-bit words, zeros past the grid; the XOR of all of out is that of src."""
+    check(lib().frq_dev_read_xor(_addr(src), int(nbytes), _addr(out), _stream(stream)))
+
+
 def dequant(qtype, w, y, n_elems: int, stream=None, w_bytes: int | None = None) -> None:
     """y[:n_elems] = dequant(w) on device buffers (enqueued)."""
     q = qtype_id(qtype)

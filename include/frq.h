@@ -175,10 +175,12 @@ typedef struct {
  *                y[i] = out + (n[0] + .. + n[i-1]) and y_stride = sum of n
  *                the result is the concatenation [W_0 x | W_1 x | ...]
  * One launch per batch row when every matrix is Q4_K (16-byte aligned) or
- * Q6_K (4-byte aligned, even block count per row), k <= 32768 and no matrix
- * takes frq_dev_gemv's matrix-core path (frq_gemv_group_fusable); otherwise
- * one launch per matrix. The outputs are bit-identical to frq_dev_gemv on
- * each matrix either way. */
+ * Q6_K (4-byte aligned, even block count per row) and k <= 32768
+ * (frq_gemv_group_fusable). That launch computes every row with the
+ * element-wise kernels, bit for bit what they give on each matrix alone;
+ * frq_dev_gemv on a Q4_K matrix that it sends to the matrix cores agrees
+ * with it to the fp32 accumulation tolerance, not bit for bit. Otherwise
+ * the group is one frq_dev_gemv launch per matrix. */
 int frq_dev_gemv_group(int count, const int* qtypes, const void* const* w, const size_t* w_bytes, const int64_t* n,
                        const float* x, int64_t k, float* const* y, int64_t batch, int64_t y_stride, void* stream);
 /* 1 if frq_dev_gemv_group would fuse these matrices into one launch, else 0. */
@@ -216,6 +218,16 @@ int frq_gemm_bf16(int qtype, const uint16_t* x_bf16, const uint8_t* w, size_t w_
  * the reference point for calibrating HBM traffic counters (bytes a
  * multiple of 16, both pointers 16-byte aligned). No reference counterpart. */
 int frq_dev_copy(void* dst, const void* src, size_t bytes, void* stream);
+
+/* A plain 16-byte-per-lane streaming read of src[0, bytes) (a multiple of
+ * 16, src 16-byte aligned) that folds its 32-bit words by XOR: workgroup b
+ * writes the XOR of its contiguous slice to out[b], and the words of out past
+ * the grid are zeroed, so the XOR of the FRQ_READ_XOR_WORDS device words of
+ * out is the XOR of all of src. The read-only reference point for the GEMV
+ * kernels, which read their weights once and write almost nothing; also a
+ * checksum of device data. No reference counterpart. */
+enum { FRQ_READ_XOR_WORDS = 2048 };
+int frq_dev_read_xor(const void* src, size_t bytes, uint32_t* out, void* stream);
 
 /* ------------------------------------------- memory, streams and events
  * Thin wrappers so a ctypes caller needs no other HIP binding. Streams are

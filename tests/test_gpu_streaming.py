@@ -42,3 +42,25 @@ def test_streamed_equals_resident(frq, depth):
                     assert bits_equal(out[L, t, :n], yr.to_host(np.float32)), (rep, L, name)
     finally:
         st.close()
+
+
+@pytest.mark.parametrize("nbytes", [0, 16, 48, 4096, 16 * 1000003, 38281216])
+def test_read_xor_checksum(frq, nbytes):
+    """The streaming read kernel (the read-only bandwidth reference) XORs every
+    32-bit word once: the fold of its output words equals NumPy's XOR,
+    including sizes that split unevenly over workgroups, and every word past
+    the grid is overwritten with zero (the output starts as garbage)."""
+    rng = np.random.default_rng(nbytes)
+    host = rng.integers(0, 2**32, max(nbytes // 4, 4), dtype=np.uint32)
+    src = device.DeviceBuffer.from_host(host)
+    out = device.DeviceBuffer.from_host(rng.integers(0, 2**32, device.READ_XOR_WORDS, dtype=np.uint32))
+    try:
+        device.read_xor(src, nbytes, out)
+        device.synchronize()
+        words = out.to_host(np.uint32)
+        assert int(np.bitwise_xor.reduce(words)) == int(np.bitwise_xor.reduce(host[:nbytes // 4]))
+        grid = min(device.READ_XOR_WORDS, max(1, -(-nbytes // 4096)))
+        assert not np.any(words[grid:])
+    finally:
+        src.free()
+        out.free()
