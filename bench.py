@@ -320,9 +320,11 @@ def decode_sweep_streamed(stream, layers: int = 32, depth: int = 3, steps: int =
             "note": "pinned host -> device over PCIe, overlapped with the GEMVs of earlier layers"}
 
 
-def prefill_gemm(stream, m: int = 512, n: int = 14336, k: int = 4096, reps: int = 20) -> dict:
+def prefill_gemm(stream, m: int = 512, n: int = 14336, k: int = 4096, reps: int = 200) -> dict:
     """Q4_K prefill GEMM on the matrix cores, Y[m, n] = X[m, k] (bf16) . W^T,
-    W rotated over 8 distinct copies (264 MB, beyond the Infinity Cache)."""
+    W rotated over 8 distinct copies (264 MB, beyond the Infinity Cache).
+    `reps` launches per graph (~16 ms at 200): a graph of 20 (2 ms) reads
+    15 % slower, before the part settles."""
     from flatrun_amd import _C
 
     raw = synth.make_blocks("Q4_K", n, k, seed=31)
@@ -353,7 +355,7 @@ def prefill_gemm(stream, m: int = 512, n: int = 14336, k: int = 4096, reps: int 
             "mfma_busy_pct_profiled": measured_mfma_util()}
 
 
-def prefill_layer(stream, m: int = 512, reps: int = 5) -> dict:
+def prefill_layer(stream, m: int = 512, reps: int = 20) -> dict:
     """One Llama-3-8B decoder layer's projections at prefill, Y = X . W^T for
     the Q4_K_M mix (q, k, o, gate, up Q4_K; v, down Q6_K), X [512 x in] bf16:
     seven bf16-MFMA GEMMs (shapes with few output tiles split K), captured as
