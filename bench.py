@@ -220,7 +220,7 @@ def run_suite(stream, steps: int, only: set | None = None) -> dict:
         if not want(name):
             continue
         w = GemvWorkload(q, n, k, seed=100 + idx, stream=stream, kernel=kernel)
-        t = w.time_throughput(steps, warmup=10)
+        t = w.time_throughput(steps, warmup=1000)   # ~10 ms and more: the part settles
         te = w.time_eager(min(steps, 200))
         tk = t / steps
         out[name] = {"gbs": round(w.bytes / tk / 1e9, 1), "kernel_us": round(tk * 1e6, 2),
