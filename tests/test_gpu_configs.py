@@ -87,3 +87,44 @@ def test_llama_layer_grouped_full_size(frq):
         got = nb.matmul_q6k(x, dev[m], n, k) if q == "Q6_K" else nb.matmul_q4k(x, dev[m], n, k)
         assert_matvec_close(got, G.matmul_f64(q, x, raws[m], n, k), G.abs_matmul_f64(q, x, raws[m], n, k),
                             what=f"layer {m}")
+
+
+@pytest.mark.parametrize("q,n,k", [("Q8_0", 4864, 896), ("Q4_K", 18944, 3584), ("Q1_0", 4096, 4096),
+                                   ("Q5_K", 18944, 3584), ("Q6_K", 152064, 3584)])
+def test_full_size_dequant_checksum(frq, q, n, k):
+    """Dequant at a benchmark config's full size (the lm_head: 545M outputs,
+    2.2 GB of fp32), bit for bit: the XOR of every fp32 output word, folded on
+    the device by the library's streaming read, equals the XOR of the oracle's
+    words, dequantized on the host in row chunks; the first, a middle and the
+    last chunk of rows are also compared word for word."""
+    raw = synth.make_blocks(q, n, k, seed=n + 3 * k)
+    row_bytes = synth.nbytes(q, 1, k)
+    w = device.DeviceBuffer.from_host(raw)
+    y = device.DeviceBuffer(4 * n * k)
+    out = device.DeviceBuffer(4 * device.READ_XOR_WORDS)
+    decode = getattr(G, "dequant_" + q.lower())
+    try:
+        device.dequant(q, w, y, n * k)
+        device.read_xor(y, 4 * n * k, out)
+        device.synchronize()
+        gpu_fold = int(np.bitwise_xor.reduce(out.to_host(np.uint32)))
+        rows = max(1, (1 << 24) // k)
+        host_fold = 0
+        spots = {0, (n // 2) // rows * rows, (n - 1) // rows * rows}
+        for r0 in range(0, n, rows):
+            r1 = min(n, r0 + rows)
+            ref = decode(raw[r0 * row_bytes:r1 * row_bytes], (r1 - r0) * k).view(np.uint32)
+            host_fold ^= int(np.bitwise_xor.reduce(ref))
+            if r0 in spots:                          # copy back just this chunk of rows
+                part = device.DeviceBuffer(4 * (r1 - r0) * k)
+                try:
+                    device.copy(part, y.ptr + 4 * r0 * k, 4 * (r1 - r0) * k)
+                    device.synchronize()
+                    assert np.array_equal(part.to_host(np.uint32), ref), (q, n, k, r0)
+                finally:
+                    part.free()
+        assert gpu_fold == host_fold, (q, n, k, hex(gpu_fold), hex(host_fold))
+    finally:
+        w.free()
+        y.free()
+        out.free()
