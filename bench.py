@@ -280,7 +280,7 @@ def gguf_load(stream, layers: int = 4) -> dict:
         out = {"layers": layers, "bytes": m.nbytes, "parse_ms": round(t_parse * 1e3, 2),
                "load_ms": round(m.load_seconds * 1e3, 1), "load_gbs": round(m.load_gbs, 2),
                "decode_step_outputs_finite": finite,
-               "note": "warm page cache; staging 2 x 64 MiB pinned, 4 host copy threads"}
+               "note": "warm page cache; staging 2 x 64 MiB pinned, 8 host copy threads"}
         x.free()
         y.free()
         m.close()
