@@ -153,7 +153,8 @@ class GemvWorkload:
 
 def cpu_baseline(work: GemvWorkload, y_gpu: np.ndarray, seconds: float) -> dict:
     """The reference's native matmul on the host (oracle/_ref, 1 thread) or, if
-    that build is absent, the C restatement; plus the NumPy path (BLAS)."""
+    that build is absent, the C restatement; plus the C restatement with rows
+    split over every host core, and the NumPy path (BLAS)."""
     from oracle import gguf_np as G
     from oracle.loader import c_oracle, ref_C
 
@@ -175,6 +176,18 @@ def cpu_baseline(work: GemvWorkload, y_gpu: np.ndarray, seconds: float) -> dict:
         if el >= seconds or reps >= 200:
             break
     gbs = work.bytes * reps / el / 1e9
+    # the C restatement with rows split over every host core: the reference's
+    # row-parallel matmul_q4_k_mt (q4_k.h:464-511) is built on NEON only
+    cores = os.cpu_count() or 1
+    co = c_oracle()
+    y_mt = co.matmul(q, x, raw, n, k, threads=cores)
+    reps_mt, t0 = 0, time.perf_counter()
+    while True:
+        co.matmul(q, x, raw, n, k, threads=cores)
+        reps_mt += 1
+        el_mt = time.perf_counter() - t0
+        if el_mt >= min(seconds, 3.0) or reps_mt >= 200:
+            break
     # NumPy path of the reference (dequant + BLAS matvec), all host cores
     t0 = time.perf_counter()
     y_np = G.matmul_numpy(q, x, raw, n, k)
@@ -185,6 +198,10 @@ def cpu_baseline(work: GemvWorkload, y_gpu: np.ndarray, seconds: float) -> dict:
         "value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": kind,
         "sample": f"{q} GEMV {n}x{k} b1, full shape x {reps} reps ({el:.1f} s): {what}",
         "ms_per_step": round(el / reps * 1e3, 3),
+        "row_parallel": {"value": round(work.bytes * reps_mt / el_mt / 1e9, 4), "unit": "GB/s",
+                         "ms_per_step": round(el_mt / reps_mt * 1e3, 3), "cores": cores, "kind": "port",
+                         "what": f"C restatement of matmul_{q.lower()}, rows split over {cores} threads",
+                         "max_rel_err_vs_gpu": float(np.max(np.abs(y_gpu - y_mt)) / np.max(np.abs(y_mt)))},
         "numpy_path": {"value": round(work.bytes / t_np / 1e9, 4), "unit": "GB/s", "ms_per_step": round(t_np * 1e3, 2),
                        "cores": os.cpu_count(), "what": "dequant_q4_k restatement + numpy BLAS matvec"},
         "gpu_vs_cpu_max_rel_err": err, "gpu_vs_numpy_max_rel_err": err_np,
