@@ -25,7 +25,9 @@ Printed: ONE JSON line with
              from its sources, 1 thread) on the same bytes, timed on the host
              for a bounded number of full-shape repetitions; plus the NumPy path;
   configs    every other benchmark workload (GB/s, mean kernel us, fraction of
-             HBM peak), the Llama-3-8B decode-step weight sweep (ms/step,
+             HBM peak; per GEMV config also the reference's CPU paths timed on
+             this host: native 1 thread, row-parallel on every core, NumPy),
+             the Llama-3-8B decode-step weight sweep (ms/step,
              graph replay and eager; resident and streamed), the prefill
              GEMM, the copy and read ceilings, and a GGUF file -> HBM load.
 """
@@ -208,6 +210,43 @@ def cpu_baseline(work: GemvWorkload, y_gpu: np.ndarray, seconds: float) -> dict:
     }
 
 
+def cpu_rates(q: str, n: int, k: int, raw: np.ndarray, x: np.ndarray, nbytes: int, budget_s: float = 1.0) -> dict:
+    """The reference's CPU paths on one benchmark config, timed on this host
+    beside the GPU figure: its native matmul (the reference's own _C built
+    from its sources, scalar x86, 1 thread; Q8_0, Q4_K and Q6_K only), the C
+    restatement with rows split over every host core (same formats), and the
+    NumPy path (dequant + BLAS matvec on all cores; skipped above 10^8
+    weights, where the fp32 dequant alone takes tens of seconds). Each runs
+    for about `budget_s`, at least one call after one warm call."""
+    from oracle import gguf_np as G
+    from oracle.loader import c_oracle, ref_C
+
+    cores = os.cpu_count() or 1
+
+    def rate(fn) -> dict:
+        fn()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or reps >= 50:
+                break
+        return {"gbs": round(nbytes * reps / el / 1e9, 4), "ms_per_call": round(el / reps * 1e3, 3)}
+
+    out = {}
+    R = ref_C()
+    if R is not None and hasattr(R, f"matmul_{q.lower()}"):
+        fn = getattr(R, f"matmul_{q.lower()}")
+        out["reference_native_1_thread"] = rate(lambda: fn(x, raw, n, k))
+    if q in ("Q8_0", "Q4_K", "Q6_K"):
+        co = c_oracle()
+        out["row_parallel"] = dict(rate(lambda: co.matmul(q, x, raw, n, k, threads=cores)), cores=cores)
+    if n * k <= 10**8:
+        out["numpy"] = dict(rate(lambda: G.matmul_numpy(q, x, raw, n, k)), cores=cores)
+    return out
+
+
 # (name, quant, out, in, kernel): kernel None = the default device path;
 # GEMV_ROWS forces the element-wise fp32 kernel (dequant and dot in one pass)
 SUITE = [
@@ -227,7 +266,7 @@ LLAMA_LAYER = [
 ]
 
 
-def run_suite(stream, steps: int, only: set | None = None) -> dict:
+def run_suite(stream, steps: int, only: set | None = None, cpu: bool = True) -> dict:
     out = {}
 
     def want(name: str) -> bool:
@@ -243,6 +282,8 @@ def run_suite(stream, steps: int, only: set | None = None) -> dict:
         out[name] = {"gbs": round(w.bytes / tk / 1e9, 1), "kernel_us": round(tk * 1e6, 2),
                      "frac_hbm": round(w.bytes / tk / 1e9 / HBM_PEAK_GBS, 4),
                      "eager_us_per_launch": round(te / min(steps, 200) * 1e6, 2), "effective_bytes": w.bytes}
+        if kernel is None and cpu:
+            out[name]["cpu"] = cpu_rates(q, n, k, w.raw, w.x_host, w.bytes)
         w.free()
     extra = [("llama3_8b_decode_resident", lambda: decode_sweep_resident(stream, steps=max(3, min(steps // 50, 20)))),
              ("llama3_8b_decode_streamed", lambda: decode_sweep_streamed(stream)),
@@ -663,7 +704,7 @@ def main() -> int:
         dst.free()
     if not a.no_suite:
         only = {c for c in a.configs.split(",") if c}
-        rec["configs"] = run_suite(stream, steps=min(a.steps, 500), only=only)
+        rec["configs"] = run_suite(stream, steps=min(a.steps, 500), only=only, cpu=not a.no_cpu)
         if "llama3_8b_decode_resident" in rec["configs"]:
             rec["decode_step_ms_resident"] = rec["configs"]["llama3_8b_decode_resident"]["ms_per_step"]
     if not a.no_cpu:
