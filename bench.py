@@ -285,9 +285,10 @@ def run_suite(stream, steps: int, only: set | None = None, cpu: bool = True) -> 
         if kernel is None and cpu:
             out[name]["cpu"] = cpu_rates(q, n, k, w.raw, w.x_host, w.bytes)
         w.free()
-    extra = [("llama3_8b_decode_resident", lambda: decode_sweep_resident(stream, steps=max(3, min(steps // 50, 20)))),
+    extra = [("llama3_8b_decode_resident", lambda: decode_sweep_resident(stream, steps=max(3, min(steps // 50, 20)),
+                                                                         cpu_baseline_on=cpu)),
              ("llama3_8b_decode_streamed", lambda: decode_sweep_streamed(stream)),
-             ("prefill_gemm_q4_k_bf16_512x14336x4096", lambda: prefill_gemm(stream)),
+             ("prefill_gemm_q4_k_bf16_512x14336x4096", lambda: prefill_gemm(stream, cpu_baseline_on=cpu)),
              ("llama3_8b_prefill_layer_512", lambda: prefill_layer(stream)),
              ("dequant", lambda: dequant_suite(stream)),
              ("copy_ceiling", lambda: copy_ceiling(stream)),
@@ -378,7 +379,8 @@ def decode_sweep_streamed(stream, layers: int = 32, depth: int = 3, steps: int =
             "note": "pinned host -> device over PCIe, overlapped with the GEMVs of earlier layers"}
 
 
-def prefill_gemm(stream, m: int = 512, n: int = 14336, k: int = 4096, reps: int = 200) -> dict:
+def prefill_gemm(stream, m: int = 512, n: int = 14336, k: int = 4096, reps: int = 200,
+                 cpu_baseline_on: bool = True) -> dict:
     """Q4_K prefill GEMM on the matrix cores, Y[m, n] = X[m, k] (bf16) . W^T,
     W rotated over 8 distinct copies (264 MB, beyond the Infinity Cache).
     `reps` launches per graph (~16 ms at 200): a graph of 20 (2 ms) reads
@@ -408,9 +410,22 @@ def prefill_gemm(stream, m: int = 512, n: int = 14336, k: int = 4096, reps: int 
     xd.free()
     yd.free()
     flop = 2 * m * n * k
-    return {"us": round(us, 2), "tflops": round(flop / us / 1e6, 1), "flop": flop,
-            "frac_bf16_peak": round(flop / us / 1e6 / BF16_PEAK_TFLOPS, 4), "peak_tflops": BF16_PEAK_TFLOPS,
-            "mfma_busy_pct_profiled": measured_mfma_util()}
+    out = {"us": round(us, 2), "tflops": round(flop / us / 1e6, 1), "flop": flop,
+           "frac_bf16_peak": round(flop / us / 1e6 / BF16_PEAK_TFLOPS, 4), "peak_tflops": BF16_PEAK_TFLOPS,
+           "mfma_busy_pct_profiled": measured_mfma_util()}
+    if cpu_baseline_on:
+        # the reference prefills with matmul_q4_k_batched: one scalar GEMV per
+        # token (_C.cpp:154-197); 4 of the 512 fp32 token rows, scaled
+        from oracle.loader import ref_C
+
+        R = ref_C()
+        if R is not None:
+            xs = np.random.default_rng(33).standard_normal((4, k)).astype(np.float32)
+            t0 = time.perf_counter()
+            R.matmul_q4_k_batched(xs, raw, n, k)
+            out["cpu"] = {"reference_native_batched_1_thread_ms": round((time.perf_counter() - t0) * m / 4 * 1e3, 1),
+                          "sample": f"4 of {m} token rows timed, scaled to {m}"}
+    return out
 
 
 def prefill_layer(stream, m: int = 512, reps: int = 20) -> dict:
@@ -564,7 +579,30 @@ def host_path_rate(reps: int = 20) -> dict:
             "note": "pageable host buffers; includes the H2D copy of the raw weight bytes every call"}
 
 
-def decode_sweep_resident(stream, steps: int, layers: int = 32) -> dict:
+def decode_step_cpu(host: dict, layers: int = 32) -> dict:
+    """The reference's CPU paths on one Llama-3-8B layer's seven projections
+    (the same seeded blocks), timed once each and scaled to 32 layers: its
+    native matmuls (1 thread) and the C restatement on every host core."""
+    from oracle.loader import c_oracle, ref_C
+
+    cores = os.cpu_count() or 1
+    R, co = ref_C(), c_oracle()
+    xs = {k: synth.make_x(k, seed=5) for k in {k for *_, k in LLAMA_LAYER}}
+    out = {"sample": "one layer's 7 projections timed once, x 32 layers"}
+    if R is not None:
+        t0 = time.perf_counter()
+        for name, q, n, k in LLAMA_LAYER:
+            getattr(R, f"matmul_{q.lower()}")(xs[k], host[name], n, k)
+        out["reference_native_1_thread_ms_per_step"] = round((time.perf_counter() - t0) * layers * 1e3, 1)
+    t0 = time.perf_counter()
+    for name, q, n, k in LLAMA_LAYER:
+        co.matmul(q, xs[k], host[name], n, k, threads=cores)
+    out["row_parallel_ms_per_step"] = round((time.perf_counter() - t0) * layers * 1e3, 1)
+    out["row_parallel_cores"] = cores
+    return out
+
+
+def decode_sweep_resident(stream, steps: int, layers: int = 32, cpu_baseline_on: bool = True) -> dict:
     """All 32 layers' raw blocks resident in HBM; one step = 224 GEMVs."""
     host = {name: synth.make_blocks(q, n, k, seed=i) for i, (name, q, n, k) in enumerate(LLAMA_LAYER)}
     dev = [{name: device.DeviceBuffer.from_host(host[name]) for name, *_ in LLAMA_LAYER} for _ in range(layers)]
@@ -625,7 +663,9 @@ def decode_sweep_resident(stream, steps: int, layers: int = 32) -> dict:
     for d in dev:
         for b in d.values():
             b.free()
+    cpu = decode_step_cpu(host) if cpu_baseline_on else None
     return {"ms_per_step": round(ms, 4), "ms_per_step_eager": round(ms_eager, 4), "weight_bytes_per_step": total,
+            **({"cpu": cpu} if cpu else {}),
             "gemvs_per_step": layers * len(LLAMA_LAYER), "gbs": round(total / (ms / 1e3) / 1e9, 1),
             "floor_ms_at_8TBs": round(total / 8e12 * 1e3, 4),
             "fused_shared_x": {"ms_per_step": round(ms_f, 4), "launches_per_step": layers * 4,
