@@ -1542,7 +1542,9 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
 }
 
 bool gemv_group_fusable(int count, const int* qtypes, const uint8_t* const* w, int64_t k) {
-    if (count < 1 || count > kGemvGroupMax || k <= 0 || k % kQKElems) return false;
+    // one matrix has nothing to fuse: it takes frq_dev_gemv's own kernel
+    // (the matrix cores for a large Q4_K matrix)
+    if (count < 2 || count > kGemvGroupMax || k <= 0 || k % kQKElems) return false;
     const int64_t nb = k / kQKElems;
     if (nb * 8 > 1024) return false;
     for (int i = 0; i < count; ++i) {

@@ -174,9 +174,9 @@ typedef struct {
  *                y[i] + b * (y_stride ? y_stride : n[i]) floats, so with
  *                y[i] = out + (n[0] + .. + n[i-1]) and y_stride = sum of n
  *                the result is the concatenation [W_0 x | W_1 x | ...]
- * One launch per batch row when every matrix is Q4_K (16-byte aligned) or
- * Q6_K (4-byte aligned, even block count per row) and k <= 32768
- * (frq_gemv_group_fusable). That launch computes every row with the
+ * One launch per batch row when there are two or more matrices, every one
+ * Q4_K (16-byte aligned) or Q6_K (4-byte aligned, even block count per row),
+ * and k <= 32768 (frq_gemv_group_fusable). That launch computes every row with the
  * element-wise kernels, bit for bit what they give on each matrix alone;
  * frq_dev_gemv on a Q4_K matrix that it sends to the matrix cores agrees
  * with it to the fp32 accumulation tolerance, not bit for bit. Otherwise

@@ -77,7 +77,7 @@ def test_llama_groups_fused_and_exact(frq, spec):
 
 
 @pytest.mark.parametrize("spec,k", [
-    ([("Q4_K", 5)], 256),                                   # R = 4, ragged last workgroup
+    ([("Q4_K", 5), ("Q4_K", 3)], 256),                      # R = 4, ragged last workgroup
     ([("Q6_K", 3), ("Q4_K", 2)], 512),                      # tiny segments, mixed
     ([("Q4_K", 37), ("Q6_K", 64), ("Q4_K", 9), ("Q6_K", 130)], 1024),   # four segments
     ([("Q4_K", 9000), ("Q6_K", 9000)], 512),                # total > 8192: R from the occupancy rule
@@ -96,6 +96,9 @@ def test_group_shapes_bit_identical(frq, spec, k):
     ([("Q5_K", 40), ("Q1_0", 33)], 1024),
     ([("Q4_K", 40), ("Q4_K", 33)], 34816),                  # 136 blocks x 8 lanes > 1024: split-K
     ([("Q6_K", 40)], 768),                                  # odd block count: no ring kernel
+    ([("Q4_K", 5)], 256),                                   # one matrix: one frq_dev_gemv launch
+    ([("Q4_K", 4096)], 4096),                               # one matrix on the matrix cores
+    ([("Q6_K", 300)], 3584),
 ])
 def test_group_fallback_bit_identical(frq, spec, k):
     y, ysep, *_, fusable = run_group(spec, k, seed=3)
