@@ -203,9 +203,11 @@ class NativeBackend:
         ``np.concatenate([W_0 x, W_1 x, ...], axis=-1)`` -- what the
         forwarder builds from separate matmul calls for q/k/v
         (model/qwen2.py:1510-1519) and gate/up (:1690-1702) -- from one
-        launch per x row when every weight is Q4_K or Q6_K (see
-        frq_dev_gemv_group). x (k,) -> (sum n,), x (seq, k) -> (seq, sum n);
-        the values equal the separate calls' bit for bit."""
+        launch per x row when there are two or more weights, every one
+        Q4_K or Q6_K (see frq_dev_gemv_group). x (k,) -> (sum n,), x (seq, k) -> (seq, sum n).
+        A fused launch computes with the element-wise kernels: where a
+        separate call takes the matrix cores (a large Q4_K matrix) the two
+        agree to the fp32 accumulation tolerance, otherwise bit for bit."""
         self._require()
         from . import device
         x_c = np.ascontiguousarray(x, dtype=np.float32)

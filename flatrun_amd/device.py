@@ -267,7 +267,8 @@ def _group_arrays(parts):
 
 
 def gemv_group(parts, x, k: int, batch: int = 1, y_stride: int = 0, stream=None) -> None:
-    """Matrices sharing x in one launch where possible (frq_dev_gemv_group).
+    """Matrices sharing x in one launch where possible (frq_dev_gemv_group;
+    a single matrix runs frq_dev_gemv's kernel).
 
     ``parts``: up to 4 tuples ``(qtype, w, n, y[, w_bytes])``; ``y`` is the
     device output of batch row 0 (an int address is accepted, e.g. an offset
