@@ -71,9 +71,13 @@ struct XDigits {
 };
 __device__ __forceinline__ XDigits x_digits(float4 v) {
     XDigits r;
-    const uint32_t a0 = __float_as_uint(v.x) & 0x7FFFFFFFu, a1 = __float_as_uint(v.y) & 0x7FFFFFFFu;
-    const uint32_t a2 = __float_as_uint(v.z) & 0x7FFFFFFFu, a3 = __float_as_uint(v.w) & 0x7FFFFFFFu;
-    uint32_t mx = max(max(a0, a1), max(a2, a3));   // |x| bit patterns order like |x|
+    // max |x| of the four values in two instructions (abs source modifiers;
+    // 4 masks + 2 integer maxes otherwise: 0.06 us of the 10.85 us launch at
+    // 3584 x 18944). Non-negative fp32 bit patterns order like their values.
+    float ma3, ma4;
+    asm("v_max3_f32 %0, |%1|, |%2|, |%3|" : "=v"(ma3) : "v"(v.x), "v"(v.y), "v"(v.z));
+    asm("v_max_f32_e64 %0, |%1|, %2" : "=v"(ma4) : "v"(v.w), "v"(ma3));
+    uint32_t mx = __float_as_uint(ma4);
     mx = max(mx, dpp_u<0xB1>(mx));                 // quad_perm [1,0,3,2]
     mx = max(mx, dpp_u<0x4E>(mx));                 // quad_perm [2,3,0,1]
     mx = max(mx, dpp_u<0x141>(mx));                // row_half_mirror: max over the 8 lanes
