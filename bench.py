@@ -17,6 +17,9 @@ Printed: ONE JSON line with
              per launch / mean launch duration over the same timed region;
   eager_launch_us  mean time per launch when each launch is issued from
              Python one by one (host-bound for kernels this short);
+  settle     the untimed burst (>= 20 ms of back-to-back launches) run before
+             the warmup and the timed region, whatever --warmup says: the
+             part raises its clocks over the first milliseconds of a burst;
   read_ceiling  the same weight copies read by the library's plain streaming
              read kernel, graph-replayed the same way: the time any kernel
              that reads those bytes once per launch needs here, and the
@@ -52,6 +55,7 @@ from flatrun_amd import _lib, device, synth  # noqa: E402
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, published
 ROTATE_BYTES = 1 << 30         # >= 1 GiB of distinct copies per workload
+SETTLE_MS = 20.0               # untimed back-to-back launches before every timed GEMV region
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "q4_k_gemv_3584x18944.traffic.json"
@@ -118,10 +122,30 @@ class GemvWorkload:
                 self.launch(start + i)
         return cap.graph
 
+    def settle(self, min_ms: float = SETTLE_MS, batch: int = 200) -> dict:
+        """Untimed graph replays of `batch` launches until at least `min_ms`
+        have run back to back: the part raises its clocks over the first
+        milliseconds of a burst, so a short timed region right after idle
+        reads slow. Independent of --warmup; returns what ran."""
+        g = self.graph(batch)
+        e0, e1 = device.Event(), device.Event()
+        launches, ms = 0, 0.0
+        e0.record(self.stream)
+        while ms < min_ms and launches < 200 * batch:
+            g.launch(self.stream)
+            launches += batch
+            e1.record(self.stream)
+            e1.synchronize()
+            ms = e0.elapsed_ms(e1)
+        g.destroy()
+        return {"launches": launches, "ms": round(ms, 3)}
+
     def time_throughput(self, steps: int, warmup: int) -> float:
         """Seconds for `steps` launches replayed back-to-back from one HIP
-        graph, after `warmup` untimed ones; events on the launching stream."""
+        graph, after a settle burst (settle) and `warmup` untimed launches;
+        events on the launching stream."""
         g_warm, g = self.graph(max(warmup, 1)), self.graph(steps, start=warmup)
+        self.settled = self.settle()
         g_warm.launch(self.stream)
         device.synchronize()
         e0, e1 = device.Event(), device.Event()
@@ -728,6 +752,7 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel_us": round(t_kernel * 1e6, 3)},
         "eager_launch_us": round(t_eager * 1e6, 3),
+        "settle": work.settled,
     }
     # the same weight copies read by a plain streaming kernel: what any kernel
     # reading these bytes once per launch can reach on this part

@@ -21,6 +21,10 @@ Typical use::
 
 from __future__ import annotations
 
+import collections
+import os
+import threading
+
 import numpy as np
 
 from . import _C, _lib
@@ -98,12 +102,90 @@ def _raw_bytes(weight) -> np.ndarray:
     return np.ascontiguousarray(weight, dtype=np.uint8)
 
 
+_GIB = 1 << 30
+
+
+def _cache_capacity(setting) -> int:
+    """Bytes of device weight cache from a constructor argument or the
+    FLATRUN_AMD_WEIGHT_CACHE setting: off for None / False / 0 / "" / "0",
+    64 GiB for True / "1", else a byte count ("48G", "512M" or digits)."""
+    if setting is None or setting is False:
+        return 0
+    if setting is True:
+        return 64 * _GIB
+    if isinstance(setting, int):
+        return max(0, setting)
+    txt = str(setting).strip().upper()
+    if txt in ("", "0", "OFF", "NO", "FALSE"):
+        return 0
+    if txt in ("1", "ON", "YES", "TRUE"):
+        return 64 * _GIB
+    mult = {"K": 1 << 10, "M": 1 << 20, "G": _GIB, "T": 1 << 40}.get(txt[-1:], 1)
+    num = txt[:-1] if txt[-1:] in "KMGT" else txt
+    try:
+        return max(0, int(float(num) * mult))
+    except ValueError as e:
+        raise ValueError(f"FLATRUN_AMD_WEIGHT_CACHE={setting!r}: expected 0/1 or a size such as 48G") from e
+
+
+class _WeightCache:
+    """Device copies of read-only host weight views, least recently used first out.
+
+    The key is the view's (address, byte count). An entry holds a reference
+    to the host array, so the memory behind a cached address stays mapped and
+    cannot be reused for other bytes while the entry lives; only read-only
+    arrays are cached (the reference's raw views are read-only mmap slices,
+    core/tensor.py:227-267), so the bytes behind a key do not change.
+    """
+
+    def __init__(self, capacity: int):
+        self.capacity = int(capacity)
+        self.bytes = 0
+        self.hits = self.misses = 0
+        self._entries: collections.OrderedDict = collections.OrderedDict()
+
+    def lookup(self, raw: np.ndarray):
+        """The resident copy of `raw`, uploading it on a miss; None if `raw`
+        is writable or larger than the whole cache."""
+        if raw.flags.writeable or raw.nbytes == 0 or raw.nbytes > self.capacity:
+            return None
+        key = (int(raw.ctypes.data), int(raw.nbytes))
+        hit = self._entries.get(key)
+        if hit is not None:
+            self._entries.move_to_end(key)
+            self.hits += 1
+            return hit[1]
+        self.misses += 1
+        while self._entries and self.bytes + raw.nbytes > self.capacity:
+            _, (_, old) = self._entries.popitem(last=False)
+            self.bytes -= old.nbytes
+            old.buffer.free()
+        dw = DeviceWeight(raw)
+        self._entries[key] = (raw, dw)
+        self.bytes += raw.nbytes
+        return dw
+
+    def clear(self) -> None:
+        for _, dw in self._entries.values():
+            dw.buffer.free()
+        self._entries.clear()
+        self.bytes = 0
+
+
 class NativeBackend:
     """Facade over the gfx950 kernels; mirrors python/__init__.py:85-227.
 
-    Stateless apart from a device scratch buffer for resident-weight calls;
-    safe to share across threads (host-buffer calls serialise inside the
-    library).
+    Holds a device scratch buffer for resident-weight calls and, when
+    enabled, a device weight cache. Safe to share across threads: calls that
+    use the scratch or the cache run one at a time (a lock), as the
+    reference's calls do under the GIL.
+
+    ``weight_cache`` (default: the FLATRUN_AMD_WEIGHT_CACHE environment
+    setting, off when unset) keeps a device copy of every read-only weight
+    view passed to a matmul, keyed by the view's (address, byte count), so a
+    forwarder that passes the same mmap slices every step pays the host to
+    device weight copy once (see _WeightCache). True = up to 64 GiB, an int
+    or "48G"-style string = that many bytes.
 
     Attributes
     ----------
@@ -112,10 +194,37 @@ class NativeBackend:
         unavailable backend raise RuntimeError.
     """
 
-    def __init__(self) -> None:
+    def __init__(self, weight_cache=None) -> None:
         self.available = is_available()
         self._neon = False
         self._scratch = None
+        self._lock = threading.RLock()
+        cap = _cache_capacity(os.environ.get("FLATRUN_AMD_WEIGHT_CACHE") if weight_cache is None else weight_cache)
+        self._cache = _WeightCache(cap) if cap > 0 else None
+
+    def cache_stats(self) -> dict:
+        """Weight-cache occupancy: bytes, entries, hits, misses (zeros when off)."""
+        c = self._cache
+        if c is None:
+            return {"enabled": False, "bytes": 0, "entries": 0, "hits": 0, "misses": 0}
+        return {"enabled": True, "capacity": c.capacity, "bytes": c.bytes, "entries": len(c._entries),
+                "hits": c.hits, "misses": c.misses}
+
+    def _cached(self, weight):
+        """The resident copy of a host weight view when the cache is on and
+        takes it, else None. The caller holds the lock until its launch has
+        finished: a later lookup may evict (free) the entry."""
+        if self._cache is None or isinstance(weight, DeviceWeight):
+            return None
+        return self._cache.lookup(_raw_bytes(weight).reshape(-1))
+
+    def _scratch_for(self, need: int):
+        """The scratch buffer, grown to `need` bytes; the caller holds the lock
+        and keeps the returned object (not its address) for the whole call."""
+        from . import device
+        if self._scratch is None or self._scratch.nbytes < need:
+            self._scratch = device.DeviceBuffer(need)
+        return self._scratch
 
     # ------------------------------------------------------------ helpers
     def _require(self) -> None:
@@ -127,6 +236,11 @@ class NativeBackend:
     def _matmul(self, qname: str, x, weight, n: int, k: int):
         self._require()
         x_c = np.ascontiguousarray(x, dtype=np.float32)
+        if self._cache is not None and not isinstance(weight, DeviceWeight):
+            with self._lock:
+                cached = self._cached(weight)
+                if cached is not None:
+                    return self._matmul_resident(qname, x_c, cached, n, k)
         if isinstance(weight, DeviceWeight):
             return self._matmul_resident(qname, x_c, weight, n, k)
         w_c = _raw_bytes(weight)
@@ -156,14 +270,13 @@ class NativeBackend:
         out = np.empty((seq, n), dtype=np.float32)
         if seq and n:
             xb = (seq * k * 4 + 255) // 256 * 256
-            need = xb + seq * n * 4
-            if self._scratch is None or self._scratch.nbytes < need:
-                self._scratch = device.DeviceBuffer(need)
-            base = self._scratch.ptr
-            if x_c.size:
-                _lib.check(_lib.lib().frq_memcpy_h2d(base, x_c.ctypes.data, x_c.nbytes))
-            device.gemv(qname, weight, base, base + xb, n, k, batch=seq, w_bytes=weight.nbytes)
-            _lib.check(_lib.lib().frq_memcpy_d2h(out.ctypes.data, base + xb, out.nbytes))
+            with self._lock:
+                scratch = self._scratch_for(xb + seq * n * 4)
+                base = scratch.ptr
+                if x_c.size:
+                    _lib.check(_lib.lib().frq_memcpy_h2d(base, x_c.ctypes.data, x_c.nbytes))
+                device.gemv(qname, weight, base, base + xb, n, k, batch=seq, w_bytes=weight.nbytes)
+                _lib.check(_lib.lib().frq_memcpy_d2h(out.ctypes.data, base + xb, out.nbytes))
         return out[0] if x_c.ndim == 1 else out
 
     def upload(self, weight) -> DeviceWeight:
@@ -223,38 +336,42 @@ class NativeBackend:
             raise ValueError(f"x must be 1-D or 2-D, got shape {x_c.shape}")
         if not 1 <= len(parts) <= device.GROUP_MAX:
             raise ValueError(f"matmul_fused takes 1..{device.GROUP_MAX} parts, got {len(parts)}")
-        ns = [int(n) for _, _, n in parts]
-        total = sum(ns)
-        out = np.empty((seq, total), dtype=np.float32)
-        temps = []
-        try:
-            ws = []
-            for q, wgt, n in parts:
-                if isinstance(wgt, DeviceWeight):
-                    ws.append(wgt)
-                else:
-                    raw = _raw_bytes(wgt).reshape(-1)
-                    dw = DeviceWeight(raw) if raw.size else None
-                    temps.append(dw)
-                    ws.append(dw)
-            if seq and total:
-                xb = (seq * k * 4 + 255) // 256 * 256
-                need = xb + seq * total * 4
-                if self._scratch is None or self._scratch.nbytes < need:
-                    self._scratch = device.DeviceBuffer(need)
-                base = self._scratch.ptr
-                if x_c.size:
-                    _lib.check(_lib.lib().frq_memcpy_h2d(base, x_c.ctypes.data, x_c.nbytes))
-                grp, off = [], 0
-                for (q, _, n), w in zip(parts, ws):
-                    grp.append((q, w if w is not None else 0, n, base + xb + 4 * off, w.nbytes if w is not None else 0))
-                    off += int(n)
-                device.gemv_group(grp, base, k, batch=seq, y_stride=total)
-                _lib.check(_lib.lib().frq_memcpy_d2h(out.ctypes.data, base + xb, out.nbytes))
-        finally:
-            for t in temps:
-                if t is not None:
-                    t.buffer.free()
+        with self._lock:   # cache entries and the scratch stay valid until the results are back
+            ns = [int(n) for _, _, n in parts]
+            total = sum(ns)
+            out = np.empty((seq, total), dtype=np.float32)
+            temps = []
+            try:
+                ws = []
+                for q, wgt, n in parts:
+                    cached = self._cached(wgt)
+                    if cached is not None:
+                        ws.append(cached)
+                    elif isinstance(wgt, DeviceWeight):
+                        ws.append(wgt)
+                    else:
+                        raw = _raw_bytes(wgt).reshape(-1)
+                        dw = DeviceWeight(raw) if raw.size else None
+                        temps.append(dw)
+                        ws.append(dw)
+                if seq and total:
+                    xb = (seq * k * 4 + 255) // 256 * 256
+                    with self._lock:
+                        scratch = self._scratch_for(xb + seq * total * 4)
+                        base = scratch.ptr
+                        if x_c.size:
+                            _lib.check(_lib.lib().frq_memcpy_h2d(base, x_c.ctypes.data, x_c.nbytes))
+                        grp, off = [], 0
+                        for (q, _, n), w in zip(parts, ws):
+                            grp.append((q, w if w is not None else 0, n, base + xb + 4 * off,
+                                        w.nbytes if w is not None else 0))
+                            off += int(n)
+                        device.gemv_group(grp, base, k, batch=seq, y_stride=total)
+                        _lib.check(_lib.lib().frq_memcpy_d2h(out.ctypes.data, base + xb, out.nbytes))
+            finally:
+                for t in temps:
+                    if t is not None:
+                        t.buffer.free()
         return out[0] if x_c.ndim == 1 else out
 
     def matmul_q5_k(self, x, weight, n: int, k: int):

@@ -107,43 +107,79 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // Counters and partial sums live in separate allocations: the counters must
 // be zero before every launch (zeroed once when allocated, left zero by every
 // launch), so nothing else may ever write their memory.
+//
+// A buffer is never freed while something may still use it. Growing replaces
+// the buffer with a larger one and keeps the old one in `retired` until the
+// stream is destroyed (frq_stream_destroy), because a graph captured earlier
+// on that stream still launches kernels on the old address; the counters of
+// a retired buffer stay zero, since every launch leaves them so. The registry
+// lock is held from the lookup through the launch, so one thread cannot
+// retire a buffer another is about to launch with. Capacities grow at least
+// twofold, so a stream retires O(log size) buffers.
 struct SkScratch {
     void* part = nullptr;
     size_t part_cap = 0;
     void* cnt = nullptr;
     size_t cnt_cap = 0;
+    std::vector<void*> retired;
 };
 std::mutex g_sk_mu;
 std::map<std::pair<int, hipStream_t>, SkScratch> g_sk;
 
-int grow(void** ptr, size_t* cap, size_t bytes, bool zero, hipStream_t stream) {
+int grow(void** ptr, size_t* cap, size_t bytes, bool zero, std::vector<void*>* retired) {
     if (*cap >= bytes) return FRQ_OK;
-    if (*ptr) {
-        FRQ_HIP(hipStreamSynchronize(stream));   // the old buffer may still be in use
-        FRQ_HIP(hipFree(*ptr));
-        *ptr = nullptr;
-        *cap = 0;
-    }
     size_t want = bytes < ((size_t)1 << 16) ? ((size_t)1 << 16) : bytes;
-    FRQ_HIP(hipMalloc(ptr, want));
-    if (zero) FRQ_HIP(hipMemset(*ptr, 0, want));
+    if (want < 2 * *cap) want = 2 * *cap;
+    void* p = nullptr;
+    FRQ_HIP(hipMalloc(&p, want));
+    if (zero) {
+        const hipError_t e = hipMemset(p, 0, want);
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return hip_fail(e, "hipMemset(scratch)");
+        }
+    }
+    if (*ptr) retired->push_back(*ptr);
+    *ptr = p;
     *cap = want;
     return FRQ_OK;
 }
 
-int sk_scratch(hipStream_t stream, size_t part_bytes, size_t cnt_bytes, float** part, uint32_t** cnt) {
+// Scratch for one launch on `stream`; the caller holds g_sk_mu (see above)
+// until the launch has been enqueued.
+int sk_scratch_locked(hipStream_t stream, size_t part_bytes, size_t cnt_bytes, float** part, uint32_t** cnt) {
     *part = nullptr;
     *cnt = nullptr;
     if (part_bytes == 0 && cnt_bytes == 0) return FRQ_OK;
     int dev = 0;
     FRQ_HIP(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_sk_mu);
     SkScratch& sc = g_sk[{dev, stream}];
-    if (int rc = grow(&sc.part, &sc.part_cap, part_bytes, false, stream)) return rc;
-    if (int rc = grow(&sc.cnt, &sc.cnt_cap, cnt_bytes, true, stream)) return rc;
+    if (int rc = grow(&sc.part, &sc.part_cap, part_bytes, false, &sc.retired)) return rc;
+    if (int rc = grow(&sc.cnt, &sc.cnt_cap, cnt_bytes, true, &sc.retired)) return rc;
     *part = static_cast<float*>(sc.part);
     *cnt = static_cast<uint32_t*>(sc.cnt);
     return FRQ_OK;
+}
+
+// Frees the scratch of every device's entry for `stream` (the stream's work
+// has finished: the caller synchronised it).
+void sk_release_stream(hipStream_t stream) {
+    std::lock_guard<std::mutex> lk(g_sk_mu);
+    for (auto it = g_sk.begin(); it != g_sk.end();) {
+        if (it->first.second != stream) {
+            ++it;
+            continue;
+        }
+        SkScratch& sc = it->second;
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        (void)hipSetDevice(it->first.first);
+        if (sc.part) (void)hipFree(sc.part);
+        if (sc.cnt) (void)hipFree(sc.cnt);
+        for (void* p : sc.retired) (void)hipFree(p);
+        (void)hipSetDevice(cur);
+        it = g_sk.erase(it);
+    }
 }
 
 // One GEMV on device buffers: the matrix-core Q4_K kernel where eligible,
@@ -164,7 +200,8 @@ int gemv_device(int qtype, const uint8_t* w, const float* x, float* y, int64_t n
     frq::gemv_sk_scratch(sp, n, &pb, &cb);
     float* part = nullptr;
     uint32_t* cnt = nullptr;
-    if (int rc = sk_scratch(s, pb, cb, &part, &cnt)) return rc;
+    std::lock_guard<std::mutex> lk(g_sk_mu);
+    if (int rc = sk_scratch_locked(s, pb, cb, &part, &cnt)) return rc;
     FRQ_HIP(frq::launch_gemv_sk(qtype, w, x, y, n, k, sp, part, cnt, s));
     return FRQ_OK;
 }
@@ -466,7 +503,8 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
         frq::gemv_sk_scratch(p, n, &pb, &cb);
         float* part = nullptr;
         uint32_t* cnt = nullptr;
-        if (int rc = sk_scratch(s, pb, cb, &part, &cnt)) return rc;
+        std::lock_guard<std::mutex> lk(g_sk_mu);
+        if (int rc = sk_scratch_locked(s, pb, cb, &part, &cnt)) return rc;
         hipError_t e = frq::launch_gemv_sk(qtype, wp, x, y, n, k, p, part, cnt, s);
         if (e != hipSuccess) return hip_fail(e, "launch_gemv_sk");
         cfg->kernel = FRQ_GEMV_SPLITK;
@@ -487,15 +525,7 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
         if (qtype != FRQ_Q4_K) return fail(FRQ_ERR_UNSUPPORTED, "the LDS row ring is a Q4_K kernel");
         p.lds = cfg->unroll > 0 ? cfg->unroll : 4;
     }
-    float* part = nullptr;
-    uint32_t* cnt = nullptr;
-    if (p.slices == 2) {                       // the two-slice Q4_K kernel meets through scratch
-        size_t pb = 0, cb = 0;
-        frq::gemv_split_scratch(qtype, n, &pb, &cb);
-        if (pb && cb)
-            if (int rc = sk_scratch(s, pb, cb, &part, &cnt)) return rc;
-    }
-    hipError_t e = frq::launch_gemv(qtype, wp, x, y, n, k, &p, s, part, cnt);
+    hipError_t e = frq::launch_gemv(qtype, wp, x, y, n, k, &p, s);
     if (e != hipSuccess) return hip_fail(e, "launch_gemv");
     cfg->kernel = p.lds > 0 ? FRQ_GEMV_ROWS_LDS : FRQ_GEMV_ROWS;
     cfg->cpl = p.cpl;
@@ -539,7 +569,8 @@ int frq_dev_gemm_bf16(int qtype, const void* w, size_t w_bytes, const uint16_t* 
     if (reinterpret_cast<uintptr_t>(y) & 3) return fail(FRQ_ERR_ALIGN, "y must be 4-byte aligned");
     float* part = nullptr;
     uint32_t* cnt = nullptr;
-    if (int rc = sk_scratch(s, frq::gemm_bf16_scratch(m, n, k), 0, &part, &cnt)) return rc;   // split-K partials
+    std::lock_guard<std::mutex> lk(g_sk_mu);
+    if (int rc = sk_scratch_locked(s, frq::gemm_bf16_scratch(m, n, k), 0, &part, &cnt)) return rc;   // split-K partials
     FRQ_HIP(frq::launch_gemm_bf16(qtype, static_cast<const uint8_t*>(w), x, y, m, n, k, s, part));
     return FRQ_OK;
 }
@@ -634,7 +665,15 @@ int frq_stream_create(void** s) {
     *s = st;
     return FRQ_OK;
 }
-int frq_stream_destroy(void* s) { FRQ_HIP(hipStreamDestroy(static_cast<hipStream_t>(s))); return FRQ_OK; }
+int frq_stream_destroy(void* s) {
+    hipStream_t st = static_cast<hipStream_t>(s);
+    if (st) {   // the stream's scratch can go once its work is done (the null stream's stays)
+        FRQ_HIP(hipStreamSynchronize(st));
+        sk_release_stream(st);
+    }
+    FRQ_HIP(hipStreamDestroy(st));
+    return FRQ_OK;
+}
 int frq_stream_synchronize(void* s) { FRQ_HIP(hipStreamSynchronize(static_cast<hipStream_t>(s))); return FRQ_OK; }
 int frq_stream_wait_event(void* s, void* e) {
     FRQ_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(s), static_cast<hipEvent_t>(e), 0));

@@ -87,33 +87,20 @@ __device__ __forceinline__ void finish_rows(int64_t row0, int64_t row_end, float
 // sums per wave collect in LDS and are added in a fixed order when y is
 // written once at the end.
 //
-// S = 2 splits every row in two halves of its blocks, one workgroup each, so
-// a long row (74 blocks at k = 18944) runs as two 5-wave workgroups instead of
-// one 10-wave workgroup: twice the resident waves per SIMD for the same rows.
-// The halves meet through memory: each writes its row sums with system-scope
-// stores (written through to memory), waits for them, and increments the row
-// block's counter (device-scope atomic); the second to arrive reads the other
-// half's sums with system-scope loads (past the L2), writes y = a + b (the
-// same bits in either order) and returns the counter to zero.
 // Body of one workgroup; `wg` plays the role of blockIdx.x (the grouped
 // kernel below passes the index inside its segment).
-template <int CPL, int U, int R, int S = 1>
+template <int CPL, int U, int R>
 __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                               float* __restrict__ y, int64_t n, int nb, float* __restrict__ part,
-                                               uint32_t* __restrict__ cnt, int64_t wg) {
+                                               float* __restrict__ y, int64_t n, int nb, int64_t wg) {
     static_assert(U <= R, "ring deeper than the row count");
-    static_assert(S == 1 || S == 2, "one or two slices");
     __shared__ float red[R * 64];                           // [row][wave][DPP row]
     constexpr int LPB = 8 / CPL;
     constexpr int NE = 16 * CPL;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
-    const int slice = (S == 2) ? (int)(wg & 1) : 0;
-    const int64_t rb = (S == 2) ? (wg >> 1) : wg;
-    const int nb0 = (S == 2) ? (nb + 1) / 2 : nb;           // blocks of the first slice
-    const int blk_first = slice ? nb0 : 0, nbs = slice ? nb - nb0 : nb0;
+    const int64_t rb = wg;
     const int blk = tid / LPB, sub = tid % LPB;
-    const bool active = blk < nbs;
-    const int gblk = blk_first + (active ? blk : 0);        // block index in the row
+    const bool active = blk < nb;
+    const int gblk = active ? blk : 0;                      // block index in the row
     const int g = (CPL == 2) ? sub : (sub >> 1);
     const int hh = (CPL == 2) ? 0 : (sub & 1);
     const ScaleDecode dec(g);
@@ -229,29 +216,10 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
         if ((lane & 15) == 15) red[j * 4 * nwaves + 4 * wave + (lane >> 4)] = v;
     });
     __syncthreads();
-    if constexpr (S == 1) {
-        for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
-            float s = 0.0f;
-            for (int w2 = 0; w2 < 4 * nwaves; ++w2) s += red[r * 4 * nwaves + w2];
-            y[row0 + r] = s;
-        }
-    } else {
-        __shared__ uint32_t arrival;
+    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
         float s = 0.0f;
-        if (tid < nrows) {
-            for (int w2 = 0; w2 < 4 * nwaves; ++w2) s += red[tid * 4 * nwaves + w2];
-            __hip_atomic_store(part + (rb * 2 + slice) * R + tid, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        }
-        __builtin_amdgcn_s_waitcnt(0);              // this thread's stores are acknowledged
-        __syncthreads();                            // ... and every thread's
-        if (tid == 0) arrival = __hip_atomic_fetch_add(cnt + rb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        if (arrival == 1) {                         // second half to finish: combine
-            if (tid < nrows)
-                y[row0 + tid] = s + __hip_atomic_load(part + (rb * 2 + (slice ^ 1)) * R + tid, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_SYSTEM);
-            if (tid == 0) __hip_atomic_store(cnt + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        for (int w2 = 0; w2 < 4 * nwaves; ++w2) s += red[r * 4 * nwaves + w2];
+        y[row0 + r] = s;
     }
 }
 
@@ -388,11 +356,10 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_lds_kernel(const uint8_t* __re
     }
 }
 
-template <int CPL, int U, int R, int S = 1>
+template <int CPL, int U, int R>
 __global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_waves_per_eu((CPL == 1 && U <= 3) ? 5 : 1)))
-gemv_q4_k_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int64_t n, int nb,
-                 float* __restrict__ part, uint32_t* __restrict__ cnt) {
-    gemv_q4_k_body<CPL, U, R, S>(w, x, y, n, nb, part, cnt, blockIdx.x);
+gemv_q4_k_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int64_t n, int nb) {
+    gemv_q4_k_body<CPL, U, R>(w, x, y, n, nb, blockIdx.x);
 }
 
 // ------------------------------------------------------------------ Q5_K
@@ -754,7 +721,7 @@ __global__ void __launch_bounds__(1024) gemv_group_kernel(GemvGroup g, const flo
         if (t < g.count && b >= g.wg_begin[t]) i = t;
     const int64_t wg = b - g.wg_begin[i];
     if (g.qtype[i] == kTypeQ4K)
-        gemv_q4_k_body<1, (R < 3 ? R : 3), R, 1>(g.w[i], x, g.y[i], g.n[i], nb, nullptr, nullptr, wg);
+        gemv_q4_k_body<1, (R < 3 ? R : 3), R>(g.w[i], x, g.y[i], g.n[i], nb, wg);
     else
         gemv_q6_k_ring_body<(R < 4 ? R : 4), R>(g.w[i], x, g.y[i], g.n[i], nb, wg);
 }
@@ -1211,14 +1178,6 @@ int q4k_ring(int cpl, int want) {
 // at most 256 workgroups (one round, every CU busy). Smaller workgroups
 // (short rows) want several resident per CU: 4 rows per workgroup up to
 // n = 8192, beyond that the fewest rows that keep <= 2560 workgroups.
-// Rows per workgroup of the two-slice Q4_K kernel: the fewest rows that keep
-// <= 1024 workgroups (4 per CU, 5 waves each at 74 blocks per row).
-int pick_rows_q4k_split(int64_t n) {
-    for (int r : kQ4KRowSet)
-        if ((n + r - 1) / r * 2 <= 1024) return r;
-    return 16;
-}
-
 int pick_rows_q4k(int64_t n, int waves) {
     const int64_t kCUs = 256;
     if (waves < 4) {
@@ -1232,23 +1191,22 @@ int pick_rows_q4k(int64_t n, int waves) {
     return 16;
 }
 
-template <int CPL, int U, int R, int S>
-void q4k_go(dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n, int nb,
-            float* part, uint32_t* cnt) {
-    gemv_q4_k_kernel<CPL, (U < R ? U : R), R, S><<<gd, bd, 0, s>>>(w, x, y, n, nb, part, cnt);
+template <int CPL, int U, int R>
+void q4k_go(dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n, int nb) {
+    gemv_q4_k_kernel<CPL, (U < R ? U : R), R><<<gd, bd, 0, s>>>(w, x, y, n, nb);
 }
 
-template <int CPL, int U, int S>
+template <int CPL, int U>
 bool q4k_rows(int rows, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n,
-              int nb, float* part, uint32_t* cnt) {
+              int nb) {
     switch (rows) {
-        case 1: q4k_go<CPL, U, 1, S>(gd, bd, s, w, x, y, n, nb, part, cnt); return true;
-        case 2: q4k_go<CPL, U, 2, S>(gd, bd, s, w, x, y, n, nb, part, cnt); return true;
-        case 4: q4k_go<CPL, U, 4, S>(gd, bd, s, w, x, y, n, nb, part, cnt); return true;
-        case 7: q4k_go<CPL, U, 7, S>(gd, bd, s, w, x, y, n, nb, part, cnt); return true;
-        case 8: q4k_go<CPL, U, 8, S>(gd, bd, s, w, x, y, n, nb, part, cnt); return true;
-        case 14: q4k_go<CPL, U, 14, S>(gd, bd, s, w, x, y, n, nb, part, cnt); return true;
-        case 16: q4k_go<CPL, U, 16, S>(gd, bd, s, w, x, y, n, nb, part, cnt); return true;
+        case 1: q4k_go<CPL, U, 1>(gd, bd, s, w, x, y, n, nb); return true;
+        case 2: q4k_go<CPL, U, 2>(gd, bd, s, w, x, y, n, nb); return true;
+        case 4: q4k_go<CPL, U, 4>(gd, bd, s, w, x, y, n, nb); return true;
+        case 7: q4k_go<CPL, U, 7>(gd, bd, s, w, x, y, n, nb); return true;
+        case 8: q4k_go<CPL, U, 8>(gd, bd, s, w, x, y, n, nb); return true;
+        case 14: q4k_go<CPL, U, 14>(gd, bd, s, w, x, y, n, nb); return true;
+        case 16: q4k_go<CPL, U, 16>(gd, bd, s, w, x, y, n, nb); return true;
         default: return false;
     }
 }
@@ -1287,21 +1245,19 @@ hipError_t launch_q4k_lds(int depth, int rows, int waves, int64_t grid, const ui
     return hipGetLastError();
 }
 
-hipError_t launch_q4k(int cpl, int ring, int rows, int slices, int waves, int64_t grid, const uint8_t* w,
-                      const float* x, float* y, int64_t n, int nb, float* part, uint32_t* cnt, hipStream_t s) {
+hipError_t launch_q4k(int cpl, int ring, int rows, int waves, int64_t grid, const uint8_t* w, const float* x,
+                      float* y, int64_t n, int nb, hipStream_t s) {
     const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
     bool ok = false;
     if (cpl == 2) {
-        ok = ring == 3 ? q4k_rows<2, 3, 1>(rows, gd, bd, s, w, x, y, n, nb, part, cnt)
-                       : q4k_rows<2, 5, 1>(rows, gd, bd, s, w, x, y, n, nb, part, cnt);
-    } else if (slices == 2) {
-        ok = q4k_rows<1, 3, 2>(rows, gd, bd, s, w, x, y, n, nb, part, cnt);
+        ok = ring == 3 ? q4k_rows<2, 3>(rows, gd, bd, s, w, x, y, n, nb)
+                       : q4k_rows<2, 5>(rows, gd, bd, s, w, x, y, n, nb);
     } else if (ring == 6) {
-        ok = q4k_rows<1, 6, 1>(rows, gd, bd, s, w, x, y, n, nb, part, cnt);
+        ok = q4k_rows<1, 6>(rows, gd, bd, s, w, x, y, n, nb);
     } else if (ring == 4) {
-        ok = q4k_rows<1, 4, 1>(rows, gd, bd, s, w, x, y, n, nb, part, cnt);
+        ok = q4k_rows<1, 4>(rows, gd, bd, s, w, x, y, n, nb);
     } else {
-        ok = q4k_rows<1, 3, 1>(rows, gd, bd, s, w, x, y, n, nb, part, cnt);
+        ok = q4k_rows<1, 3>(rows, gd, bd, s, w, x, y, n, nb);
     }
     if (!ok) return hipErrorInvalidConfiguration;
     return hipGetLastError();
@@ -1446,15 +1402,8 @@ bool gemv_supported(int qtype, int64_t n, int64_t k) {
     return pick_cpl(qtype, k / f.belems) != 0;
 }
 
-void gemv_split_scratch(int qtype, int64_t n, size_t* part_bytes, size_t* cnt_bytes) {
-    // upper bounds for any row count: two sums per row, one counter per row
-    const bool q4k = qtype == kTypeQ4K && n > 0;
-    *part_bytes = q4k ? (size_t)(n + 16) * 2 * sizeof(float) : 0;
-    *cnt_bytes = q4k ? (size_t)n * sizeof(uint32_t) : 0;
-}
-
 hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k,
-                       GemvPlan* plan, hipStream_t stream, float* part, uint32_t* cnt) {
+                       GemvPlan* plan, hipStream_t stream) {
     const Fmt f = fmt_of(qtype);
     if (f.belems == 0 || k % f.belems) return hipErrorInvalidValue;
     if (n <= 0) return hipSuccess;
@@ -1516,19 +1465,15 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
         return launch_q4k_lds(p.lds, p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
     }
     if (qtype == kTypeQ4K) {
-        // one slice unless asked: two slices measured slower on every shape
-        // tried (3584 x 18944: 13.1 vs 12.0 us), despite twice the waves
-        if (p.slices <= 0) p.slices = 1;
-        if (p.slices != 1 && (p.slices != 2 || p.cpl != 1 || !part || !cnt)) return hipErrorInvalidConfiguration;
-        if (p.slices == 2) p.waves = (int)((((nb + 1) / 2) * 8 + 63) / 64);
-        if (p.rows_per_wg <= 0) p.rows_per_wg = p.slices == 2 ? pick_rows_q4k_split(n) : pick_rows_q4k(n, p.waves);
+        if (p.slices > 1) return hipErrorInvalidConfiguration;   // every row in one workgroup
+        p.slices = 1;
+        if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q4k(n, p.waves);
         if (!q4k_rows_ok(p.rows_per_wg)) return hipErrorInvalidConfiguration;
         p.unroll = q4k_ring(p.cpl, p.unroll > 0 ? p.unroll : 3);
-        p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg * p.slices;
+        p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
         if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
         if (plan) *plan = p;
-        return launch_q4k(p.cpl, p.unroll, p.rows_per_wg, p.slices, p.waves, p.grid, w, x, y, n, (int)nb, part, cnt,
-                          stream);
+        return launch_q4k(p.cpl, p.unroll, p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
     }
     if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows(n, p.waves);
     if (p.unroll != 4 && p.unroll != 8) p.unroll = p.rows_per_wg >= 8 ? 8 : 4;

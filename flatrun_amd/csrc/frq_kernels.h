@@ -23,7 +23,7 @@ struct GemvPlan {
     int waves = 0;          // wavefronts per workgroup
     int rows_per_wg = 0;    // output rows owned by one workgroup
     int unroll = 0;         // rows whose loads are issued together
-    int slices = 0;         // Q4_K: 1, or 2 halves of every row (needs scratch); 0 = choose
+    int slices = 0;         // 1: every row in one workgroup (0 = choose; nothing else is accepted)
     int lds = 0;            // Q4_K: > 0 = row ring of that many rows in LDS instead of registers
     int64_t grid = 0;       // workgroups
 };
@@ -45,13 +45,8 @@ hipError_t launch_dequant(int qtype, const uint8_t* w, float* y, int64_t n_elems
 // y[n] = W[n, k] . x[k] with fp32 accumulation. `plan` may be pre-filled
 // (cpl/rows_per_wg/unroll > 0) to override the heuristic; on return it holds
 // the geometry that was launched.
-// `part` / `cnt`: scratch for the two-slice Q4_K kernel (may be null: one
-// slice). Sizes from gemv_split_scratch; the counters must be zero before the
-// first launch, every launch leaves them zero, and launches sharing them must
-// be ordered (one stream).
 hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k,
-                       GemvPlan* plan, hipStream_t stream, float* part = nullptr, uint32_t* cnt = nullptr);
-void gemv_split_scratch(int qtype, int64_t n, size_t* part_bytes, size_t* cnt_bytes);
+                       GemvPlan* plan, hipStream_t stream);
 
 // Checks that a GEMV of this shape can be planned; returns false with no launch otherwise.
 bool gemv_supported(int qtype, int64_t n, int64_t k);

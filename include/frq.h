@@ -153,9 +153,8 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  *   cpl           work unit per lane (format specific)
  *   rows          rows per work item (SPLITK) / per workgroup (ROWS)
  *   unroll        rows per load batch
- *   slices        K-slices per row: output for SPLITK; for the ROWS kernel
- *                 of Q4_K also an input (0 = choose, 1, or 2: every row in
- *                 two halves, one workgroup each, combined through memory)
+ *   slices        K-slices per row: output for SPLITK; 1 for the ROWS
+ *                 kernels (an input of 0 or 1; anything else is rejected)
  *   waves_per_wg  wavefronts per workgroup (output)
  *   items         work items / workgroups launched (output)              */
 enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2, FRQ_GEMV_ROWS_LDS = 3, FRQ_GEMV_MX = 4 };
@@ -261,6 +260,11 @@ int frq_device_synchronize(void);
  * points that allocate on first use (the split-K scratch of very long rows
  * and of split GEMMs, the host workspace) must have run once for the shape
  * before capture.
+ * Scratch lifetime: each (device, stream) has its own scratch; it grows when
+ * a later call on that stream needs more, and the buffers it replaces stay
+ * allocated (a graph captured earlier still launches on them) until
+ * frq_stream_destroy, which synchronises the stream and frees them. Destroy
+ * the graphs captured on a stream before destroying the stream.
  * Captured work records kernels only (no memset nodes). No reference
  * counterpart: the reference calls its matmuls one by one from Python.     */
 int frq_stream_begin_capture(void* stream);

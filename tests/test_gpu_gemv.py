@@ -124,20 +124,19 @@ def test_launch_geometry_sweep(frq, q, n, k):
         for cpl in (1, 2, 4, 8):
             for rows in (1, 3, 4, 7, 8, 14, 16, 32, 64):
                 for unroll in (2, 4, 8):
-                    for slices in ((0, 1, 2) if (q == "Q4_K" and kernel == _lib.GEMV_ROWS) else (0,)):
-                        try:
-                            cfg = device.gemv_tuned(q, w, xd, yd, n, k, kernel=kernel, cpl=cpl, rows=rows,
-                                                    unroll=unroll, slices=slices)
-                        except RuntimeError:
-                            continue                     # geometry not valid for this format / k
-                        device.synchronize()
-                        y = yd.to_host(np.float32)
-                        assert_matvec_close(y, y64, absw, what=f"{cfg}")
-                        key = (cfg["kernel"], cfg["cpl"], cfg["slices"] if kernel == _lib.GEMV_ROWS else 0)
-                        if key in seen:
-                            assert bits_equal(y, seen[key]), cfg
-                        else:
-                            seen[key] = y
+                    try:
+                        cfg = device.gemv_tuned(q, w, xd, yd, n, k, kernel=kernel, cpl=cpl, rows=rows,
+                                                unroll=unroll)
+                    except RuntimeError:
+                        continue                         # geometry not valid for this format / k
+                    device.synchronize()
+                    y = yd.to_host(np.float32)
+                    assert_matvec_close(y, y64, absw, what=f"{cfg}")
+                    key = (cfg["kernel"], cfg["cpl"])
+                    if key in seen:
+                        assert bits_equal(y, seen[key]), cfg
+                    else:
+                        seen[key] = y
     assert seen
 
 
@@ -188,43 +187,21 @@ def test_q4_k_lds_ring_rejects(frq):
         yd.free()
 
 
-def test_two_slice_rows_repeated_and_alternating(frq):
-    """The two-slice Q4_K kernel (halves combined through memory) gives the
-    same bits launch after launch, alternating with other shapes that share
-    the stream's scratch, and in a captured graph replayed several times."""
-    cases = [(3584, 18944, 1), (257, 18944, 2), (1000, 16384, 3)]
-    s = device.Stream()
-    bufs = []
-    for n, k, seed in cases:
-        raw = synth.make_blocks("Q4_K", n, k, seed=seed)
-        x = synth.make_x(k, seed=seed + 10)
-        bufs.append((n, k, raw, x, device.DeviceBuffer.from_host(raw), device.DeviceBuffer.from_host(x),
-                     device.DeviceBuffer(4 * n)))
-    ref = []
-    for n, k, raw, x, w, xd, yd in bufs:
-        cfg = device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_lib.GEMV_ROWS, slices=2, stream=s)
-        assert cfg["slices"] == 2
-        s.synchronize()
-        y = yd.to_host(np.float32)
-        assert_matvec_close(y, G.matmul_f64("Q4_K", x, raw, n, k), G.abs_matmul_f64("Q4_K", x, raw, n, k))
-        ref.append(y)
-    for _ in range(20):
-        for n, k, raw, x, w, xd, yd in bufs:
-            device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_lib.GEMV_ROWS, slices=2, stream=s)
-    s.synchronize()
-    for (n, k, *_, yd), r in zip(bufs, ref):
-        assert bits_equal(yd.to_host(np.float32), r)
-    with device.Graph.capture(s) as cap:
-        for n, k, raw, x, w, xd, yd in bufs:
-            device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_lib.GEMV_ROWS, slices=2, stream=s)
+def test_rows_kernel_rejects_two_slices(frq):
+    """A row is never split over workgroups by the whole-row kernels: a
+    request for two slices is refused before anything is launched."""
+    n, k = 64, 3584
+    raw = synth.make_blocks("Q4_K", n, k, seed=4)
+    w = device.DeviceBuffer.from_host(raw)
+    xd = device.DeviceBuffer.from_host(synth.make_x(k, seed=5))
+    yd = device.DeviceBuffer(4 * n)
     try:
-        for _ in range(3):
-            cap.launch(s)
-            s.synchronize()
-            for (n, k, *_, yd), r in zip(bufs, ref):
-                assert bits_equal(yd.to_host(np.float32), r)
+        with pytest.raises(RuntimeError):
+            device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_lib.GEMV_ROWS, slices=2)
     finally:
-        cap.destroy()
+        w.free()
+        xd.free()
+        yd.free()
 
 
 def test_split_k_repeated_launches(frq):
@@ -247,6 +224,89 @@ def test_split_k_repeated_launches(frq):
     device.synchronize()
     assert bits_equal(y1.to_host(np.float32), ref1)
     assert bits_equal(y2.to_host(np.float32), ref2)
+
+
+def test_split_k_scratch_growth_keeps_captured_graph_valid(frq):
+    """A graph captured with a small split-K launch still replays to the eager
+    bits after a larger split-K launch on the same stream has grown (and
+    replaced) the stream's scratch: the replaced buffer stays allocated until
+    the stream is destroyed."""
+    small, big = (64, 8192 * 5), (3000, 8192 * 5)      # k > 32768: split-K GEMV
+    s = device.Stream()
+    bufs = {}
+    for tag, (n, k) in (("small", small), ("big", big)):
+        raw = synth.make_blocks("Q4_K", n, k, seed=n)
+        x = synth.make_x(k, seed=n + 1)
+        bufs[tag] = (n, k, raw, x, device.DeviceBuffer.from_host(raw), device.DeviceBuffer.from_host(x),
+                     device.DeviceBuffer(4 * n))
+    n, k, raw, x, w, xd, yd = bufs["small"]
+    device.gemv("Q4_K", w, xd, yd, n, k, stream=s)
+    s.synchronize()
+    ref = yd.to_host(np.float32)
+    assert_matvec_close(ref, G.matmul_f64("Q4_K", x, raw, n, k), G.abs_matmul_f64("Q4_K", x, raw, n, k))
+    with device.Graph.capture(s) as cap:
+        device.gemv("Q4_K", w, xd, yd, n, k, stream=s)
+    try:
+        bn, bk, braw, bx, bw, bxd, byd = bufs["big"]
+        device.gemv("Q4_K", bw, bxd, byd, bn, bk, stream=s)      # grows the stream's scratch
+        s.synchronize()
+        assert_matvec_close(byd.to_host(np.float32), G.matmul_f64("Q4_K", bx, braw, bn, bk),
+                            G.abs_matmul_f64("Q4_K", bx, braw, bn, bk))
+        for _ in range(3):
+            device.copy(yd, xd, 16, stream=s)                       # clobber y eagerly
+            cap.launch(s)
+            s.synchronize()
+            assert bits_equal(yd.to_host(np.float32), ref)
+            device.gemv("Q4_K", bw, bxd, byd, bn, bk, stream=s)
+        s.synchronize()
+    finally:
+        cap.destroy()
+        s.synchronize()
+        s.destroy()
+
+
+def test_weight_cache_drop_in(frq):
+    """The opt-in weight cache: read-only host views are uploaded once per
+    (address, size) and give the bits of the uncached call; writable arrays
+    are never cached; a view of other bytes misses."""
+    import threading
+
+    from flatrun_amd import NativeBackend
+
+    n, k = 700, 3584
+    raw = synth.make_blocks("Q4_K", n, k, seed=21)
+    ro = raw.copy()
+    ro.flags.writeable = False
+    x = synth.make_x(k, seed=22)
+    plain = NativeBackend(weight_cache=False)
+    cached = NativeBackend(weight_cache="1G")
+    ref = plain.matmul_q4k(x, raw, n, k)
+    for _ in range(3):
+        assert bits_equal(cached.matmul_q4k(x, ro, n, k), ref)
+    st = cached.cache_stats()
+    assert st["entries"] == 1 and st["misses"] == 1 and st["hits"] == 2
+    assert bits_equal(cached.matmul_q4k(x, raw, n, k), ref)            # writable: not cached
+    assert cached.cache_stats()["entries"] == 1
+    raw2 = synth.make_blocks("Q4_K", n, k, seed=23)
+    raw2.flags.writeable = False
+    assert bits_equal(cached.matmul_q4k(x, raw2, n, k), plain.matmul_q4k(x, raw2, n, k))
+    assert cached.cache_stats()["entries"] == 2
+    # many threads on one backend: each gets its own x's result
+    xs = [synth.make_x(k, seed=100 + i) for i in range(8)]
+    want = [plain.matmul_q4k(xi, raw, n, k) for xi in xs]
+    got = [None] * len(xs)
+
+    def work(i):
+        for _ in range(5):
+            got[i] = cached.matmul_q4k(xs[i], ro, n, k)
+
+    th = [threading.Thread(target=work, args=(i,)) for i in range(len(xs))]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    for g, w_ in zip(got, want):
+        assert bits_equal(g, w_)
 
 
 def test_resident_weights_match_host_path(backend):
