@@ -126,17 +126,22 @@ struct SkScratch {
 std::mutex g_sk_mu;
 std::map<std::pair<int, hipStream_t>, SkScratch> g_sk;
 
-int grow(void** ptr, size_t* cap, size_t bytes, bool zero, std::vector<void*>* retired) {
+int grow(void** ptr, size_t* cap, size_t bytes, bool zero, std::vector<void*>* retired, hipStream_t stream) {
     if (*cap >= bytes) return FRQ_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    FRQ_HIP(hipStreamIsCapturing(stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(FRQ_ERR_UNSUPPORTED, "scratch for this shape must exist before graph capture: run the call once "
+                                         "on the stream before capturing it");
     size_t want = bytes < ((size_t)1 << 16) ? ((size_t)1 << 16) : bytes;
     if (want < 2 * *cap) want = 2 * *cap;
     void* p = nullptr;
     FRQ_HIP(hipMalloc(&p, want));
-    if (zero) {
-        const hipError_t e = hipMemset(p, 0, want);
+    if (zero) {   // on the launch stream: ordered before the kernel that first reads it
+        const hipError_t e = hipMemsetAsync(p, 0, want, stream);
         if (e != hipSuccess) {
             (void)hipFree(p);
-            return hip_fail(e, "hipMemset(scratch)");
+            return hip_fail(e, "hipMemsetAsync(scratch)");
         }
     }
     if (*ptr) retired->push_back(*ptr);
@@ -154,8 +159,8 @@ int sk_scratch_locked(hipStream_t stream, size_t part_bytes, size_t cnt_bytes, f
     int dev = 0;
     FRQ_HIP(hipGetDevice(&dev));
     SkScratch& sc = g_sk[{dev, stream}];
-    if (int rc = grow(&sc.part, &sc.part_cap, part_bytes, false, &sc.retired)) return rc;
-    if (int rc = grow(&sc.cnt, &sc.cnt_cap, cnt_bytes, true, &sc.retired)) return rc;
+    if (int rc = grow(&sc.part, &sc.part_cap, part_bytes, false, &sc.retired, stream)) return rc;
+    if (int rc = grow(&sc.cnt, &sc.cnt_cap, cnt_bytes, true, &sc.retired, stream)) return rc;
     *part = static_cast<float*>(sc.part);
     *cnt = static_cast<uint32_t*>(sc.cnt);
     return FRQ_OK;
@@ -186,7 +191,13 @@ void sk_release_stream(hipStream_t stream) {
 // else the whole-row kernel when a row fits one workgroup, else split-K.
 int gemv_device(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s) {
     if (frq::gemv_mx_eligible(qtype, w, x, n, k)) {
-        FRQ_HIP(frq::launch_gemv_mx(qtype, w, x, y, n, k, 0, s));
+        frq::MxPlan mp;
+        frq::plan_gemv_mx(n, k, &mp);
+        float* part = nullptr;
+        uint32_t* cnt = nullptr;
+        std::lock_guard<std::mutex> lk(g_sk_mu);
+        if (int rc = sk_scratch_locked(s, 0, frq::gemv_mx_slot_bytes(mp, n), &part, &cnt)) return rc;
+        FRQ_HIP(frq::launch_gemv_mx(w, x, y, n, k, mp, reinterpret_cast<uint64_t*>(cnt), s));
         return FRQ_OK;
     }
     if (frq::gemv_supported(qtype, n, k)) {   // whole-row kernel, one slice: no scratch
@@ -477,19 +488,29 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     hipStream_t s = static_cast<hipStream_t>(stream);
     const uint8_t* wp = static_cast<const uint8_t*>(w);
     if (cfg->kernel == FRQ_GEMV_MX || (cfg->kernel == FRQ_GEMV_AUTO && frq::gemv_mx_eligible(qtype, wp, x, n, k))) {
-        if (qtype != FRQ_Q4_K && qtype != FRQ_Q6_K)
-            return fail(FRQ_ERR_UNSUPPORTED, "the matrix-core GEMV takes Q4_K and Q6_K");
-        int used = 0;
-        hipError_t e = frq::launch_gemv_mx(qtype, wp, x, y, n, k, cfg->rows, s, &used);
+        if (qtype != FRQ_Q4_K) return fail(FRQ_ERR_UNSUPPORTED, "the matrix-core GEMV takes Q4_K");
+        if ((reinterpret_cast<uintptr_t>(wp) | reinterpret_cast<uintptr_t>(x)) & 15)
+            return fail(FRQ_ERR_ALIGN, "the matrix-core GEMV needs 16-byte aligned weights and x");
+        frq::MxPlan mp;
+        mp.rows = cfg->rows;
+        mp.tiles = cfg->cpl;
+        mp.ksplit = cfg->slices;
+        if (!frq::plan_gemv_mx(n, k, &mp))
+            return fail(FRQ_ERR_UNSUPPORTED, "matrix-core GEMV: no plan for n=%lld k=%lld rows=%d tiles=%d ksplit=%d",
+                        (long long)n, (long long)k, cfg->rows, cfg->cpl, cfg->slices);
+        float* part = nullptr;
+        uint32_t* cnt = nullptr;
+        std::lock_guard<std::mutex> lk(g_sk_mu);
+        if (int rc = sk_scratch_locked(s, 0, frq::gemv_mx_slot_bytes(mp, n), &part, &cnt)) return rc;
+        hipError_t e = frq::launch_gemv_mx(wp, x, y, n, k, mp, reinterpret_cast<uint64_t*>(cnt), s);
         if (e != hipSuccess) return hip_fail(e, "launch_gemv_mx");
-        const int64_t nb = k / 256, L = (nb + 15) / 16;
         cfg->kernel = FRQ_GEMV_MX;
-        cfg->cpl = 0;
-        cfg->rows = used;
-        cfg->unroll = (int32_t)L;
-        cfg->slices = 1;
-        cfg->waves_per_wg = (int32_t)((nb + L - 1) / L);
-        cfg->items = (n + used - 1) / used;
+        cfg->cpl = mp.tiles;
+        cfg->rows = mp.rows;
+        cfg->unroll = mp.blocks;
+        cfg->slices = mp.ksplit;
+        cfg->waves_per_wg = mp.waves;
+        cfg->items = mp.grid;
         return FRQ_OK;
     }
     if (cfg->kernel == FRQ_GEMV_SPLITK ||

@@ -51,18 +51,28 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
 // Checks that a GEMV of this shape can be planned; returns false with no launch otherwise.
 bool gemv_supported(int qtype, int64_t n, int64_t k);
 
-// Q4_K / Q6_K GEMV on the matrix cores (frq_gemv_mx.hip), batch 1: k a
-// multiple of 256 up to 16 * mx_max_blocks(qtype) blocks (Q4_K 20480, Q6_K
-// 16384), x 16-byte aligned, w 16-byte (Q4_K) / 2-byte (Q6_K) aligned. The
-// default path takes it (gemv_mx_eligible) for Q4_K when the row rule gives
-// >= kMxMinRows rows per workgroup (n > 1280); Q6_K only through the tuned entry.
-constexpr int kMxMinRows = 6;
-int mx_max_blocks(int qtype);
-int gemv_mx_rows(int64_t n);
+// Q4_K GEMV on the matrix cores (frq_gemv_mx.hip), batch 1: k a multiple of
+// 256, x and w 16-byte aligned. A workgroup owns `rows` output rows (tiles of
+// <= 16 rows, 1 or 2 per wavefront) and the whole row (ksplit 1) or one half
+// of it (ksplit 2: two workgroups per row set, combined through one 64-bit
+// slot per row that must be zero before a launch; every launch leaves it
+// zero, and launches sharing slots must be ordered, e.g. one stream).
+// Wavefronts own `blocks` consecutive 256-element blocks of the range.
+// plan_gemv_mx fills the fields left <= 0 and checks the rest. The default
+// path takes it (gemv_mx_eligible) for Q4_K with n > 1280.
+struct MxPlan {
+    int rows = 0;      // output rows per workgroup (<= 16 * tiles)
+    int tiles = 0;     // 16-row MFMA tiles per wavefront: 1 or 2
+    int ksplit = 0;    // workgroups per row set: 1 or 2
+    int blocks = 0;    // blocks per wavefront (derived, <= 4)
+    int waves = 0;     // wavefronts per workgroup (derived)
+    int64_t grid = 0;  // workgroups (derived)
+};
+bool plan_gemv_mx(int64_t n, int64_t k, MxPlan* plan);
+size_t gemv_mx_slot_bytes(const MxPlan& plan, int64_t n);
 bool gemv_mx_eligible(int qtype, const uint8_t* w, const float* x, int64_t n, int64_t k);
-// rows = output rows per workgroup (1..16; <= 0: gemv_mx_rows(n)); *rows_used gets what ran.
-hipError_t launch_gemv_mx(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int rows,
-                          hipStream_t stream, int* rows_used = nullptr);
+hipError_t launch_gemv_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, const MxPlan& plan,
+                          uint64_t* slots, hipStream_t stream);
 
 // Grouped GEMV: y_i[n_i] = W_i[n_i, k] . x[k] for up to kGemvGroupMax
 // matrices sharing x (q/k/v, gate/up), in ONE launch when every W_i is Q4_K

@@ -130,11 +130,23 @@ int frq_dev_dequant(int qtype, const void* w, size_t w_bytes, int64_t n_elems, f
 
 /* y[b, n] = W[n, k] . x[b, k] for b < batch: the decode matvec of
  * matmul_<q> / matmul_<q>_batched (_C.cpp:99-283) on device buffers.
- * Q4_K rows with k <= 20480 and n > 1280 (w and x 16-byte aligned) run on
- * the matrix cores (int8 MFMA on the nibbles and on x split into four
- * 8-bit digits per 32-element sub-block, exact integer dot products); the
- * other shapes and formats on the element-wise kernels. Both stay within the
- * fp32 accumulation tolerance of the fp64 result; their bits differ. */
+ * Q4_K with n > 1280 and k <= 32768 (w and x 16-byte aligned) runs on the
+ * matrix cores: int8 MFMA on the 4-bit codes and on x written per
+ * 32-element sub-block as a 60-bit fixed-point number relative to the
+ * sub-block's max |x| (eight 8-bit digits), exact integer dot products, then
+ *   y_i = sum_s [ d*sc_s * sum(q x) - dmin*m_s * sum(x) ]
+ * in fp32. Every x within 2^36 of its sub-block's max |x| is carried
+ * exactly; a block whose x is not (a wider range, |x| >= 2^30, inf, NaN) is
+ * computed per weight in fp32 (w = fl(fl(d*sc)*q) - fl(dmin*m), q4_k.h:153-185).
+ * For every finite x the error of row i is therefore within the fp32
+ * accumulation bound  c * 2^-24 * sum_j (d*sc_j*q_ij + dmin*m_j) |x_j|  (c a
+ * small multiple of the summation depth; sum_j |w_ij x_j| for per-weight
+ * blocks), which the tests hold to 1e-5 of sum_j |w_ij x_j| (componentwise)
+ * and of max |y| (normwise). Rows longer than 64 blocks, and n <= 4096 with
+ * k >= 8192, are split in two halves of k over two workgroups that combine
+ * in a fixed order through per-row slots in the stream's scratch. The
+ * other shapes and formats run on the element-wise kernels (the same bound,
+ * other bits). */
 int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
                  int64_t batch, void* stream);
 
@@ -145,11 +157,12 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  *                 fixup) or FRQ_GEMV_ROWS (one workgroup spans all of k)
  *                 or FRQ_GEMV_ROWS_LDS (Q4_K: as ROWS, rows staged through
  *                 an LDS ring of `unroll` rows by direct-to-LDS loads)
- *                 or FRQ_GEMV_MX (the matrix-core kernel: Q4_K, k <= 20480,
- *                 or Q6_K, k <= 16384; `rows` = output rows per workgroup,
- *                 1..16, 0 = choose; on return `unroll` = blocks per
- *                 wavefront). AUTO takes the kernel frq_dev_gemv takes
- *                 (the matrix cores for Q4_K only).
+ *                 or FRQ_GEMV_MX (the matrix-core kernel, Q4_K, k <= 32768:
+ *                 `rows` = output rows per workgroup (<= 16 per tile),
+ *                 `cpl` = 16-row tiles per wavefront (1 or 2), `slices` =
+ *                 workgroups per row (1: k <= 16384, or 2 halves of k), 0 =
+ *                 choose; on return `unroll` = blocks per wavefront). AUTO
+ *                 takes the kernel frq_dev_gemv takes.
  *   cpl           work unit per lane (format specific)
  *   rows          rows per work item (SPLITK) / per workgroup (ROWS)
  *   unroll        rows per load batch
