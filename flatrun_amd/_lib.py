@@ -84,6 +84,7 @@ SIGNATURES: dict[str, list] = {
     "frq_matmul": [_i32, _vp, _sz, _vp, _sz, _sz, _sz, _vp],
     "frq_dev_dequant": [_i32, _vp, _sz, _i64, _vp, _vp],
     "frq_dev_gemv": [_i32, _vp, _sz, _vp, _vp, _i64, _i64, _i64, _vp],
+    "frq_dev_gemv_noalloc": [_i32, _vp, _sz, _vp, _vp, _i64, _i64, _i64, _vp],
     "frq_dev_gemv_group": [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _vp],
     "frq_gemv_group_fusable": [_i32, _vp, _vp, _i64],
     "frq_dev_gemv_tuned": [_i32, _vp, _sz, _vp, _vp, _i64, _i64, _c.c_void_p, _vp],

@@ -189,14 +189,27 @@ void sk_release_stream(hipStream_t stream) {
 
 // One GEMV on device buffers: the matrix-core Q4_K kernel where eligible,
 // else the whole-row kernel when a row fits one workgroup, else split-K.
-int gemv_device(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s) {
+// Scratch (the matrix-core kernel's per-row exchange slots when rows are
+// split over two workgroups, the split-K partials) comes from the stream's
+// registry, or from `fixed` when given (nothing is allocated then; a shape
+// that needs more than `fixed` holds is refused before anything launches).
+int gemv_device(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s,
+                const frq::FixedScratch* fixed = nullptr) {
     if (frq::gemv_mx_eligible(qtype, w, x, n, k)) {
         frq::MxPlan mp;
         frq::plan_gemv_mx(n, k, &mp);
+        const size_t need = frq::gemv_mx_slot_bytes(mp, n);
+        if (fixed) {
+            if (need > fixed->slot_bytes)
+                return fail(FRQ_ERR_UNSUPPORTED, "gemv: %zu bytes of row slots needed, the fixed scratch holds %zu",
+                            need, fixed->slot_bytes);
+            FRQ_HIP(frq::launch_gemv_mx(w, x, y, n, k, mp, fixed->slots, s));
+            return FRQ_OK;
+        }
         float* part = nullptr;
         uint32_t* cnt = nullptr;
         std::lock_guard<std::mutex> lk(g_sk_mu);
-        if (int rc = sk_scratch_locked(s, 0, frq::gemv_mx_slot_bytes(mp, n), &part, &cnt)) return rc;
+        if (int rc = sk_scratch_locked(s, 0, need, &part, &cnt)) return rc;
         FRQ_HIP(frq::launch_gemv_mx(w, x, y, n, k, mp, reinterpret_cast<uint64_t*>(cnt), s));
         return FRQ_OK;
     }
@@ -209,12 +222,37 @@ int gemv_device(int qtype, const uint8_t* w, const float* x, float* y, int64_t n
         return fail(FRQ_ERR_UNSUPPORTED, "gemv: k=%lld has no kernel plan for this format", (long long)k);
     size_t pb = 0, cb = 0;
     frq::gemv_sk_scratch(sp, n, &pb, &cb);
+    if (fixed) {
+        if (pb > fixed->part_bytes || cb > 0)
+            return fail(FRQ_ERR_UNSUPPORTED, "gemv: %zu bytes of split-K partials needed, the fixed scratch holds %zu",
+                        pb, fixed->part_bytes);
+        FRQ_HIP(frq::launch_gemv_sk(qtype, w, x, y, n, k, sp, fixed->part, nullptr, s));
+        return FRQ_OK;
+    }
     float* part = nullptr;
     uint32_t* cnt = nullptr;
     std::lock_guard<std::mutex> lk(g_sk_mu);
     if (int rc = sk_scratch_locked(s, pb, cb, &part, &cnt)) return rc;
     FRQ_HIP(frq::launch_gemv_sk(qtype, w, x, y, n, k, sp, part, cnt, s));
     return FRQ_OK;
+}
+
+// Scratch a GEMV of this shape needs (0 for both when none), for callers
+// that bring their own: slot bytes must be zero before the launch.
+void gemv_scratch_need(int qtype, const uint8_t* w, const float* x, int64_t n, int64_t k, size_t* slot_bytes,
+                       size_t* part_bytes) {
+    *slot_bytes = *part_bytes = 0;
+    if (frq::gemv_mx_eligible(qtype, w, x, n, k)) {
+        frq::MxPlan mp;
+        frq::plan_gemv_mx(n, k, &mp);
+        *slot_bytes = frq::gemv_mx_slot_bytes(mp, n);
+        return;
+    }
+    if (frq::gemv_supported(qtype, n, k)) return;
+    frq::SplitKPlan sp;
+    if (!frq::plan_gemv_sk(qtype, n, k, &sp)) return;
+    size_t cb = 0;
+    frq::gemv_sk_scratch(sp, n, part_bytes, &cb);
 }
 
 // Host dequant: stage weight, decode, copy back. n_elems may be ragged.
@@ -425,8 +463,8 @@ static int dev_gemv_checks(int qtype, const void* w, size_t w_bytes, const float
     return FRQ_OK;
 }
 
-int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
-                 int64_t batch, void* stream) {
+static int dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
+                    int64_t batch, void* stream, const frq::FixedScratch* fixed) {
     Fmt f;
     if (int rc = dev_gemv_checks(qtype, w, w_bytes, x, y, n, k, batch, &f)) return rc;
     if (n == 0 || batch == 0) return FRQ_OK;
@@ -435,9 +473,24 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
         FRQ_HIP(frq::launch_fill(y, 0.0f, batch * n, s));
         return FRQ_OK;
     }
+    const uint8_t* wp = static_cast<const uint8_t*>(w);
+    if (fixed) {   // refuse an oversized shape before any row is launched
+        size_t sb = 0, pb = 0;
+        gemv_scratch_need(qtype, wp, x, n, k, &sb, &pb);
+        if (sb > fixed->slot_bytes || pb > fixed->part_bytes)
+            return fail(FRQ_ERR_UNSUPPORTED,
+                        "%s gemv n=%lld k=%lld needs %zu slot + %zu partial bytes of scratch; the fixed scratch "
+                        "holds %zu + %zu", f.name, (long long)n, (long long)k, sb, pb, fixed->slot_bytes,
+                        fixed->part_bytes);
+    }
     for (int64_t b = 0; b < batch; ++b)
-        if (int rc = gemv_device(qtype, static_cast<const uint8_t*>(w), x + b * k, y + b * n, n, k, s)) return rc;
+        if (int rc = gemv_device(qtype, wp, x + b * k, y + b * n, n, k, s, fixed)) return rc;
     return FRQ_OK;
+}
+
+int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
+                 int64_t batch, void* stream) {
+    return dev_gemv(qtype, w, w_bytes, x, y, n, k, batch, stream, nullptr);
 }
 
 int frq_gemv_group_fusable(int count, const int* qtypes, const void* const* w, int64_t k) {
@@ -747,3 +800,13 @@ int frq_graph_destroy(void* ex) {
 }
 
 }  // extern "C"
+
+namespace frq {
+// frq_dev_gemv with its scratch in `fixed` (frq_noalloc.hip).
+int dev_gemv_fixed(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
+                   int64_t batch, void* stream, const FixedScratch& fixed) {
+    return dev_gemv(qtype, w, w_bytes, x, y, n, k, batch, stream, &fixed);
+}
+int fail_unsupported(const char* msg) { return fail(FRQ_ERR_UNSUPPORTED, "%s", msg); }
+int fail_hip(hipError_t e, const char* what) { return hip_fail(e, what); }
+}  // namespace frq

@@ -131,4 +131,20 @@ size_t gemm_bf16_scratch(int64_t m, int64_t n, int64_t k);
 hipError_t launch_gemm_bf16(int qtype, const uint8_t* w, const uint16_t* x, float* y, int64_t m, int64_t n, int64_t k,
                             hipStream_t stream, float* part = nullptr);
 
+// Scratch a caller brings in place of the stream registry's: exchange slots
+// (zero before a launch, left zero by every launch) and split-K partials.
+struct FixedScratch {
+    uint64_t* slots = nullptr;
+    size_t slot_bytes = 0;
+    float* part = nullptr;
+    size_t part_bytes = 0;
+};
+// frq_dev_gemv with its scratch taken from `fixed` (frq_api.cpp); allocates
+// nothing and refuses shapes that need more than `fixed` holds.
+int dev_gemv_fixed(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
+                   int64_t batch, void* stream, const FixedScratch& fixed);
+// Sets the calling thread's error message and returns FRQ_ERR_UNSUPPORTED / FRQ_ERR_HIP.
+int fail_unsupported(const char* msg);
+int fail_hip(hipError_t e, const char* what);
+
 }  // namespace frq

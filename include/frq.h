@@ -150,6 +150,24 @@ int frq_dev_dequant(int qtype, const void* w, size_t w_bytes, int64_t n_elems, f
 int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
                  int64_t batch, void* stream);
 
+/* frq_dev_gemv that allocates nothing. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, kernels and results (bit for bit) as frq_dev_gemv; the scratch
+ * that frq_dev_gemv grows per stream is one fixed device array of
+ * FRQ_NOALLOC_SCRATCH_BYTES per GPU instead (held until the process ends):
+ * 1 MiB of row-exchange slots (8 bytes per output row of a Q4_K matrix whose
+ * rows are split over two workgroups: n <= 131072) and 3 MiB of split-K
+ * partials (n x slices x 4 bytes, rows longer than one workgroup). A shape
+ * that needs more is refused with FRQ_ERR_UNSUPPORTED before anything is
+ * launched. Every call on a GPU shares that GPU's array: calls that overlap
+ * on one GPU (different streams or threads) race; calls ordered on one
+ * stream do not. The first call on a device clears the slots with a kernel
+ * on `stream`; every launch leaves them zero. */
+#define FRQ_NOALLOC_SCRATCH_BYTES (4u << 20)
+int frq_dev_gemv_noalloc(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
+                         int64_t batch, void* stream);
+
 /* Launch geometry of one GEMV, for tuning sweeps and profiling. Fields set
  * to 0 are chosen by the library; on return every field holds what ran.
  *   kernel        FRQ_GEMV_AUTO, FRQ_GEMV_SPLITK (one wavefront per
