@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 from conftest import assert_matvec_close, bits_equal
-from flatrun_amd import NativeBackend, device, synth
+from flatrun_amd import NativeBackend, _lib, device, synth
 from oracle import gguf_np as G
 
 pytestmark = pytest.mark.gpu
@@ -91,12 +91,13 @@ def test_llama_layer_grouped_full_size(frq):
 
 @pytest.mark.parametrize("q,n,k", [("Q8_0", 4864, 896), ("Q4_K", 18944, 3584), ("Q1_0", 4096, 4096),
                                    ("Q5_K", 18944, 3584), ("Q6_K", 152064, 3584)])
-def test_full_size_dequant_checksum(frq, q, n, k):
+def test_full_size_dequant_word_for_word(frq, q, n, k):
     """Dequant at a benchmark config's full size (the lm_head: 545M outputs,
-    2.2 GB of fp32), bit for bit: the XOR of every fp32 output word, folded on
-    the device by the library's streaming read, equals the XOR of the oracle's
-    words, dequantized on the host in row chunks; the first, a middle and the
-    last chunk of rows are also compared word for word."""
+    2.2 GB of fp32), bit for bit and in place: every chunk of rows is copied
+    back and compared word for word with the oracle's decode of the same
+    rows, so a wrong element order fails as surely as a wrong value. The
+    device-side XOR fold of all output words (the streaming read kernel)
+    must also equal the oracle's."""
     raw = synth.make_blocks(q, n, k, seed=n + 3 * k)
     row_bytes = synth.nbytes(q, 1, k)
     w = device.DeviceBuffer.from_host(raw)
@@ -110,19 +111,17 @@ def test_full_size_dequant_checksum(frq, q, n, k):
         gpu_fold = int(np.bitwise_xor.reduce(out.to_host(np.uint32)))
         rows = max(1, (1 << 24) // k)
         host_fold = 0
-        spots = {0, (n // 2) // rows * rows, (n - 1) // rows * rows}
+        got = np.empty(rows * k, np.uint32)
         for r0 in range(0, n, rows):
             r1 = min(n, r0 + rows)
             ref = decode(raw[r0 * row_bytes:r1 * row_bytes], (r1 - r0) * k).view(np.uint32)
             host_fold ^= int(np.bitwise_xor.reduce(ref))
-            if r0 in spots:                          # copy back just this chunk of rows
-                part = device.DeviceBuffer(4 * (r1 - r0) * k)
-                try:
-                    device.copy(part, y.ptr + 4 * r0 * k, 4 * (r1 - r0) * k)
-                    device.synchronize()
-                    assert np.array_equal(part.to_host(np.uint32), ref), (q, n, k, r0)
-                finally:
-                    part.free()
+            part = got[:(r1 - r0) * k]
+            _lib.check(_lib.lib().frq_memcpy_d2h(part.ctypes.data, y.ptr + 4 * r0 * k, part.nbytes))
+            if not np.array_equal(part, ref):
+                bad = int(np.flatnonzero(part != ref)[0])
+                raise AssertionError(f"{q} {n}x{k}: first differing element at row {r0 + bad // k}, "
+                                     f"column {bad % k}: {part[bad]:#010x} != {ref[bad]:#010x}")
         assert gpu_fold == host_fold, (q, n, k, hex(gpu_fold), hex(host_fold))
     finally:
         w.free()
