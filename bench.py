@@ -31,8 +31,10 @@ Printed: ONE JSON line with
              HBM peak; per GEMV config also the reference's CPU paths timed on
              this host: native 1 thread, row-parallel on every core, NumPy),
              the Llama-3-8B decode-step weight sweep (ms/step,
-             graph replay and eager; resident and streamed), the prefill
-             GEMM, the copy and read ceilings, and a GGUF file -> HBM load.
+             graph replay and eager; resident and streamed), the fp32
+             batched matvec at seq 4 / 32 / 512 (the re-prefill call), the
+             prefill GEMM, the copy and read ceilings, and a GGUF file -> HBM
+             load.
 """
 
 from __future__ import annotations
@@ -90,23 +92,23 @@ class GemvWorkload:
     """Rotating device copies of one seeded weight, x and y resident in HBM."""
 
     def __init__(self, q: str, n: int, k: int, seed: int, stream, rotate_bytes: int = ROTATE_BYTES,
-                 kernel: int | None = None):
-        self.q, self.n, self.k, self.kernel = q, n, k, kernel
+                 kernel: int | None = None, batch: int = 1):
+        self.q, self.n, self.k, self.kernel, self.batch = q, n, k, kernel, batch
         self.raw = synth.make_blocks(q, n, k, seed=seed)
         self.ncopies = max(2, math.ceil(rotate_bytes / self.raw.nbytes))
         self.w = [device.DeviceBuffer.from_host(self.raw) for _ in range(self.ncopies)]
-        self.x_host = synth.make_x(k, seed=seed + 1)
+        self.x_host = synth.make_x(k, seed=seed + 1, batch=batch if batch > 1 else None)
         self.x = device.DeviceBuffer.from_host(self.x_host)
-        self.y = device.DeviceBuffer(4 * n)
+        self.y = device.DeviceBuffer(4 * n * batch)
         self.stream = stream
-        self.bytes = effective_bytes(q, n, k)
+        self.bytes = effective_bytes(q, n, k, batch)
         self.launch(0)                     # first launch allocates any per-stream scratch, outside graph capture
         device.synchronize()
 
     def launch(self, i: int) -> None:
         if self.kernel is None:
-            device.gemv(self.q, self.w[i % self.ncopies], self.x, self.y, self.n, self.k, stream=self.stream,
-                        w_bytes=self.raw.nbytes)
+            device.gemv(self.q, self.w[i % self.ncopies], self.x, self.y, self.n, self.k, batch=self.batch,
+                        stream=self.stream, w_bytes=self.raw.nbytes)
         else:
             device.gemv_tuned(self.q, self.w[i % self.ncopies], self.x, self.y, self.n, self.k, kernel=self.kernel,
                               stream=self.stream, w_bytes=self.raw.nbytes)
@@ -314,6 +316,7 @@ def run_suite(stream, steps: int, only: set | None = None, cpu: bool = True) -> 
              ("llama3_8b_decode_streamed", lambda: decode_sweep_streamed(stream)),
              ("prefill_gemm_q4_k_bf16_512x14336x4096", lambda: prefill_gemm(stream, cpu_baseline_on=cpu)),
              ("llama3_8b_prefill_layer_512", lambda: prefill_layer(stream)),
+             ("batched_f32_q4_k_3584x18944", lambda: batched_f32(stream, cpu_baseline_on=cpu)),
              ("dequant", lambda: dequant_suite(stream)),
              ("copy_ceiling", lambda: copy_ceiling(stream)),
              ("read_ceiling_447MB", lambda: read_ceiling(stream, synth.nbytes("Q6_K", 152064, 3584), reps=50)),
@@ -449,6 +452,45 @@ def prefill_gemm(stream, m: int = 512, n: int = 14336, k: int = 4096, reps: int 
             R.matmul_q4_k_batched(xs, raw, n, k)
             out["cpu"] = {"reference_native_batched_1_thread_ms": round((time.perf_counter() - t0) * m / 4 * 1e3, 1),
                           "sample": f"4 of {m} token rows timed, scaled to {m}"}
+    return out
+
+
+def batched_f32(stream, q: str = "Q4_K", n: int = 3584, k: int = 18944, seqs=(4, 32, 512),
+                cpu_baseline_on: bool = True) -> dict:
+    """The fp32 batched matvec (frq_dev_gemv with batch = seq rows of x), the
+    shape of the reference CLI's re-prefill: every generated token multiplies
+    the whole sequence so far by each weight (matmul_<q>_batched, one fp32
+    matvec per row). One matrix-core GEMM launch reads W once per tile of x
+    rows. Per seq: mean launch time over a graph-replayed region (weight
+    copies rotated past the Infinity Cache), effective GB/s (W once + x + y),
+    GFLOP/s (2 seq n k), and the time of seq single-row launches for
+    comparison; cpu: the reference's native batched matmul (1 thread) on 2
+    rows, scaled to seq."""
+    single = GemvWorkload(q, n, k, seed=300, stream=stream)
+    t1 = single.time_throughput(500, warmup=200) / 500
+    single.free()
+    out = {"shape": f"{q} {n}x{k}", "single_row_us": round(t1 * 1e6, 2)}
+    for seq in seqs:
+        steps = 200 if seq <= 32 else 40
+        w = GemvWorkload(q, n, k, seed=300 + seq, stream=stream, batch=seq)
+        t = w.time_throughput(steps, warmup=20) / steps
+        out[f"seq{seq}"] = {"us": round(t * 1e6, 2), "gbs": round(w.bytes / t / 1e9, 1),
+                            "gflops": round(2 * seq * n * k / t / 1e9, 1),
+                            "seq_single_row_launches_us": round(seq * t1 * 1e6, 1),
+                            "speedup_vs_single_rows": round(seq * t1 / t, 2)}
+        w.free()
+    if cpu_baseline_on:
+        from oracle.loader import ref_C
+
+        R = ref_C()
+        if R is not None:
+            raw = synth.make_blocks(q, n, k, seed=301)
+            xs = synth.make_x(k, seed=302, batch=2)
+            t0 = time.perf_counter()
+            getattr(R, f"matmul_{q.lower()}_batched")(xs, raw, n, k)
+            per_row = (time.perf_counter() - t0) / 2
+            out["cpu"] = {"reference_native_batched_1_thread_ms_per_row": round(per_row * 1e3, 2),
+                          "sample": "2 rows timed; the reference's batched loop is one matvec per row"}
     return out
 
 

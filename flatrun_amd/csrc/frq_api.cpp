@@ -255,6 +255,37 @@ void gemv_scratch_need(int qtype, const uint8_t* w, const float* x, int64_t n, i
     frq::gemv_sk_scratch(sp, n, part_bytes, &cb);
 }
 
+// Rows of x that take the fp32-contract matrix-core GEMM (W read once per
+// tile of x rows) instead of one GEMV per row: Q4_K, Q6_K and Q8_0 with two
+// or more rows.
+bool batched_gemm(int qtype, const uint8_t* w, const float* x, int64_t batch, int64_t n, int64_t k) {
+    if (batch < 2 || !frq::gemm_f32_supported(qtype, batch, n, k)) return false;
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
+    return !(reinterpret_cast<uintptr_t>(x) & 15) && !(qtype == FRQ_Q4_K ? (wa & 15) : (wa & 1));
+}
+
+// y[b * ldy + i] = (W x_b)[i] for b < batch: the GEMM for two or more rows
+// where batched_gemm allows, else one GEMV per row. Scratch as gemv_device.
+int gemv_batched(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int64_t batch,
+                 int64_t ldy, hipStream_t s, const frq::FixedScratch* fixed = nullptr) {
+    if (batched_gemm(qtype, w, x, batch, n, k)) {
+        if (fixed) {   // as many K-splits as the fixed partial region holds
+            FRQ_HIP(frq::launch_gemm_f32(qtype, w, x, y, batch, n, k, ldy, s, fixed->part, fixed->part_bytes));
+            return FRQ_OK;
+        }
+        const size_t pb = frq::gemm_f32_scratch(batch, n, k);
+        float* part = nullptr;
+        uint32_t* cnt = nullptr;
+        std::lock_guard<std::mutex> lk(g_sk_mu);
+        if (int rc = sk_scratch_locked(s, pb, 0, &part, &cnt)) return rc;
+        FRQ_HIP(frq::launch_gemm_f32(qtype, w, x, y, batch, n, k, ldy, s, part, pb));
+        return FRQ_OK;
+    }
+    for (int64_t b = 0; b < batch; ++b)
+        if (int rc = gemv_device(qtype, w, x + b * k, y + b * ldy, n, k, s, fixed)) return rc;
+    return FRQ_OK;
+}
+
 // Host dequant: stage weight, decode, copy back. n_elems may be ragged.
 int host_dequant(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, float* out) {
     if (n_elems == 0) return FRQ_OK;
@@ -291,8 +322,7 @@ int host_matmul(int qtype, const float* x, size_t seq, const uint8_t* weight, si
     float* dy = reinterpret_cast<float*>(dw + wb + xb);
     FRQ_HIP(hipMemcpy(dw, weight, weight_bytes, hipMemcpyHostToDevice));
     FRQ_HIP(hipMemcpy(dx, x, seq * k * 4, hipMemcpyHostToDevice));
-    for (size_t s = 0; s < seq; ++s)
-        if (int rc = gemv_device(qtype, dw, dx + s * k, dy + s * n, (int64_t)n, (int64_t)k, nullptr)) return rc;
+    if (int rc = gemv_batched(qtype, dw, dx, dy, (int64_t)n, (int64_t)k, (int64_t)seq, (int64_t)n, nullptr)) return rc;
     FRQ_HIP(hipMemcpy(out, dy, seq * n * 4, hipMemcpyDeviceToHost));
     return FRQ_OK;
 }
@@ -476,16 +506,15 @@ static int dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, fl
     const uint8_t* wp = static_cast<const uint8_t*>(w);
     if (fixed) {   // refuse an oversized shape before any row is launched
         size_t sb = 0, pb = 0;
-        gemv_scratch_need(qtype, wp, x, n, k, &sb, &pb);
+        if (!batched_gemm(qtype, wp, x, batch, n, k))   // the batched GEMM splits K within what is there
+            gemv_scratch_need(qtype, wp, x, n, k, &sb, &pb);
         if (sb > fixed->slot_bytes || pb > fixed->part_bytes)
             return fail(FRQ_ERR_UNSUPPORTED,
                         "%s gemv n=%lld k=%lld needs %zu slot + %zu partial bytes of scratch; the fixed scratch "
                         "holds %zu + %zu", f.name, (long long)n, (long long)k, sb, pb, fixed->slot_bytes,
                         fixed->part_bytes);
     }
-    for (int64_t b = 0; b < batch; ++b)
-        if (int rc = gemv_device(qtype, wp, x + b * k, y + b * n, n, k, s, fixed)) return rc;
-    return FRQ_OK;
+    return gemv_batched(qtype, wp, x, y, n, k, batch, n, s, fixed);
 }
 
 int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
@@ -516,6 +545,13 @@ int frq_dev_gemv_group(int count, const int* qtypes, const void* const* w, const
     float* yb[frq::kGemvGroupMax];
     for (int i = 0; i < count; ++i) wp[i] = static_cast<const uint8_t*>(w[i]);
     const bool fused = k > 0 && frq::gemv_group_fusable(count, qtypes, wp, k);
+    if (k > 0 && batch >= 2) {   // prefill-shaped: each matrix once, its rows of x together
+        for (int i = 0; i < count; ++i)
+            if (n[i])
+                if (int rc = gemv_batched(qtypes[i], wp[i], x, y[i], n[i], k, batch, y_stride ? y_stride : n[i], s))
+                    return rc;
+        return FRQ_OK;
+    }
     for (int64_t b = 0; b < batch; ++b) {
         for (int i = 0; i < count; ++i) yb[i] = y[i] + b * (y_stride ? y_stride : n[i]);
         if (k == 0) {   // empty dot products are 0 (kernel fill: graph-capturable)

@@ -349,6 +349,17 @@ __global__ void __launch_bounds__(256) gemm_split_reduce_kernel(const float* __r
     }
 }
 
+// The same sum with rows of `cols` elements written `ldy` floats apart.
+__global__ void __launch_bounds__(256) gemm_split_reduce_strided_kernel(const float* __restrict__ part,
+                                                                        float* __restrict__ y, int S, int64_t count,
+                                                                        int64_t cols, int64_t ldy) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    float v = part[i];
+    for (int q = 1; q < S; ++q) v += part[q * count + i];
+    y[(i / cols) * ldy + i % cols] = v;
+}
+
 }  // namespace
 
 bool gemm_bf16_supported(int qtype, int64_t m, int64_t n, int64_t k) {
@@ -378,6 +389,21 @@ int gemm_bf16_splits(int64_t m, int64_t n, int64_t k) {
 size_t gemm_bf16_scratch(int64_t m, int64_t n, int64_t k) {
     const int sp = gemm_bf16_splits(m, n, k);
     return sp > 1 ? (size_t)sp * (size_t)m * (size_t)n * sizeof(float) : 0;
+}
+
+hipError_t launch_split_reduce(const float* part, float* y, int splits, int64_t rows, int64_t cols, int64_t ldy,
+                               hipStream_t stream) {
+    const int64_t count = rows * cols;
+    if (count <= 0) return hipSuccess;
+    if (ldy == cols) {
+        const int64_t threads = (count + 3) / 4;
+        gemm_split_reduce_kernel<<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream>>>(part, y, splits,
+                                                                                                     count);
+    } else {
+        gemm_split_reduce_strided_kernel<<<dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream>>>(
+            part, y, splits, count, cols, ldy);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm_bf16(int qtype, const uint8_t* w, const uint16_t* x, float* y, int64_t m, int64_t n, int64_t k,

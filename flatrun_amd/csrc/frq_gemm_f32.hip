@@ -1,0 +1,417 @@
+// Batched matvec with the fp32 contract on the gfx950 matrix cores:
+//   Y[M, N] (fp32) = X[M, K] (fp32) . W[N, K]^T, W = raw Q4_K, Q6_K or Q8_0 blocks.
+//
+// The reference's batched entry points (matmul_<q>_batched, _C.cpp:154-283)
+// run one fp32 matvec per row of X and dequantize W again for every row. Here
+// W is read once per tile of X rows, and the products run on
+// v_mfma_f32_32x32x16_bf16 without giving up the fp32 contract:
+//   * W enters as its integer codes, which bf16 holds exactly: Q4_K q in
+//     0..15, Q6_K q - 32 in -32..31, Q8_0 q in -128..127;
+//   * X enters as three bf16 pieces, x = x1 + x2 + x3 with x1 = bf16(x),
+//     x2 = bf16(x - x1), x3 = bf16(x - x1 - x2) (round to nearest; every
+//     subtraction is exact), which carry all 24 bits of an fp32 x whose
+//     pieces stay normal (|x| >= 2^-110);
+//   * every product code * piece is exact in fp32, and the matrix cores sum
+//     them in fp32 over one sub-block (Q4_K 32 elements, Q6_K 16, Q8_0 32);
+//   * the sub-block's scale is applied in fp32 per (row, sub-block):
+//     y += d*sc * S - dmin*m * sum(x) (Q4_K), y += d*sc * S (Q6_K),
+//     y += d * S (Q8_0), with sum(x) of the sub-block in fp32.
+// So every row's error is bounded like the matvec kernels':
+//   |y - y_exact| <= c * 2^-24 * sum_j (|s_j q_j| + |t_j|) |x_j|,
+// c a small multiple of the summation depth (tested at 1e-5 against fp64).
+//
+// Tiling: a workgroup of 4 waves owns a BM x BN tile of Y (WM x WN waves of
+// 32 x 64, two 32 x 32 MFMA tiles each) and walks K in steps of 32. Each
+// step stages X's three bf16 pieces and sum(x) (BM rows) and W's codes and
+// per-row scales (BN rows) into LDS, double-buffered, the next step's global
+// loads in flight during this step's MFMAs. Few output tiles (few X rows)
+// split K over S workgroups whose fp32 partial planes a second kernel adds
+// in split order (deterministic).
+// MFMA operand layouts (32x32x16, 8 bf16 per lane): A lane l holds row l%32,
+// k = 8*(l/32) .. +7 of the 16-k slice; B lane l holds column l%32, same k;
+// D register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#include "frq_common.h"
+#include "frq_kernels.h"
+
+namespace frq {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kCK = 32;              // K per step
+constexpr int kCRow = kCK + 8;       // bf16 per LDS row (rows padded to 80 bytes)
+
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));   // round to nearest even
+}
+__device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+// Codes of one step for one W row: `cnt` (16 or 32) consecutive elements of
+// the step starting at element `k0` of the step, as bf16, plus the row's
+// scales for the step (written by the thread with k0 == 0).
+template <int QT>
+struct CFmt;
+
+// Q4_K: step j of a block is sub-block j (32 elements): qs bytes
+// 32 (j >> 1) + i, low nibbles for even j, high for odd (gguf.py:209-219).
+template <>
+struct CFmt<kTypeQ4K> {
+    static constexpr int kBytes = kQ4KBytes, kElems = kQKElems;
+    template <int CNT>
+    struct Raw {
+        u32x4 h;
+        u32x4 q[CNT / 16];
+    };
+    template <int CNT>
+    __device__ static void load(Raw<CNT>& r, const uint8_t* wrow, int step, int k0) {
+        const uint8_t* bp = wrow + (int64_t)(step >> 3) * kQ4KBytes;
+        const int j = step & 7;
+        r.h = *reinterpret_cast<const u32x4*>(bp);
+#pragma unroll
+        for (int c = 0; c < CNT / 16; ++c) r.q[c] = *reinterpret_cast<const u32x4*>(bp + 16 + 32 * (j >> 1) + k0 + 16 * c);
+    }
+    template <int CNT>
+    __device__ static void codes(const Raw<CNT>& r, int step, uint32_t* out, float* scl, bool first) {
+        const int j = step & 7;
+        const uint32_t sh = (j & 1) ? 4u : 0u;
+#pragma unroll
+        for (int c = 0; c < CNT / 16; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t v = (r.q[c][i] >> sh) & 0x0F0F0F0Fu;
+                out[8 * c + 2 * i] = bf16_pair((float)(v & 15u), (float)((v >> 8) & 15u));
+                out[8 * c + 2 * i + 1] = bf16_pair((float)((v >> 16) & 15u), (float)(v >> 24));
+            }
+        if (first) {
+            uint32_t sc, mn;
+            k4_scale_min(r.h[1], r.h[2], r.h[3], j, sc, mn);
+            scl[0] = f16_bits_to_f32(r.h[0]) * (float)sc;
+            scl[1] = f16_bits_to_f32(r.h[0] >> 16) * (float)mn;
+        }
+    }
+};
+
+// Q8_0: a step is one block [d f16][q int8 x 32] (34 bytes, 2-byte aligned).
+template <>
+struct CFmt<kTypeQ80> {
+    static constexpr int kBytes = kQ80Bytes, kElems = kQ80Elems;
+    template <int CNT>
+    struct Raw {
+        uint32_t d;
+        uint32_t q[CNT / 4];
+    };
+    template <int CNT>
+    __device__ static void load(Raw<CNT>& r, const uint8_t* wrow, int step, int k0) {
+        const uint8_t* bp = wrow + (int64_t)step * kQ80Bytes;
+        r.d = ld_u16(bp);
+#pragma unroll
+        for (int i = 0; i < CNT / 4; ++i) r.q[i] = ld_u32_a2(bp + 2 + k0 + 4 * i);
+    }
+    template <int CNT>
+    __device__ static void codes(const Raw<CNT>& r, int step, uint32_t* out, float* scl, bool first) {
+        (void)step;
+#pragma unroll
+        for (int i = 0; i < CNT / 4; ++i) {
+            const uint32_t v = r.q[i];
+            out[2 * i] = bf16_pair((float)(int)(int8_t)(v & 0xFFu), (float)(int)(int8_t)((v >> 8) & 0xFFu));
+            out[2 * i + 1] = bf16_pair((float)(int)(int8_t)((v >> 16) & 0xFFu), (float)(int)(int8_t)(v >> 24));
+        }
+        if (first) {
+            scl[0] = f16_bits_to_f32(r.d);
+            scl[1] = 0.0f;
+        }
+    }
+};
+
+// Q6_K: step j of a block covers elements 32j .. 32j+31 = 128h + 32ks + l
+// (h = j >> 2, ks = j & 3, l < 32): q = nibble of ql[64h + 32 (ks & 1) + l]
+// (high nibble for ks >= 2) | bits 2ks, 2ks+1 of qh[32h + l] << 4, code
+// q - 32, scale sc[8h + l / 16 + 2ks] (gguf.py:401-419): two 16-element
+// sub-blocks per step. Fields are 2-byte aligned (210-byte blocks).
+template <>
+struct CFmt<kTypeQ6K> {
+    static constexpr int kBytes = kQ6KBytes, kElems = kQKElems;
+    template <int CNT>
+    struct Raw {
+        uint32_t ql[CNT / 4], qh[CNT / 4];
+        uint32_t sc, d;
+    };
+    template <int CNT>
+    __device__ static void load(Raw<CNT>& r, const uint8_t* wrow, int step, int k0) {
+        const uint8_t* bp = wrow + (int64_t)(step >> 3) * kQ6KBytes;
+        const int j = step & 7, h = j >> 2, ks = j & 3;
+#pragma unroll
+        for (int i = 0; i < CNT / 4; ++i) {
+            r.ql[i] = ld_u32_a2(bp + 64 * h + 32 * (ks & 1) + k0 + 4 * i);
+            r.qh[i] = ld_u32_a2(bp + 128 + 32 * h + k0 + 4 * i);
+        }
+        r.sc = ld_u16(bp + 192 + 8 * h + 2 * ks);   // sc[8h + 2ks], sc[8h + 2ks + 1]
+        r.d = ld_u16(bp + 208);
+    }
+    template <int CNT>
+    __device__ static void codes(const Raw<CNT>& r, int step, uint32_t* out, float* scl, bool first) {
+        const int ks = step & 3;
+        const uint32_t nsh = ks >= 2 ? 4u : 0u, hsh = 2u * (uint32_t)ks;
+#pragma unroll
+        for (int i = 0; i < CNT / 4; ++i) {
+            const uint32_t q = ((r.ql[i] >> nsh) & 0x0F0F0F0Fu) | (((r.qh[i] >> hsh) & 0x03030303u) << 4);
+            out[2 * i] = bf16_pair((float)((int)(q & 63u) - 32), (float)((int)((q >> 8) & 63u) - 32));
+            out[2 * i + 1] = bf16_pair((float)((int)((q >> 16) & 63u) - 32), (float)((int)(q >> 24) - 32));
+        }
+        if (first) {
+            const float d = f16_bits_to_f32(r.d);
+            scl[0] = d * (float)(int)(int8_t)(r.sc & 0xFFu);
+            scl[1] = d * (float)(int)(int8_t)((r.sc >> 8) & 0xFFu);
+        }
+    }
+};
+
+template <int QT, int WM, int WN>
+__global__ void __launch_bounds__(256) gemm_f32c_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                        float* __restrict__ y, int M, int N, int K, int64_t ldy, int S,
+                                                        float* __restrict__ part) {
+    static_assert(WM * WN == 4, "four waves");
+    constexpr int BM = 32 * WM, BN = 64 * WN;
+    constexpr int XT = 256 / BM, XV = kCK / XT;      // X staging: threads per row, values per thread
+    constexpr int WT = 256 / BN, WV = kCK / WT;      // W staging: threads per row, codes per thread
+    static_assert((XV == 4 || XV == 8) && (WV == 16 || WV == 32), "staging shapes");
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2][3][BM * kCRow];
+    __shared__ __attribute__((aligned(16))) uint16_t ws[2][BN * kCRow];
+    __shared__ __attribute__((aligned(16))) float xsum[2][BM];
+    __shared__ __attribute__((aligned(16))) float wsc[2][BN][2];
+    using F = CFmt<QT>;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % WM, wn = wave / WM;
+    const int mtiles = (M + BM - 1) / BM;
+    const int mt = (int)(blockIdx.x % mtiles), rest = (int)(blockIdx.x / mtiles);
+    const int split = rest % S, nt = rest / S;
+    const int m0 = mt * BM, n0 = nt * BN;
+    const int64_t row_bytes = (int64_t)(K / F::kElems) * F::kBytes;
+    const int total = K / kCK;                          // K-split `split` covers steps [sbase, sbase + steps)
+    const int sbase = (int)((int64_t)split * total / S);
+    const int steps = (int)((int64_t)(split + 1) * total / S) - sbase;
+
+    const int xr = tid / XT, xk = (tid % XT) * XV;    // X staging: row xr, elements xk .. xk + XV - 1
+    const float* xrow = x + (int64_t)(m0 + xr < M ? m0 + xr : M - 1) * K;
+    const int wr = tid / WT, wk = (tid % WT) * WV;    // W staging: row wr, codes wk .. wk + WV - 1
+    const uint8_t* wrow = w + (int64_t)(n0 + wr < N ? n0 + wr : N - 1) * row_bytes;
+
+    struct Stage {
+        f32x4 xv[XV / 4];
+        typename F::template Raw<WV> wr;
+    };
+    Stage st;
+    auto load_step = [&](int s) __attribute__((always_inline)) {
+        const int kb = (sbase + s) * kCK;
+#pragma unroll
+        for (int i = 0; i < XV / 4; ++i) st.xv[i] = *reinterpret_cast<const f32x4*>(xrow + kb + xk + 4 * i);
+        F::template load<WV>(st.wr, wrow, sbase + s, wk);
+    };
+    auto stage_step = [&](int buf, int s) __attribute__((always_inline)) {
+        // X: three bf16 pieces per value and the row's sum over the step
+        uint32_t p1[XV / 2], p2[XV / 2], p3[XV / 2];
+        float sx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XV / 2; ++i) {
+            const float a = st.xv[i >> 1][2 * (i & 1)], b = st.xv[i >> 1][2 * (i & 1) + 1];
+            sx += a + b;
+            p1[i] = bf16_pair(a, b);
+            const float ra = a - bf16_lo(p1[i]), rb = b - bf16_hi(p1[i]);
+            p2[i] = bf16_pair(ra, rb);
+            p3[i] = bf16_pair(ra - bf16_lo(p2[i]), rb - bf16_hi(p2[i]));
+        }
+        const int xo = xr * kCRow + xk;
+        if constexpr (XV == 8) {
+            *reinterpret_cast<u32x4*>(&xs[buf][0][xo]) = u32x4{p1[0], p1[1], p1[2], p1[3]};
+            *reinterpret_cast<u32x4*>(&xs[buf][1][xo]) = u32x4{p2[0], p2[1], p2[2], p2[3]};
+            *reinterpret_cast<u32x4*>(&xs[buf][2][xo]) = u32x4{p3[0], p3[1], p3[2], p3[3]};
+        } else {
+            *reinterpret_cast<u32x2*>(&xs[buf][0][xo]) = u32x2{p1[0], p1[1]};
+            *reinterpret_cast<u32x2*>(&xs[buf][1][xo]) = u32x2{p2[0], p2[1]};
+            *reinterpret_cast<u32x2*>(&xs[buf][2][xo]) = u32x2{p3[0], p3[1]};
+        }
+        if constexpr (XV == 4) {   // 8 values per row-quad lane group: sum over the XT lanes of the row
+            static_assert(XT == 8, "layout");
+            sx += dpp_mov<0xB1>(sx);
+            sx += dpp_mov<0x4E>(sx);
+            sx += dpp_mov<0x141>(sx);
+        } else {
+            static_assert(XT == 4, "layout");
+            sx += dpp_mov<0xB1>(sx);
+            sx += dpp_mov<0x4E>(sx);
+        }
+        if (tid % XT == 0) xsum[buf][xr] = sx;
+        // W: codes and per-row scales
+        uint32_t cw[WV / 2];
+        float scl[2];
+        F::template codes<WV>(st.wr, sbase + s, cw, scl, wk == 0);
+#pragma unroll
+        for (int i = 0; i < WV / 8; ++i)
+            *reinterpret_cast<u32x4*>(&ws[buf][wr * kCRow + wk + 8 * i]) = u32x4{cw[4 * i], cw[4 * i + 1], cw[4 * i + 2],
+                                                                                cw[4 * i + 3]};
+        if (wk == 0) {
+            wsc[buf][wr][0] = scl[0];
+            wsc[buf][wr][1] = scl[1];
+        }
+    };
+
+    f32x16 acc[2];
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[ni][r] = 0.0f;
+
+    const int arow = 32 * wm + (lane & 31), kh = 8 * (lane >> 5);
+    auto compute = [&](int buf) __attribute__((always_inline)) {
+        f32x16 cs[2];
+        // sum(x) of the lane's 16 rows (Q4_K min term): rows 32 wm + 8 i + 4 (l / 32) + j
+        f32x4 sxr[4];
+        if constexpr (QT == kTypeQ4K) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                sxr[i] = *reinterpret_cast<const f32x4*>(&xsum[buf][32 * wm + 8 * i + 4 * (lane >> 5)]);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            bf16x8 a[3], b[2];
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+                a[p] = *reinterpret_cast<const bf16x8*>(&xs[buf][p][arow * kCRow + 16 * ks + kh]);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+                b[ni] = *reinterpret_cast<const bf16x8*>(&ws[buf][(64 * wn + 32 * ni + (lane & 31)) * kCRow + 16 * ks + kh]);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                if (QT == kTypeQ6K || ks == 0) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) cs[ni][r] = 0.0f;
+                }
+#pragma unroll
+                for (int p = 0; p < 3; ++p) cs[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[p], b[ni], cs[ni], 0, 0, 0);
+            }
+            if (QT == kTypeQ6K || ks == 1) {   // one sub-block done: scale it into the accumulators
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni) {
+                    const int nl = 64 * wn + 32 * ni + (lane & 31);
+                    const float s = wsc[buf][nl][QT == kTypeQ6K ? ks : 0];
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[ni][r] = __builtin_fmaf(s, cs[ni][r], acc[ni][r]);
+                    if constexpr (QT == kTypeQ4K) {
+                        const float t = wsc[buf][nl][1];
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[ni][r] = __builtin_fmaf(-t, sxr[r >> 2][r & 3], acc[ni][r]);
+                    }
+                }
+            }
+        }
+    };
+
+    load_step(0);
+    stage_step(0, 0);
+    __syncthreads();
+    for (int s = 0; s < steps; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < steps) load_step(s + 1);
+        compute(buf);
+        if (s + 1 < steps) stage_step(buf ^ 1, s + 1);
+        __syncthreads();
+    }
+
+    // S > 1: this split's partial tile goes to plane `split` (rows of N)
+    float* out = S == 1 ? y : part + (int64_t)split * M * N;
+    const int64_t ld = S == 1 ? ldy : N;
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+        const int n = n0 + 64 * wn + 32 * ni + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = m0 + 32 * wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < M && n < N) out[(int64_t)m * ld + n] = acc[ni][r];
+        }
+    }
+}
+
+template <int QT>
+void f32c_go(bool small_m, dim3 g, hipStream_t s, const uint8_t* w, const float* x, float* y, int M, int N, int K,
+             int64_t ldy, int S, float* part) {
+    if (small_m)
+        gemm_f32c_kernel<QT, 1, 4><<<g, dim3(256), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
+    else
+        gemm_f32c_kernel<QT, 2, 2><<<g, dim3(256), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
+}
+
+// Tile shape: BM x BN = 32 x 256 for up to 32 rows of X, else 64 x 128.
+void f32c_tile(int64_t m, int* bm, int* bn) {
+    const bool small = m <= 32;
+    *bm = small ? 32 : 64;
+    *bn = small ? 256 : 128;
+}
+
+}  // namespace
+
+bool gemm_f32_supported(int qtype, int64_t m, int64_t n, int64_t k) {
+    const int64_t kq = qtype == kTypeQ80 ? kQ80Elems : (qtype == kTypeQ4K || qtype == kTypeQ6K) ? kQKElems : 0;
+    if (kq == 0 || m <= 0 || n <= 0 || k <= 0 || k % kq || m > 0x7FFFFFFF || n > 0x7FFFFFFF || k > 0x7FFFFFFF)
+        return false;
+    int bm, bn;
+    f32c_tile(m, &bm, &bn);
+    return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) <= 0x7FFFFFFF;
+}
+
+// K-splits: the largest S in {1, 2, 4, ..., 64} that leaves every split >= 8
+// steps (splits differ by at most one step), keeps the grid within two
+// workgroups per CU and its partial planes within `part_cap` bytes; shapes
+// that fill the GPU are not split.
+int gemm_f32_splits(int64_t m, int64_t n, int64_t k, size_t part_cap) {
+    int bm, bn;
+    f32c_tile(m, &bm, &bn);
+    const int64_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+    const int64_t steps = k / kCK;
+    const double plane = (double)m * (double)n * sizeof(float);
+    int best = 1;
+    for (int sp = 2; sp <= 64; sp *= 2) {
+        if (steps / sp < 8 || tiles * sp > 512 || sp * plane > (double)part_cap) break;
+        best = sp;
+    }
+    return best;
+}
+
+size_t gemm_f32_scratch(int64_t m, int64_t n, int64_t k, size_t part_cap) {
+    const int sp = gemm_f32_splits(m, n, k, part_cap);
+    return sp > 1 ? (size_t)sp * (size_t)m * (size_t)n * sizeof(float) : 0;
+}
+
+hipError_t launch_gemm_f32(int qtype, const uint8_t* w, const float* x, float* y, int64_t m, int64_t n, int64_t k,
+                           int64_t ldy, hipStream_t stream, float* part, size_t part_cap) {
+    if (ldy < n) return hipErrorInvalidValue;
+    if (!gemm_f32_supported(qtype, m, n, k)) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(x) & 15) return hipErrorInvalidValue;
+    if (qtype == kTypeQ4K && (reinterpret_cast<uintptr_t>(w) & 15)) return hipErrorInvalidValue;
+    if (qtype != kTypeQ4K && (reinterpret_cast<uintptr_t>(w) & 1)) return hipErrorInvalidValue;
+    const int sp = gemm_f32_splits(m, n, k, part ? part_cap : 0);
+    int bm, bn;
+    f32c_tile(m, &bm, &bn);
+    const int64_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+    if (tiles * sp > 0x7FFFFFFF) return hipErrorInvalidValue;
+    const dim3 g((unsigned)(tiles * sp));
+    const bool small = bm == 32;
+    switch (qtype) {
+        case kTypeQ4K: f32c_go<kTypeQ4K>(small, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
+        case kTypeQ6K: f32c_go<kTypeQ6K>(small, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
+        case kTypeQ80: f32c_go<kTypeQ80>(small, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
+        default: return hipErrorInvalidValue;
+    }
+    if (sp > 1) return launch_split_reduce(part, y, sp, m, n, ldy, stream);
+    return hipGetLastError();
+}
+
+}  // namespace frq

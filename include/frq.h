@@ -146,7 +146,15 @@ int frq_dev_dequant(int qtype, const void* w, size_t w_bytes, int64_t n_elems, f
  * k >= 8192, are split in two halves of k over two workgroups that combine
  * in a fixed order through per-row slots in the stream's scratch. The
  * other shapes and formats run on the element-wise kernels (the same bound,
- * other bits). */
+ * other bits).
+ * batch >= 2 with Q4_K, Q6_K or Q8_0 (x 16-byte aligned, k a multiple of the
+ * block) is one fp32-contract GEMM that reads W once per 32 or 64 rows of x:
+ * bf16 matrix cores on W's exact integer codes and on x split into three
+ * bf16 pieces (all 24 bits of every x with |x| >= 2^-110), fp32 sums per
+ * sub-block, then the sub-block scales in fp32 -- the same error bound, other
+ * bits than one row at a time. Few output tiles split k over workgroups
+ * whose fp32 partials a second kernel adds in a fixed order (scratch of the
+ * stream). Q5_K and Q1_0 run one matvec per row. */
 int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
                  int64_t batch, void* stream);
 
@@ -158,9 +166,12 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  * FRQ_NOALLOC_SCRATCH_BYTES per GPU instead (held until the process ends):
  * 1 MiB of row-exchange slots (8 bytes per output row of a Q4_K matrix whose
  * rows are split over two workgroups: n <= 131072) and 3 MiB of split-K
- * partials (n x slices x 4 bytes, rows longer than one workgroup). A shape
- * that needs more is refused with FRQ_ERR_UNSUPPORTED before anything is
- * launched. Every call on a GPU shares that GPU's array: calls that overlap
+ * partials (n x slices x 4 bytes, rows longer than one workgroup). A batch-1
+ * shape that needs more is refused with FRQ_ERR_UNSUPPORTED before anything
+ * is launched. The batched GEMM (batch >= 2) splits k only as far as its
+ * partials (splits x batch x n x 4 bytes) fit in the 3 MiB, so it never
+ * refuses; where that is fewer splits than frq_dev_gemv takes, the bits
+ * differ from frq_dev_gemv's within the same bound. Every call on a GPU shares that GPU's array: calls that overlap
  * on one GPU (different streams or threads) race; calls ordered on one
  * stream do not. The first call on a device clears the slots with a kernel
  * on `stream`; every launch leaves them zero. */

@@ -52,16 +52,20 @@ def test_gemv_shapes(frq, q, n, k):
 
 
 @pytest.mark.parametrize("q", QS)
-def test_gemv_batched_equals_rows(frq, q):
+def test_gemv_batched(frq, q):
+    """Batched host entry: Q4_K, Q6_K and Q8_0 rows go through the fp32
+    GEMM (W read once), checked against the oracle; Q5_K and Q1_0 run one
+    GEMV per row, bit for bit the single-row results."""
     be = synth.BLOCK[q][1]
     n, k = 45, 8 * be
     raw = synth.make_blocks(q, n, k, seed=3)
     xs = synth.make_x(k, seed=4, batch=3)
     yb = gpu_matmul(q, xs, raw, n, k)
     assert yb.shape == (3, n)
-    for s in range(3):
-        assert bits_equal(yb[s], gpu_matmul(q, xs[s], raw, n, k))
     check(q, raw, xs, n, k, yb)
+    if q in ("Q5_K", "Q1_0"):
+        for s in range(3):
+            assert bits_equal(yb[s], gpu_matmul(q, xs[s], raw, n, k))
 
 
 @pytest.mark.parametrize("q", ["Q4_K", "Q6_K", "Q8_0"])

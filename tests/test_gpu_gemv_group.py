@@ -45,7 +45,7 @@ def run_group(parts_spec, k, seed=0, batch=1, concat=True):
         sep = []
         for (q, n), w, r in zip(parts_spec, ws, raws):
             ys = device.DeviceBuffer(max(4, batch * n * 4))
-            if n and fusable:       # the element-wise kernels, row by row
+            if n and fusable and batch == 1:       # the element-wise kernels
                 for b in range(batch):
                     device.gemv_tuned(q, w, xd.ptr + 4 * b * k, ys.ptr + 4 * b * n, n, k, kernel=_lib.GEMV_ROWS,
                                       w_bytes=r.nbytes)

@@ -280,7 +280,7 @@ def test_mx_repeat_and_graph_replay(frq):
 
 
 def test_mx_batched_rows(frq):
-    """frq_dev_gemv with batch 3 runs the kernel once per x row."""
+    """frq_dev_gemv with batch 3 (Q4_K): every row meets the oracle."""
     n, k, b = 2048, 4096, 3
     raw = synth.make_blocks("Q4_K", n, k, seed=31)
     xs = synth.make_x(k, seed=32, batch=b)
@@ -293,8 +293,6 @@ def test_mx_batched_rows(frq):
         ys = yd.to_host(np.float32).reshape(b, n)
         for i in range(b):
             oracle_check(ys[i], raw, xs[i], n, k, f"batch row {i}")
-            y1, _ = run_mx(raw, xs[i], n, k)
-            assert bits_equal(ys[i], y1)
     finally:
         w.free()
         xd.free()
