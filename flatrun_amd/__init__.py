@@ -21,7 +21,6 @@ Typical use::
 
 from __future__ import annotations
 
-import collections
 import os
 import threading
 
@@ -29,6 +28,7 @@ import numpy as np
 
 from . import _C, _lib
 from ._lib import FrqError, LibraryMissing
+from .residency import WeightCache
 
 __all__ = [
     "NativeBackend",
@@ -128,50 +128,6 @@ def _cache_capacity(setting) -> int:
         raise ValueError(f"FLATRUN_AMD_WEIGHT_CACHE={setting!r}: expected 0/1 or a size such as 48G") from e
 
 
-class _WeightCache:
-    """Device copies of read-only host weight views, least recently used first out.
-
-    The key is the view's (address, byte count). An entry holds a reference
-    to the host array, so the memory behind a cached address stays mapped and
-    cannot be reused for other bytes while the entry lives; only read-only
-    arrays are cached (the reference's raw views are read-only mmap slices,
-    core/tensor.py:227-267), so the bytes behind a key do not change.
-    """
-
-    def __init__(self, capacity: int):
-        self.capacity = int(capacity)
-        self.bytes = 0
-        self.hits = self.misses = 0
-        self._entries: collections.OrderedDict = collections.OrderedDict()
-
-    def lookup(self, raw: np.ndarray):
-        """The resident copy of `raw`, uploading it on a miss; None if `raw`
-        is writable or larger than the whole cache."""
-        if raw.flags.writeable or raw.nbytes == 0 or raw.nbytes > self.capacity:
-            return None
-        key = (int(raw.ctypes.data), int(raw.nbytes))
-        hit = self._entries.get(key)
-        if hit is not None:
-            self._entries.move_to_end(key)
-            self.hits += 1
-            return hit[1]
-        self.misses += 1
-        while self._entries and self.bytes + raw.nbytes > self.capacity:
-            _, (_, old) = self._entries.popitem(last=False)
-            self.bytes -= old.nbytes
-            old.buffer.free()
-        dw = DeviceWeight(raw)
-        self._entries[key] = (raw, dw)
-        self.bytes += raw.nbytes
-        return dw
-
-    def clear(self) -> None:
-        for _, dw in self._entries.values():
-            dw.buffer.free()
-        self._entries.clear()
-        self.bytes = 0
-
-
 class NativeBackend:
     """Facade over the gfx950 kernels; mirrors python/__init__.py:85-227.
 
@@ -181,11 +137,16 @@ class NativeBackend:
     reference's calls do under the GIL.
 
     ``weight_cache`` (default: the FLATRUN_AMD_WEIGHT_CACHE environment
-    setting, off when unset) keeps a device copy of every read-only weight
-    view passed to a matmul, keyed by the view's (address, byte count), so a
-    forwarder that passes the same mmap slices every step pays the host to
-    device weight copy once (see _WeightCache). True = up to 64 GiB, an int
-    or "48G"-style string = that many bytes.
+    setting, off when unset) keeps a device copy of every host weight passed
+    to a matmul, keyed by its content (byte count and 128-bit digest,
+    flatrun_amd.residency), so a forwarder that passes the same weights every
+    step -- as fresh copies, which is what the reference's mmap handles
+    return -- pays the host to device weight copy once and a hash per call.
+    True = up to 64 GiB, an int or "48G"-style string = that many bytes.
+
+    :meth:`attach_stream` binds a :class:`flatrun_amd.streaming.SchedulerStream`:
+    weights of the layer it has streamed for the scheduler are then taken
+    from its device ring (checked before the cache).
 
     Attributes
     ----------
@@ -200,23 +161,38 @@ class NativeBackend:
         self._scratch = None
         self._lock = threading.RLock()
         cap = _cache_capacity(os.environ.get("FLATRUN_AMD_WEIGHT_CACHE") if weight_cache is None else weight_cache)
-        self._cache = _WeightCache(cap) if cap > 0 else None
+        self._cache = WeightCache(cap) if cap > 0 else None
+        self._stream_src = None
+
+    def attach_stream(self, stream) -> None:
+        """Take the weights of the scheduler's current layer from `stream`'s
+        device ring (a SchedulerStream; None detaches). Weights it does not
+        hold go the usual way."""
+        with self._lock:
+            self._stream_src = stream
 
     def cache_stats(self) -> dict:
         """Weight-cache occupancy: bytes, entries, hits, misses (zeros when off)."""
         c = self._cache
         if c is None:
             return {"enabled": False, "bytes": 0, "entries": 0, "hits": 0, "misses": 0}
-        return {"enabled": True, "capacity": c.capacity, "bytes": c.bytes, "entries": len(c._entries),
+        return {"enabled": True, "capacity": c.capacity, "bytes": c.bytes, "entries": len(c),
                 "hits": c.hits, "misses": c.misses}
 
     def _cached(self, weight):
-        """The resident copy of a host weight view when the cache is on and
-        takes it, else None. The caller holds the lock until its launch has
-        finished: a later lookup may evict (free) the entry."""
-        if self._cache is None or isinstance(weight, DeviceWeight):
+        """The device copy of a host weight from the attached stream or the
+        cache, else None. The caller holds the lock until its launch has
+        finished: a later lookup may evict (free) a cache entry."""
+        if isinstance(weight, DeviceWeight) or (self._cache is None and self._stream_src is None):
             return None
-        return self._cache.lookup(_raw_bytes(weight).reshape(-1))
+        raw = _raw_bytes(weight).reshape(-1)
+        if self._stream_src is not None:
+            dw = self._stream_src.lookup(raw)
+            if dw is not None:
+                return dw
+        if self._cache is None:
+            return None
+        return self._cache.lookup(raw, DeviceWeight)
 
     def _scratch_for(self, need: int):
         """The scratch buffer, grown to `need` bytes; the caller holds the lock
@@ -236,7 +212,7 @@ class NativeBackend:
     def _matmul(self, qname: str, x, weight, n: int, k: int):
         self._require()
         x_c = np.ascontiguousarray(x, dtype=np.float32)
-        if self._cache is not None and not isinstance(weight, DeviceWeight):
+        if (self._cache is not None or self._stream_src is not None) and not isinstance(weight, DeviceWeight):
             with self._lock:
                 cached = self._cached(weight)
                 if cached is not None:

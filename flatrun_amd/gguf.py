@@ -35,7 +35,6 @@ import mmap
 import os
 import struct
 import time
-from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -414,44 +413,17 @@ class ResidentModel:
 
     def _upload(self, infos, offs, staging: int, threads: int, stream) -> None:
         from . import device
+        from .streaming import StagedCopier
 
-        staging = max(staging, 1 << 16)
-        slots = [device.PinnedBuffer(staging) for _ in range(2)]
-        done = [device.Event() for _ in range(2)]
-        used = [False, False]
         cs = device.Stream() if stream is None else stream
-        pool = ThreadPoolExecutor(max_workers=max(1, threads))
-        src_all = np.frombuffer(self.file._mm, dtype=np.uint8) if infos else None
-
-        def fill(dst: np.ndarray, src: np.ndarray) -> None:
-            parts = max(1, min(threads, src.size >> 20))
-            step = (src.size + parts - 1) // parts
-            list(pool.map(lambda i: np.copyto(dst[i * step:(i + 1) * step], src[i * step:(i + 1) * step]),
-                          range(parts)))
-
+        copier = StagedCopier(staging, threads)
         try:
-            k = 0
             for t in infos:
-                pos = 0
-                while pos < t.nbytes:
-                    m = min(staging, t.nbytes - pos)
-                    s = k & 1
-                    if used[s]:
-                        done[s].synchronize()          # the slot's previous transfer has finished
-                    fill(slots[s].array[:m], src_all[t.offset + pos: t.offset + pos + m])
-                    device.memcpy_h2d_async(self.arena.ptr + offs[t.name] + pos, slots[s].ptr, m, stream=cs)
-                    done[s].record(cs)
-                    used[s] = True
-                    pos += m
-                    k += 1
+                copier.copy(self.arena.ptr + offs[t.name],
+                            np.frombuffer(self.file._mm, dtype=np.uint8, count=t.nbytes, offset=t.offset), cs)
             cs.synchronize()
         finally:
-            pool.shutdown()
-            del src_all
-            for e in done:
-                e.destroy()
-            for p in slots:
-                p.free()
+            copier.close()
             if stream is None:
                 cs.destroy()
 

@@ -270,9 +270,10 @@ def test_split_k_scratch_growth_keeps_captured_graph_valid(frq):
 
 
 def test_weight_cache_drop_in(frq):
-    """The opt-in weight cache: read-only host views are uploaded once per
-    (address, size) and give the bits of the uncached call; writable arrays
-    are never cached; a view of other bytes misses."""
+    """The opt-in weight cache: a host weight is uploaded once per content
+    (size and digest) and gives the bits of the uncached call, whether the
+    caller passes the same array, a writable copy, or a fresh copy per call
+    (what the reference's mmap handles return); other bytes miss."""
     import threading
 
     from flatrun_amd import NativeBackend
@@ -289,8 +290,12 @@ def test_weight_cache_drop_in(frq):
         assert bits_equal(cached.matmul_q4k(x, ro, n, k), ref)
     st = cached.cache_stats()
     assert st["entries"] == 1 and st["misses"] == 1 and st["hits"] == 2
-    assert bits_equal(cached.matmul_q4k(x, raw, n, k), ref)            # writable: not cached
-    assert cached.cache_stats()["entries"] == 1
+    assert bits_equal(cached.matmul_q4k(x, raw, n, k), ref)            # writable, same bytes: a hit
+    for _ in range(2):                                                  # a fresh bytes copy per call
+        view = np.ndarray(shape=(raw.size,), dtype=np.uint8, buffer=raw.tobytes())
+        assert bits_equal(cached.matmul_q4k(x, view, n, k), ref)
+    st = cached.cache_stats()
+    assert st["entries"] == 1 and st["misses"] == 1 and st["hits"] == 5
     raw2 = synth.make_blocks("Q4_K", n, k, seed=23)
     raw2.flags.writeable = False
     assert bits_equal(cached.matmul_q4k(x, raw2, n, k), plain.matmul_q4k(x, raw2, n, k))
