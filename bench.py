@@ -321,7 +321,8 @@ def run_suite(stream, steps: int, only: set | None = None, cpu: bool = True) -> 
              ("copy_ceiling", lambda: copy_ceiling(stream)),
              ("read_ceiling_447MB", lambda: read_ceiling(stream, synth.nbytes("Q6_K", 152064, 3584), reps=50)),
              ("gguf_load_llama3_8b_4_layers", lambda: gguf_load(stream)),
-             ("host_path_q4_k_3584x18944", host_path_rate)]
+             ("host_path_q4_k_3584x18944", host_path_rate),
+             ("drop_in_host_call_q4_k_3584x18944", drop_in_host_call)]
     for name, fn in extra:
         if want(name):
             out[name] = fn()
@@ -491,6 +492,67 @@ def batched_f32(stream, q: str = "Q4_K", n: int = 3584, k: int = 18944, seqs=(4,
             per_row = (time.perf_counter() - t0) / 2
             out["cpu"] = {"reference_native_batched_1_thread_ms_per_row": round(per_row * 1e3, 2),
                           "sample": "2 rows timed; the reference's batched loop is one matvec per row"}
+    return out
+
+
+def drop_in_host_call(q: str = "Q4_K", n: int = 3584, k: int = 18944, reps: int = 20) -> dict:
+    """The one-line drop-in (NativeBackend.matmul_q4k(x, raw, n, k) on host
+    arrays), per call, median ms of `reps`, with the weight read from a file
+    mapping as the reference's forwarder reads it:
+      copy_view     what MmapTensorHandle.view returns (core/tensor.py:240-247):
+                    an array over ``mmap[a:b]``, a fresh bytes copy per call
+                    (the copy is timed inside the call, as the forwarder pays it);
+      zero_copy     an array over ``memoryview(mmap)[a:b]`` (no copy; file-backed);
+    each without the weight cache (the weight crosses PCIe every call) and
+    with it (content key: a hash of the copy per call, or once for the
+    file-backed view). ``handle_copy_ms`` is the reference's copy alone."""
+    import mmap
+    import tempfile
+
+    from flatrun_amd import NativeBackend
+
+    raw = synth.make_blocks(q, n, k, seed=41)
+    x = synth.make_x(k, seed=42)
+    meth = {"Q4_K": "matmul_q4k", "Q6_K": "matmul_q6_k", "Q8_0": "matmul_q8_0"}[q]
+    nb = raw.nbytes
+
+    def med(fn) -> float:
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return round(float(np.median(ts)) * 1e3, 3)
+
+    out = {"shape": f"{q} {n}x{k}", "weight_bytes": nb}
+    with tempfile.TemporaryDirectory() as d:
+        path = Path(d) / "w.bin"
+        path.write_bytes(raw.tobytes())
+        with open(path, "rb") as fh:
+            mm = mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ)
+
+            def copy_view():
+                a = np.ndarray(shape=(nb,), dtype=np.uint8, buffer=mm[0:nb])
+                a.flags.writeable = False
+                return a
+
+            def zero_view():
+                a = np.ndarray(shape=(nb,), dtype=np.uint8, buffer=memoryview(mm)[0:nb])
+                a.flags.writeable = False
+                return a
+
+            out["handle_copy_ms"] = med(lambda: mm[0:nb])
+            for cache in (False, True):
+                be = NativeBackend(weight_cache="4G" if cache else False)
+                for vname, view in (("copy_view", copy_view), ("zero_copy", zero_view)):
+                    out[f"{vname}_{'cached' if cache else 'uncached'}_ms"] = med(
+                        lambda: getattr(be, meth)(x, view(), n, k))
+                if cache:
+                    st = be.cache_stats()
+                    out["cache_hits"], out["cache_misses"] = st["hits"], st["misses"]
+                    be._cache.clear()
+            mm.close()
     return out
 
 
@@ -726,6 +788,25 @@ def decode_sweep_resident(stream, steps: int, layers: int = 32, cpu_baseline_on:
     fused_ok = all(device.gemv_group_fusable([(p[0], p[1]) for p in parts], k)
                    for parts, k in groups[0] if len(parts) > 1)
     ycat.free()
+    # the forwarder's chain with resident activations (flatrun_amd.layer):
+    # q|k|v -> o (on the q part) -> gate|up -> SiLU.mul -> down, per layer
+    from flatrun_amd.layer import DecoderProjections
+
+    drivers = [DecoderProjections({nm: (spec[nm][0], dev[L][nm], spec[nm][1], kk, host[nm].nbytes)
+                                   for nm, _, _, kk in LLAMA_LAYER}, max_seq=1, stream=stream)
+               for L in range(layers)]
+
+    def step_driver():
+        for L, dp in enumerate(drivers):
+            qkv = dp.qkv_proj(x)
+            dp.mlp(dp.o_proj(qkv))          # seq 1: the q part leads each qkv row
+
+    with device.Graph.capture(stream) as capd:
+        step_driver()
+    ms_d = timed(lambda: capd.launch(stream))
+    capd.destroy()
+    for dp in drivers:
+        dp.close()
     for d in dev:
         for b in d.values():
             b.free()
@@ -736,7 +817,12 @@ def decode_sweep_resident(stream, steps: int, layers: int = 32, cpu_baseline_on:
             "floor_ms_at_8TBs": round(total / 8e12 * 1e3, 4),
             "fused_shared_x": {"ms_per_step": round(ms_f, 4), "launches_per_step": layers * 4,
                                "gbs": round(total / (ms_f / 1e3) / 1e9, 1), "groups_fused": fused_ok,
-                               "note": "q|k|v and gate|up as one grouped launch each"}}
+                               "note": "q|k|v and gate|up as one grouped launch each"},
+            "decoder_chain_resident": {"ms_per_step": round(ms_d, 4), "launches_per_step": layers * 5,
+                                       "gbs": round(total / (ms_d / 1e3) / 1e9, 1),
+                                       "note": "DecoderProjections per layer: q|k|v grouped, o on the q part, "
+                                               "gate|up grouped, SiLU.mul, down; activations resident, "
+                                               "one graph per step"}}
 
 
 def main() -> int:

@@ -741,6 +741,19 @@ int frq_dev_read_xor(const void* src, size_t bytes, uint32_t* out, void* stream)
     return FRQ_OK;
 }
 
+int frq_dev_silu_mul(const float* gateup, int64_t ld_in, float* out, int64_t ld_out, int64_t rows, int64_t inter,
+                     void* stream) {
+    if (rows < 0 || inter < 0) return fail(FRQ_ERR_INVALID, "silu_mul: negative rows or inter");
+    if (rows == 0 || inter == 0) return FRQ_OK;
+    if (ld_in < 2 * inter || ld_out < inter)
+        return fail(FRQ_ERR_INVALID, "silu_mul: ld_in must be >= 2 inter and ld_out >= inter");
+    if (!gateup || !out) return fail(FRQ_ERR_INVALID, "silu_mul: null buffer");
+    if (((reinterpret_cast<uintptr_t>(gateup) | reinterpret_cast<uintptr_t>(out)) & 3) != 0)
+        return fail(FRQ_ERR_ALIGN, "silu_mul: buffers must be 4-byte aligned");
+    FRQ_HIP(frq::launch_silu_mul(gateup, ld_in, out, ld_out, rows, inter, static_cast<hipStream_t>(stream)));
+    return FRQ_OK;
+}
+
 int frq_set_device(int device) { FRQ_HIP(hipSetDevice(device)); return FRQ_OK; }
 int frq_malloc(void** ptr, size_t bytes) {
     if (!ptr) return fail(FRQ_ERR_INVALID, "null ptr");

@@ -153,6 +153,11 @@ size_t gemm_f32_scratch(int64_t m, int64_t n, int64_t k, size_t part_cap = SIZE_
 hipError_t launch_gemm_f32(int qtype, const uint8_t* w, const float* x, float* y, int64_t m, int64_t n, int64_t k,
                            int64_t ldy, hipStream_t stream, float* part, size_t part_cap);
 
+// out[r, i] = silu(gateup[r, i]) * gateup[r, inter + i] for r < rows, rows of
+// gateup ld_in floats apart and of out ld_out apart (frq_act.hip).
+hipError_t launch_silu_mul(const float* gateup, int64_t ld_in, float* out, int64_t ld_out, int64_t rows,
+                           int64_t inter, hipStream_t stream);
+
 // Scratch a caller brings in place of the stream registry's: exchange slots
 // (zero before a launch, left zero by every launch) and split-K partials.
 struct FixedScratch {

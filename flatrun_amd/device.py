@@ -339,3 +339,12 @@ def dequant(qtype, w, y, n_elems: int, stream=None, w_bytes: int | None = None) 
     q = qtype_id(qtype)
     wb = _nbytes(w) if w_bytes is None else int(w_bytes)
     check(lib().frq_dev_dequant(q, _addr(w), wb, int(n_elems), _addr(y), _stream(stream)))
+
+
+def silu_mul(gateup, out, rows: int, inter: int, ld_in: int = 0, ld_out: int = 0, stream=None) -> None:
+    """out[r, :inter] = silu(gate) * up for the grouped gate|up rows of
+    gateup (gate first; rows ld_in floats apart, default 2 inter; out rows
+    ld_out apart, default inter), enqueued (frq_dev_silu_mul)."""
+    li = int(ld_in) or 2 * int(inter)
+    lo = int(ld_out) or int(inter)
+    check(lib().frq_dev_silu_mul(_addr(gateup), li, _addr(out), lo, int(rows), int(inter), _stream(stream)))

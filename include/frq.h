@@ -270,6 +270,16 @@ int frq_dev_copy(void* dst, const void* src, size_t bytes, void* stream);
 enum { FRQ_READ_XOR_WORDS = 2048 };
 int frq_dev_read_xor(const void* src, size_t bytes, uint32_t* out, void* stream);
 
+/* The SwiGLU activation between a decoder block's gate|up and down
+ * projections, on device: out[r * ld_out + i] = silu(g) * u with
+ * g = gateup[r * ld_in + i], u = gateup[r * ld_in + inter + i] (the grouped
+ * gate|up output, gate first) for r < rows, i < inter; ld_in >= 2 inter,
+ * ld_out >= inter, 4-byte aligned. The fp32 operations of the forwarder's
+ * NumPy chain in its order (exp(-g), + 1, reciprocal, * g, * u;
+ * model/qwen2.py:1703-1740); only exp's last-place rounding differs. */
+int frq_dev_silu_mul(const float* gateup, int64_t ld_in, float* out, int64_t ld_out, int64_t rows, int64_t inter,
+                     void* stream);
+
 /* ------------------------------------------- memory, streams and events
  * Thin wrappers so a ctypes caller needs no other HIP binding. Streams are
  * created at the default priority.                                         */

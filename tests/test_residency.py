@@ -47,12 +47,12 @@ def test_file_backed_detection(mapped):
 
 def test_digest_content_and_order():
     rng = np.random.default_rng(1)
-    big = rng.integers(0, 256, 3 * residency.CHUNK + 1234, dtype=np.uint8)    # chunked path
+    c = 1 << 20
+    big = rng.integers(0, 256, 3 * c + 1234, dtype=np.uint8)
     k0 = residency.content_key(big)
     assert k0 == residency.content_key(big.copy()) and k0[0] == big.size
-    swapped = np.concatenate([big[residency.CHUNK:2 * residency.CHUNK], big[:residency.CHUNK],
-                              big[2 * residency.CHUNK:]])
-    assert residency.content_key(swapped) != k0                  # chunk order is part of the digest
+    swapped = np.concatenate([big[c:2 * c], big[:c], big[2 * c:]])
+    assert residency.content_key(swapped) != k0                  # order is part of the digest
     flip = big.copy()
     flip[-1] ^= 1
     assert residency.content_key(flip) != k0
