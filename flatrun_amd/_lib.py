@@ -31,7 +31,7 @@ QTYPES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K, "Q1_0": Q1_0,
 BLOCKS = {Q8_0: (34, 32), Q4_K: (144, 256), Q5_K: (176, 256), Q6_K: (210, 256), Q1_0: (18, 128)}
 
 
-GEMV_AUTO, GEMV_SPLITK, GEMV_ROWS, GEMV_ROWS_LDS, GEMV_MX = 0, 1, 2, 3, 4
+GEMV_AUTO, GEMV_SPLITK, GEMV_ROWS, GEMV_ROWS_LDS, GEMV_MX, GEMV_MX_H = 0, 1, 2, 3, 4, 5
 
 
 class GemvConfig(ctypes.Structure):

@@ -576,7 +576,8 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     if (n == 0 || k == 0) return fail(FRQ_ERR_SHAPE, "tuned gemv needs n > 0 and k > 0");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const uint8_t* wp = static_cast<const uint8_t*>(w);
-    if (cfg->kernel == FRQ_GEMV_MX || (cfg->kernel == FRQ_GEMV_AUTO && frq::gemv_mx_eligible(qtype, wp, x, n, k))) {
+    if (cfg->kernel == FRQ_GEMV_MX || cfg->kernel == FRQ_GEMV_MX_H ||
+        (cfg->kernel == FRQ_GEMV_AUTO && frq::gemv_mx_eligible(qtype, wp, x, n, k))) {
         if (qtype != FRQ_Q4_K) return fail(FRQ_ERR_UNSUPPORTED, "the matrix-core GEMV takes Q4_K");
         if ((reinterpret_cast<uintptr_t>(wp) | reinterpret_cast<uintptr_t>(x)) & 15)
             return fail(FRQ_ERR_ALIGN, "the matrix-core GEMV needs 16-byte aligned weights and x");
@@ -584,6 +585,7 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
         mp.rows = cfg->rows;
         mp.tiles = cfg->cpl;
         mp.ksplit = cfg->slices;
+        mp.layout = cfg->kernel == FRQ_GEMV_MX_H ? 1 : cfg->kernel == FRQ_GEMV_MX ? 0 : -1;
         if (!frq::plan_gemv_mx(n, k, &mp))
             return fail(FRQ_ERR_UNSUPPORTED, "matrix-core GEMV: no plan for n=%lld k=%lld rows=%d tiles=%d ksplit=%d",
                         (long long)n, (long long)k, cfg->rows, cfg->cpl, cfg->slices);
@@ -593,7 +595,7 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
         if (int rc = sk_scratch_locked(s, 0, frq::gemv_mx_slot_bytes(mp, n), &part, &cnt)) return rc;
         hipError_t e = frq::launch_gemv_mx(wp, x, y, n, k, mp, reinterpret_cast<uint64_t*>(cnt), s);
         if (e != hipSuccess) return hip_fail(e, "launch_gemv_mx");
-        cfg->kernel = FRQ_GEMV_MX;
+        cfg->kernel = mp.layout == 1 ? FRQ_GEMV_MX_H : FRQ_GEMV_MX;
         cfg->cpl = mp.tiles;
         cfg->rows = mp.rows;
         cfg->unroll = mp.blocks;

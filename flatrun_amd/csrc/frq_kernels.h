@@ -64,6 +64,8 @@ struct MxPlan {
     int rows = 0;      // output rows per workgroup (<= 16 * tiles)
     int tiles = 0;     // 16-row MFMA tiles per wavefront: 1 or 2
     int ksplit = 0;    // workgroups per row set: 1 or 2
+    int layout = -1;   // weight loads: 0 header / qs 0..63 / qs 64..127 per block, 1 the headers of a
+                       // wavefront's blocks in one load (frq_gemv_mx.hip); < 0 = choose
     int blocks = 0;    // blocks per wavefront (derived, <= 4)
     int waves = 0;     // wavefronts per workgroup (derived)
     int64_t grid = 0;  // workgroups (derived)

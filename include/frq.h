@@ -190,8 +190,11 @@ int frq_dev_gemv_noalloc(int qtype, const void* w, size_t w_bytes, const float* 
  *                 `rows` = output rows per workgroup (<= 16 per tile),
  *                 `cpl` = 16-row tiles per wavefront (1 or 2), `slices` =
  *                 workgroups per row (1: k <= 16384, or 2 halves of k), 0 =
- *                 choose; on return `unroll` = blocks per wavefront). AUTO
- *                 takes the kernel frq_dev_gemv takes.
+ *                 choose; on return `unroll` = blocks per wavefront)
+ *                 or FRQ_GEMV_MX_H (the same with the block headers of a
+ *                 wavefront's blocks in one load per row, shared across
+ *                 lanes with ds_bpermute). AUTO takes the kernel
+ *                 frq_dev_gemv takes.
  *   cpl           work unit per lane (format specific)
  *   rows          rows per work item (SPLITK) / per workgroup (ROWS)
  *   unroll        rows per load batch
@@ -199,7 +202,8 @@ int frq_dev_gemv_noalloc(int qtype, const void* w, size_t w_bytes, const float* 
  *                 kernels (an input of 0 or 1; anything else is rejected)
  *   waves_per_wg  wavefronts per workgroup (output)
  *   items         work items / workgroups launched (output)              */
-enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2, FRQ_GEMV_ROWS_LDS = 3, FRQ_GEMV_MX = 4 };
+enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2, FRQ_GEMV_ROWS_LDS = 3, FRQ_GEMV_MX = 4,
+       FRQ_GEMV_MX_H = 5 };
 typedef struct {
     int32_t kernel, cpl, rows, unroll, slices, waves_per_wg;
     int64_t items;
