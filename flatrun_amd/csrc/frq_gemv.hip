@@ -1315,17 +1315,19 @@ void q80_go(dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, f
     gemv_q8_0_ring_kernel<(U < R ? U : R), R><<<gd, bd, 0, s>>>(w, x, y, n, nb);
 }
 
-hipError_t launch_q80_ring(int rows, int waves, int64_t grid, const uint8_t* w, const float* x, float* y, int64_t n,
-                           int nb, hipStream_t s) {
+hipError_t launch_q80_ring(int ring, int rows, int waves, int64_t grid, const uint8_t* w, const float* x, float* y,
+                           int64_t n, int nb, hipStream_t s) {
+    // ring >= rows: every row's loads in flight at once; else 4 rows at a time
     const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
+    const bool full = ring >= rows;
     switch (rows) {
         case 1: q80_go<4, 1>(gd, bd, s, w, x, y, n, nb); break;
         case 2: q80_go<4, 2>(gd, bd, s, w, x, y, n, nb); break;
         case 4: q80_go<4, 4>(gd, bd, s, w, x, y, n, nb); break;
-        case 7: q80_go<4, 7>(gd, bd, s, w, x, y, n, nb); break;
-        case 8: q80_go<4, 8>(gd, bd, s, w, x, y, n, nb); break;
-        case 14: q80_go<4, 14>(gd, bd, s, w, x, y, n, nb); break;
-        case 16: q80_go<4, 16>(gd, bd, s, w, x, y, n, nb); break;
+        case 7: if (full) q80_go<7, 7>(gd, bd, s, w, x, y, n, nb); else q80_go<4, 7>(gd, bd, s, w, x, y, n, nb); break;
+        case 8: if (full) q80_go<8, 8>(gd, bd, s, w, x, y, n, nb); else q80_go<4, 8>(gd, bd, s, w, x, y, n, nb); break;
+        case 14: if (full) q80_go<14, 14>(gd, bd, s, w, x, y, n, nb); else q80_go<4, 14>(gd, bd, s, w, x, y, n, nb); break;
+        case 16: if (full) q80_go<16, 16>(gd, bd, s, w, x, y, n, nb); else q80_go<4, 16>(gd, bd, s, w, x, y, n, nb); break;
         default: return hipErrorInvalidConfiguration;
     }
     return hipGetLastError();
@@ -1344,17 +1346,19 @@ void q10_go(dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, f
     gemv_q1_0_ring_kernel<(U < R ? U : R), R><<<gd, bd, 0, s>>>(w, x, y, n, nb);
 }
 
-hipError_t launch_q10_ring(int rows, int waves, int64_t grid, const uint8_t* w, const float* x, float* y, int64_t n,
-                           int nb, hipStream_t s) {
+hipError_t launch_q10_ring(int ring, int rows, int waves, int64_t grid, const uint8_t* w, const float* x, float* y,
+                           int64_t n, int nb, hipStream_t s) {
+    // ring >= rows: every row's loads in flight at once; else 4 rows at a time
     const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
+    const bool full = ring >= rows;
     switch (rows) {
         case 1: q10_go<4, 1>(gd, bd, s, w, x, y, n, nb); break;
         case 2: q10_go<4, 2>(gd, bd, s, w, x, y, n, nb); break;
         case 4: q10_go<4, 4>(gd, bd, s, w, x, y, n, nb); break;
-        case 7: q10_go<4, 7>(gd, bd, s, w, x, y, n, nb); break;
-        case 8: q10_go<4, 8>(gd, bd, s, w, x, y, n, nb); break;
-        case 14: q10_go<4, 14>(gd, bd, s, w, x, y, n, nb); break;
-        case 16: q10_go<4, 16>(gd, bd, s, w, x, y, n, nb); break;
+        case 7: if (full) q10_go<7, 7>(gd, bd, s, w, x, y, n, nb); else q10_go<4, 7>(gd, bd, s, w, x, y, n, nb); break;
+        case 8: if (full) q10_go<8, 8>(gd, bd, s, w, x, y, n, nb); else q10_go<4, 8>(gd, bd, s, w, x, y, n, nb); break;
+        case 14: if (full) q10_go<14, 14>(gd, bd, s, w, x, y, n, nb); else q10_go<4, 14>(gd, bd, s, w, x, y, n, nb); break;
+        case 16: if (full) q10_go<16, 16>(gd, bd, s, w, x, y, n, nb); else q10_go<4, 16>(gd, bd, s, w, x, y, n, nb); break;
         default: return hipErrorInvalidConfiguration;
     }
     return hipGetLastError();
@@ -1426,11 +1430,11 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
         p.waves = (int)((nb * 4 + 63) / 64);
         if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q6k(n, p.waves);
         if (!q4k_rows_ok(p.rows_per_wg)) return hipErrorInvalidConfiguration;
-        p.unroll = 4;
+        p.unroll = p.unroll >= p.rows_per_wg ? p.rows_per_wg : 4;
         p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
         if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
         if (plan) *plan = p;
-        return launch_q10_ring(p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
+        return launch_q10_ring(p.unroll, p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
     }
     if (qtype == kTypeQ10 && p.cpl == kQ10RingUnit) return hipErrorInvalidValue;   // layout not eligible
     if (qtype == kTypeQ80 && (p.cpl <= 0 || p.cpl == kQ80RingUnit) && q80_ring_ok(w, nb)) {
@@ -1438,11 +1442,11 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
         p.waves = (int)((nb * 2 + 63) / 64);
         if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q6k(n, p.waves);
         if (!q4k_rows_ok(p.rows_per_wg)) return hipErrorInvalidConfiguration;
-        p.unroll = 4;
+        p.unroll = p.unroll >= p.rows_per_wg ? p.rows_per_wg : 4;
         p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
         if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
         if (plan) *plan = p;
-        return launch_q80_ring(p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
+        return launch_q80_ring(p.unroll, p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
     }
     if (qtype == kTypeQ80 && p.cpl == kQ80RingUnit) return hipErrorInvalidValue;   // layout not eligible
     if (p.cpl <= 0) p.cpl = pick_cpl(qtype, nb);
