@@ -264,11 +264,19 @@ bool batched_gemm(int qtype, const uint8_t* w, const float* x, int64_t batch, in
     return !(reinterpret_cast<uintptr_t>(x) & 15) && !(qtype == FRQ_Q4_K ? (wa & 15) : (wa & 1));
 }
 
+// Up to this many rows of x, a Q4_K matrix that the matrix-core GEMV takes
+// runs one GEMV per row rather than the GEMM: each GEMV reads the weights
+// again, but its time per row stays below the GEMM's time at a few rows
+// (3584 x 18944: 11.7 us per row against 45 us for the GEMM at 4 rows).
+constexpr int64_t kMxRowsBeforeGemm = 3;
+
 // y[b * ldy + i] = (W x_b)[i] for b < batch: the GEMM for two or more rows
-// where batched_gemm allows, else one GEMV per row. Scratch as gemv_device.
+// where batched_gemm allows (past kMxRowsBeforeGemm rows for a Q4_K matrix
+// the matrix-core GEMV takes), else one GEMV per row. Scratch as gemv_device.
 int gemv_batched(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int64_t batch,
                  int64_t ldy, hipStream_t s, const frq::FixedScratch* fixed = nullptr) {
-    if (batched_gemm(qtype, w, x, batch, n, k)) {
+    const bool rows_first = batch <= kMxRowsBeforeGemm && frq::gemv_mx_eligible(qtype, w, x, n, k);
+    if (!rows_first && batched_gemm(qtype, w, x, batch, n, k)) {
         if (fixed) {   // as many K-splits as the fixed partial region holds
             FRQ_HIP(frq::launch_gemm_f32(qtype, w, x, y, batch, n, k, ldy, s, fixed->part, fixed->part_bytes));
             return FRQ_OK;

@@ -140,6 +140,23 @@ __device__ __forceinline__ void nibbles8(uint32_t w, float (&f)[8], uint32_t mas
         : "v"(mask_a), "v"(mask_b), "v"(w));
 }
 
+// Four 6-bit Q6_K codes q as the signed bytes 4 (q - 32), converted to float
+// exactly (one sign-extending byte-select convert each): lo holds the low
+// nibbles at bits 2..5 of each byte, hi2 the two high bits at bits 6, 7 with
+// the upper one flipped (so bit 7 is the sign of q - 32). Byte value:
+// 4 lo + 64 (hi ^ 2) read as int8 = 4 (lo + 16 hi - 32).
+__device__ __forceinline__ void q6_quad_signed(uint32_t lo, uint32_t hi2, float (&f)[4]) {
+    uint32_t t, q;
+    asm("v_and_b32 %0, %6, %7\n\t"
+        "v_and_or_b32 %1, %8, %9, %0\n\t"
+        "v_cvt_f32_i32_sdwa %2, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f32_i32_sdwa %3, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f32_i32_sdwa %4, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f32_i32_sdwa %5, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3"
+        : "=&v"(t), "=&v"(q), "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3])
+        : "s"(0xC0C0C0C0u), "v"(hi2), "v"(lo), "s"(0x3C3C3C3Cu));
+}
+
 // Byte b of w as float: one v_cvt_f32_ubyte<b>.
 __device__ __forceinline__ float byte_f(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
 

@@ -5,8 +5,9 @@
 // run one fp32 matvec per row of X and dequantize W again for every row. Here
 // W is read once per tile of X rows, and the products run on
 // v_mfma_f32_32x32x16_bf16 without giving up the fp32 contract:
-//   * W enters as its integer codes, which bf16 holds exactly: Q4_K q in
-//     0..15, Q6_K q - 32 in -32..31, Q8_0 q in -128..127;
+//   * W enters as integer codes, which bf16 holds exactly: Q4_K q - c in
+//     -15..15 (c the sub-block's code nearest t / s, below), Q6_K q - 32 in
+//     -32..31, Q8_0 q in -128..127;
 //   * X enters as three bf16 pieces, x = x1 + x2 + x3 with x1 = bf16(x),
 //     x2 = bf16(x - x1), x3 = bf16(x - x1 - x2) (round to nearest; every
 //     subtraction is exact), which carry all 24 bits of an fp32 x whose
@@ -14,10 +15,12 @@
 //   * every product code * piece is exact in fp32, and the matrix cores sum
 //     them in fp32 over one sub-block (Q4_K 32 elements, Q6_K 16, Q8_0 32);
 //   * the sub-block's scale is applied in fp32 per (row, sub-block):
-//     y += d*sc * S - dmin*m * sum(x) (Q4_K), y += d*sc * S (Q6_K),
-//     y += d * S (Q8_0), with sum(x) of the sub-block in fp32.
-// So every row's error is bounded like the matvec kernels':
-//   |y - y_exact| <= c * 2^-24 * sum_j (|s_j q_j| + |t_j|) |x_j|,
+//     y += s * S - (t - s c) * sum(x) (Q4_K, s = d*sc, t = dmin*m),
+//     y += d*sc * S (Q6_K), y += d * S (Q8_0), with sum(x) of the sub-block
+//     in fp32.
+// The codes make every term of S and sum(x) within 3 |w_j x_j| (Q4_K, see
+// CFmt<Q4_K>::codes) or equal to it, so every row's error is bounded like
+// the matvec kernels':  |y - y_exact| <= c * 2^-24 * sum_j |w_j x_j|,
 // c a small multiple of the summation depth (tested at 1e-5 against fp64).
 //
 // Tiling: a workgroup of 4 waves owns a BM x BN tile of Y (WM x WN waves of
@@ -78,23 +81,34 @@ struct CFmt<kTypeQ4K> {
 #pragma unroll
         for (int c = 0; c < CNT / 16; ++c) r.q[c] = *reinterpret_cast<const u32x4*>(bp + 16 + 32 * (j >> 1) + k0 + 16 * c);
     }
+    // Centred codes: w = s q - t = s (q - c) - (t - s c) with c = round(t / s)
+    // clamped to 0 .. 15, so the code q - c (-15 .. 15, exact in bf16) is 0 on
+    // the weight nearest zero and |s (q - c)| + |t - s c| <= 3 |w| for every
+    // q (|t - s c| <= |s| / 2 unless clamped, and then both terms have the
+    // sign of w). The sub-block sum s * S - t' * sum(x) then keeps the bound
+    // sum |w x| even for an outlier x on a weight where s q = t.
     template <int CNT>
     __device__ static void codes(const Raw<CNT>& r, int step, uint32_t* out, float* scl, bool first) {
         const int j = step & 7;
         const uint32_t sh = (j & 1) ? 4u : 0u;
+        uint32_t sc, mn;
+        k4_scale_min(r.h[1], r.h[2], r.h[3], j, sc, mn);
+        const float s = f16_bits_to_f32(r.h[0]) * (float)sc;          // exact
+        const float t = f16_bits_to_f32(r.h[0] >> 16) * (float)mn;    // exact
+        // s = 0 or non-finite: fmaxf drops a NaN, so c lands in 0 .. 15 anyway
+        const float cf = fminf(fmaxf(__builtin_rintf(t * __builtin_amdgcn_rcpf(s)), 0.0f), 15.0f);
+        const int ci = (int)cf;
 #pragma unroll
         for (int c = 0; c < CNT / 16; ++c)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t v = (r.q[c][i] >> sh) & 0x0F0F0F0Fu;
-                out[8 * c + 2 * i] = bf16_pair((float)(v & 15u), (float)((v >> 8) & 15u));
-                out[8 * c + 2 * i + 1] = bf16_pair((float)((v >> 16) & 15u), (float)(v >> 24));
+                out[8 * c + 2 * i] = bf16_pair((float)((int)(v & 15u) - ci), (float)((int)((v >> 8) & 15u) - ci));
+                out[8 * c + 2 * i + 1] = bf16_pair((float)((int)((v >> 16) & 15u) - ci), (float)((int)(v >> 24) - ci));
             }
         if (first) {
-            uint32_t sc, mn;
-            k4_scale_min(r.h[1], r.h[2], r.h[3], j, sc, mn);
-            scl[0] = f16_bits_to_f32(r.h[0]) * (float)sc;
-            scl[1] = f16_bits_to_f32(r.h[0] >> 16) * (float)mn;
+            scl[0] = s;
+            scl[1] = __builtin_fmaf(-s, cf, t);                       // t - s c, one rounding
         }
     }
 };

@@ -21,8 +21,15 @@
 //     enough bytes in flight per wave to cover HBM latency.
 //   * Per-row partials are reduced across the wave with DPP, then across the
 //     workgroup's waves through LDS in a fixed order (deterministic output).
-//   * Scale algebra: sum_i (s*q_i - t) x_i = s * sum_i q_i x_i - t * sum_i x_i;
-//     the per-lane sums of x are computed once with x.
+//   * Every product is w_i x_i with the weight itself: Q4_K / Q5_K form
+//     w = fma(s, q, -t) per weight (fl(fl(d*sc)*q - dmin*m): d*sc*q is exact
+//     in fp32, so this is the dequantized weight's bits), Q6_K and Q8_0 feed
+//     their signed codes (4 (q - 32) and q) and apply the block scale to the
+//     sub-block sum. No sum is formed as s * sum(q x) - t * sum(x): with an
+//     outlier x_j on a weight where s q_j = t that form cancels two terms of
+//     size t |x_j| and loses the bound sum_i |w_i x_i|. Q1_0 sums
+//     d * (2 sum_{bit set} x - sum x): its weights are all +-d, so the terms
+//     of both sums are within 3 |w_i x_i| and the bound holds.
 #include <algorithm>
 #include <cstdint>
 
@@ -31,11 +38,6 @@
 
 namespace frq {
 
-__device__ __forceinline__ uint32_t vxor(uint32_t a, uint32_t mask) {
-    uint32_t r;
-    asm("v_xor_b32 %0, %1, %2" : "=v"(r) : "s"(mask), "v"(a));
-    return r;
-}
 __device__ __forceinline__ float sbf(uint32_t w, int b) { return (float)(int)(int8_t)((w >> (8 * b)) & 0xFFu); }
 
 // Writes the U row partials of one row batch: wave-reduce each, then either
@@ -137,7 +139,6 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
     };
 
     float xl[NE], xh[NE];                                   // x of plane A, plane B
-    float sxl = 0.0f, sxh = 0.0f;
     {
         const float* xb = x + (int64_t)gblk * kQKElems + 64 * g + 16 * hh;
         const float* xa = xb + (own_hi ? 32 : 0);
@@ -150,33 +151,39 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
             xh[i] = c.x; xh[i + 1] = c.y; xh[i + 2] = c.z; xh[i + 3] = c.w;
         }
     }
-    // x first, then the first U rows, then the first use of x: waiting for
-    // x (in-order vmcnt) leaves every row load in flight. The barriers keep
-    // the scheduler from reordering the three phases. Inactive lanes keep
-    // block 0's x; their partial is discarded by a select below.
+    // x first, then the first U rows: the first use of x waits for x only
+    // (in-order vmcnt) and leaves every row load in flight. The barriers keep
+    // the scheduler from reordering the phases. Inactive lanes keep block 0's
+    // x; their partial is discarded by a select below.
     __builtin_amdgcn_sched_barrier(0);
     Q4KRow<CPL> ring[U];
 #pragma unroll
     for (int i = 0; i < U; ++i) load1(ring[i], i);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < NE; ++i) {
-        sxl += xl[i];
-        sxh += xh[i];
-    }
-    // CPL = 1: sum of x over this lane's pair, both lanes' shares
-    const float sxt = sxl + dpp_mov<0xB1>(sxh);             // quad_perm [1,0,3,2]
 
     static_for<0, R>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         Q4KRow<CPL>& t = ring[j % U];
         // everything read from the slot is read before the slot is refilled
         const float d = f16_bits_to_f32(t.hd.x), dm = f16_bits_to_f32(t.hd.x >> 16);
-        uint32_t sc0 = 0, m0 = 0, sc1 = 0, m1 = 0;
-        if constexpr (CPL == 1)
+        // (s, t) of plane A and plane B: w = fma(s, f, -t) per weight (f = q,
+        // or 16 q with s pre-divided by 16)
+        float sa, ta, sb, tb;
+        if constexpr (CPL == 1) {
+            uint32_t sc0, m0;
             pdec(t.hd.y, t.hd.z, t.hd.w, sc0, m0);          // this lane's pair 2g + hh
-        else
+            sa = (d * hfac) * (float)sc0;
+            ta = dm * (float)m0;
+            sb = dpp_mov<0xB1>(sa);                         // plane B is the neighbour's pair
+            tb = dpp_mov<0xB1>(ta);
+        } else {
+            uint32_t sc0, m0, sc1, m1;
             dec(t.hd.y, t.hd.z, t.hd.w, sc0, m0, sc1, m1);
+            sa = d * (float)sc0;
+            ta = dm * (float)m0;
+            sb = (d * 0.0625f) * (float)sc1;
+            tb = dm * (float)m1;
+        }
         float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
@@ -186,30 +193,18 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
                 float f[8];                                       // plane A, plane B
                 nibbles8(qw[wd], f, mask_a, mask_b);
                 const int e = 16 * c + 4 * wd;
-                a0 = __builtin_fmaf(f[0], xl[e + 0], a0);
-                a1 = __builtin_fmaf(f[1], xl[e + 1], a1);
-                b0 = __builtin_fmaf(f[4], xh[e + 0], b0);
-                b1 = __builtin_fmaf(f[5], xh[e + 1], b1);
-                a0 = __builtin_fmaf(f[2], xl[e + 2], a0);
-                a1 = __builtin_fmaf(f[3], xl[e + 3], a1);
-                b0 = __builtin_fmaf(f[6], xh[e + 2], b0);
-                b1 = __builtin_fmaf(f[7], xh[e + 3], b1);
+                a0 = __builtin_fmaf(__builtin_fmaf(sa, f[0], -ta), xl[e + 0], a0);
+                a1 = __builtin_fmaf(__builtin_fmaf(sa, f[1], -ta), xl[e + 1], a1);
+                b0 = __builtin_fmaf(__builtin_fmaf(sb, f[4], -tb), xh[e + 0], b0);
+                b1 = __builtin_fmaf(__builtin_fmaf(sb, f[5], -tb), xh[e + 1], b1);
+                a0 = __builtin_fmaf(__builtin_fmaf(sa, f[2], -ta), xl[e + 2], a0);
+                a1 = __builtin_fmaf(__builtin_fmaf(sa, f[3], -ta), xl[e + 3], a1);
+                b0 = __builtin_fmaf(__builtin_fmaf(sb, f[6], -tb), xh[e + 2], b0);
+                b1 = __builtin_fmaf(__builtin_fmaf(sb, f[7], -tb), xh[e + 3], b1);
             }
         }
         if constexpr (j + U < R) load1(t, j + U);               // refill the slot: row j + U
-        float pu;
-        if constexpr (CPL == 1) {
-            const float so = (d * hfac) * (float)sc0, to = dm * (float)m0;
-            const float dot = (a0 + a1) + dpp_mov<0xB1>(b0 + b1);   // this lane's pair, both halves
-            pu = __builtin_fmaf(-to, sxt, so * dot);
-        } else {
-            const float s0 = d * (float)sc0, t0 = dm * (float)m0;
-            const float s1 = (d * 0.0625f) * (float)sc1, t1 = dm * (float)m1;
-            pu = s0 * (a0 + a1);
-            pu = __builtin_fmaf(-t0, sxl, pu);
-            pu = __builtin_fmaf(s1, b0 + b1, pu);
-            pu = __builtin_fmaf(-t1, sxh, pu);
-        }
+        const float pu = (a0 + a1) + (b0 + b1);
         // results go to LDS (lgkmcnt): a global store would count in vmcnt
         // and force waits on the in-flight row loads.
         const float v = row16_sum(active ? pu : 0.0f);
@@ -289,7 +284,6 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_lds_kernel(const uint8_t* __re
     };
 
     float xl[16], xh[16];
-    float sxl = 0.0f, sxh = 0.0f;
     {
         const float* xb = x + (int64_t)gblk * kQKElems + 64 * g + 16 * hh;
         const float* xa = xb + (own_hi ? 32 : 0);
@@ -305,12 +299,6 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_lds_kernel(const uint8_t* __re
     __builtin_amdgcn_sched_barrier(0);
     static_for<0, D>([&](auto ic) { issue(ic); });
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        sxl += xl[i];
-        sxh += xh[i];
-    }
-    const float sxt = sxl + dpp_mov<0xB1>(sxh);
 
     static_for<0, R>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
@@ -323,6 +311,9 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_lds_kernel(const uint8_t* __re
         const float d = f16_bits_to_f32(hd.x), dm = f16_bits_to_f32(hd.x >> 16);
         uint32_t sc0, m0;
         pdec(hd.y, hd.z, hd.w, sc0, m0);
+        // per-weight w = fma(s, f, -t), plane B with the neighbour's pair
+        const float sa = (d * hfac) * (float)sc0, ta = dm * (float)m0;
+        const float sb = dpp_mov<0xB1>(sa), tb = dpp_mov<0xB1>(ta);
         float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
         const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
@@ -330,21 +321,19 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_lds_kernel(const uint8_t* __re
             float f[8];
             nibbles8(qw[wd], f, mask_a, mask_b);
             const int e = 4 * wd;
-            a0 = __builtin_fmaf(f[0], xl[e + 0], a0);
-            a1 = __builtin_fmaf(f[1], xl[e + 1], a1);
-            b0 = __builtin_fmaf(f[4], xh[e + 0], b0);
-            b1 = __builtin_fmaf(f[5], xh[e + 1], b1);
-            a0 = __builtin_fmaf(f[2], xl[e + 2], a0);
-            a1 = __builtin_fmaf(f[3], xl[e + 3], a1);
-            b0 = __builtin_fmaf(f[6], xh[e + 2], b0);
-            b1 = __builtin_fmaf(f[7], xh[e + 3], b1);
+            a0 = __builtin_fmaf(__builtin_fmaf(sa, f[0], -ta), xl[e + 0], a0);
+            a1 = __builtin_fmaf(__builtin_fmaf(sa, f[1], -ta), xl[e + 1], a1);
+            b0 = __builtin_fmaf(__builtin_fmaf(sb, f[4], -tb), xh[e + 0], b0);
+            b1 = __builtin_fmaf(__builtin_fmaf(sb, f[5], -tb), xh[e + 1], b1);
+            a0 = __builtin_fmaf(__builtin_fmaf(sa, f[2], -ta), xl[e + 2], a0);
+            a1 = __builtin_fmaf(__builtin_fmaf(sa, f[3], -ta), xl[e + 3], a1);
+            b0 = __builtin_fmaf(__builtin_fmaf(sb, f[6], -tb), xh[e + 2], b0);
+            b1 = __builtin_fmaf(__builtin_fmaf(sb, f[7], -tb), xh[e + 3], b1);
         }
         // the slot has been read into registers: refill it with row j + D
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (j + D < R) issue(Int<j + D>{});
-        const float so = (d * hfac) * (float)sc0, to = dm * (float)m0;
-        const float dot = (a0 + a1) + dpp_mov<0xB1>(b0 + b1);
-        const float pu = __builtin_fmaf(-to, sxt, so * dot);
+        const float pu = (a0 + a1) + (b0 + b1);
         const float v = row16_sum(active ? pu : 0.0f);
         if ((lane & 15) == 15) red[j * 4 * nwaves + 4 * wave + (lane >> 4)] = v;
     });
@@ -379,7 +368,6 @@ __global__ void __launch_bounds__(512) gemv_q5_k_kernel(const uint8_t* __restric
     const uint32_t rot_lo = (uint32_t)(2 * g + 28) & 31u, rot_hi = (uint32_t)(2 * g + 29) & 31u;
 
     float xl[NE], xh[NE];
-    float sxl = 0.0f, sxh = 0.0f;
     if (active) {
         const float* xb = x + (int64_t)blk * kQKElems + 64 * g;
 #pragma unroll
@@ -393,8 +381,6 @@ __global__ void __launch_bounds__(512) gemv_q5_k_kernel(const uint8_t* __restric
 #pragma unroll
         for (int i = 0; i < NE; ++i) { xl[i] = 0.0f; xh[i] = 0.0f; }
     }
-#pragma unroll
-    for (int i = 0; i < NE; ++i) { sxl += xl[i]; sxh += xh[i]; }
 
     const int64_t row0 = (int64_t)blockIdx.x * rows_per_wg;
     const int64_t row_end = row0 + rows_per_wg < n ? row0 + rows_per_wg : n;
@@ -423,6 +409,9 @@ __global__ void __launch_bounds__(512) gemv_q5_k_kernel(const uint8_t* __restric
             k4_scale_min(hd[u].y, hd[u].z, hd[u].w, 2 * g, sc0, m0);
             k4_scale_min(hd[u].y, hd[u].z, hd[u].w, 2 * g + 1, sc1, m1);
             const float d = f16_bits_to_f32(hd[u].x), dm = f16_bits_to_f32(hd[u].x >> 16);
+            // per weight: w = fma(s, q, -t), q the 5-bit code
+            const float s0 = d * (float)sc0, t0 = dm * (float)m0;
+            const float s1 = d * (float)sc1, t1 = dm * (float)m1;
             float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
@@ -439,22 +428,17 @@ __global__ void __launch_bounds__(512) gemv_q5_k_kernel(const uint8_t* __restric
                     const uint32_t lo = vand_or(sw[wd], 0x0F0F0F0Fu, vand(hl, 0x10101010u));
                     const uint32_t hi = vand_or(sw[wd] >> 4, 0x0F0F0F0Fu, vand(hh, 0x10101010u));
                     const int e = 16 * c + 4 * wd;
-                    a0 = __builtin_fmaf(byte_f(lo, 0), xl[e + 0], a0);
-                    a1 = __builtin_fmaf(byte_f(lo, 1), xl[e + 1], a1);
-                    a0 = __builtin_fmaf(byte_f(lo, 2), xl[e + 2], a0);
-                    a1 = __builtin_fmaf(byte_f(lo, 3), xl[e + 3], a1);
-                    b0 = __builtin_fmaf(byte_f(hi, 0), xh[e + 0], b0);
-                    b1 = __builtin_fmaf(byte_f(hi, 1), xh[e + 1], b1);
-                    b0 = __builtin_fmaf(byte_f(hi, 2), xh[e + 2], b0);
-                    b1 = __builtin_fmaf(byte_f(hi, 3), xh[e + 3], b1);
+                    a0 = __builtin_fmaf(__builtin_fmaf(s0, byte_f(lo, 0), -t0), xl[e + 0], a0);
+                    a1 = __builtin_fmaf(__builtin_fmaf(s0, byte_f(lo, 1), -t0), xl[e + 1], a1);
+                    a0 = __builtin_fmaf(__builtin_fmaf(s0, byte_f(lo, 2), -t0), xl[e + 2], a0);
+                    a1 = __builtin_fmaf(__builtin_fmaf(s0, byte_f(lo, 3), -t0), xl[e + 3], a1);
+                    b0 = __builtin_fmaf(__builtin_fmaf(s1, byte_f(hi, 0), -t1), xh[e + 0], b0);
+                    b1 = __builtin_fmaf(__builtin_fmaf(s1, byte_f(hi, 1), -t1), xh[e + 1], b1);
+                    b0 = __builtin_fmaf(__builtin_fmaf(s1, byte_f(hi, 2), -t1), xh[e + 2], b0);
+                    b1 = __builtin_fmaf(__builtin_fmaf(s1, byte_f(hi, 3), -t1), xh[e + 3], b1);
                 }
             }
-            const float s0 = d * (float)sc0, t0 = dm * (float)m0;
-            const float s1 = d * (float)sc1, t1 = dm * (float)m1;
-            float pu = s0 * (a0 + a1);
-            pu = __builtin_fmaf(-t0, sxl, pu);
-            pu = __builtin_fmaf(s1, b0 + b1, pu);
-            part[u] = __builtin_fmaf(-t1, sxh, pu);
+            part[u] = (a0 + a1) + (b0 + b1);
         }
         row_partials_out<U>(part, rb, row0, row_end, y, red, nwaves, wave, lane);
     }
@@ -482,18 +466,14 @@ __global__ void __launch_bounds__(512) gemv_q6_k_kernel(const uint8_t* __restric
     const bool active = blk < nb;
 
     float xv[4][LQ];
-    float xs[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        xs[k] = 0.0f;
 #pragma unroll
         for (int i = 0; i < LQ; i += 4) {
             float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
             if (active) a = *reinterpret_cast<const float4*>(x + (int64_t)blk * kQKElems + 128 * h + 32 * k + l0 + i);
             xv[k][i] = a.x; xv[k][i + 1] = a.y; xv[k][i + 2] = a.z; xv[k][i + 3] = a.w;
         }
-#pragma unroll
-        for (int i = 0; i < LQ; ++i) xs[k] += xv[k][i];
     }
 
     const int64_t row0 = (int64_t)blockIdx.x * rows_per_wg;
@@ -526,7 +506,8 @@ __global__ void __launch_bounds__(512) gemv_q6_k_kernel(const uint8_t* __restric
         float part[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const float d = f16_bits_to_f32(dd[u]);
+            // codes enter as 4 (q - 32) (exact signed bytes): the scale carries 1/4
+            const float d = f16_bits_to_f32(dd[u]) * 0.25f;
             const float sk[4] = {sbf(sca[u], sidx), sbf(sca[u], sidx + 2), sbf(scb[u], sidx), sbf(scb[u], sidx + 2)};
             float pu = 0.0f;
 #pragma unroll
@@ -535,18 +516,16 @@ __global__ void __launch_bounds__(512) gemv_q6_k_kernel(const uint8_t* __restric
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
                     const uint32_t src = (k & 1) ? ql1[u][c] : ql0[u][c];
-                    // bits 2k, 2k+1 of each qh byte -> bits 4, 5
-                    const uint32_t hsh = (k == 0) ? (qh[u][c] << 4) : (k == 1) ? (qh[u][c] << 2)
-                                       : (k == 2) ? qh[u][c] : (qh[u][c] >> 2);
-                    const uint32_t q = vand_or((k >= 2) ? (src >> 4) : src, 0x0F0F0F0Fu, vand(hsh, 0x30303030u));
-                    a0 = __builtin_fmaf(byte_f(q, 0), xv[k][4 * c + 0], a0);
-                    a1 = __builtin_fmaf(byte_f(q, 1), xv[k][4 * c + 1], a1);
-                    a0 = __builtin_fmaf(byte_f(q, 2), xv[k][4 * c + 2], a0);
-                    a1 = __builtin_fmaf(byte_f(q, 3), xv[k][4 * c + 3], a1);
+                    const uint32_t qhx = qh[u][c] ^ 0xAAAAAAAAu;    // upper bit of each 2-bit field flipped
+                    // bits 2k, 2k+1 of each qh byte -> bits 6, 7; the nibble -> bits 2..5
+                    const uint32_t hsh = (k == 0) ? (qhx << 6) : (k == 1) ? (qhx << 4) : (k == 2) ? (qhx << 2) : qhx;
+                    const uint32_t q = vand_or((k >= 2) ? (src >> 2) : (src << 2), 0x3C3C3C3Cu, vand(hsh, 0xC0C0C0C0u));
+                    a0 = __builtin_fmaf(sbf(q, 0), xv[k][4 * c + 0], a0);     // 4 (q - 32), signed
+                    a1 = __builtin_fmaf(sbf(q, 1), xv[k][4 * c + 1], a1);
+                    a0 = __builtin_fmaf(sbf(q, 2), xv[k][4 * c + 2], a0);
+                    a1 = __builtin_fmaf(sbf(q, 3), xv[k][4 * c + 3], a1);
                 }
-                // sum_l (q - 32) x = sum_l q x - 32 sum_l x
-                const float dotk = __builtin_fmaf(-32.0f, xs[k], a0 + a1);
-                pu = __builtin_fmaf(d * sk[k], dotk, pu);
+                pu = __builtin_fmaf(d * sk[k], a0 + a1, pu);
             }
             part[u] = pu;
         }
@@ -577,20 +556,6 @@ __device__ __forceinline__ void load_win3(const uint8_t* p, uint32_t (&wv)[3]) {
     wv[0] = q[0];
     wv[1] = q[1];
     wv[2] = q[2];
-}
-
-// Four 6-bit quants of one dword as floats: (src & 0x0F0F0F0F) | (hsh & 0x30303030),
-// one v_cvt_f32_ubyteN each, grouped so the FMAs that follow do not stall.
-__device__ __forceinline__ void q6_quad(uint32_t src, uint32_t hsh, float (&f)[4]) {
-    uint32_t t, q;
-    asm("v_and_b32 %0, %6, %7\n\t"
-        "v_and_or_b32 %1, %8, %9, %0\n\t"
-        "v_cvt_f32_ubyte0 %2, %1\n\t"
-        "v_cvt_f32_ubyte1 %3, %1\n\t"
-        "v_cvt_f32_ubyte2 %4, %1\n\t"
-        "v_cvt_f32_ubyte3 %5, %1"
-        : "=&v"(t), "=&v"(q), "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3])
-        : "s"(0x30303030u), "v"(hsh), "v"(src), "s"(0x0F0F0F0Fu));
 }
 
 template <int U, int R>
@@ -625,7 +590,6 @@ __device__ __forceinline__ void gemv_q6_k_ring_body(const uint8_t* __restrict__ 
     };
 
     float xv[4][8];
-    float xs[4];
     {
         const float* xb = x + (int64_t)blk * kQKElems + 128 * h + l0;
 #pragma unroll
@@ -641,12 +605,6 @@ __device__ __forceinline__ void gemv_q6_k_ring_body(const uint8_t* __restrict__ 
 #pragma unroll
     for (int i = 0; i < U; ++i) load1(ring[i], i);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        xs[k] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) xs[k] += xv[k][i];
-    }
 
     static_for<0, R>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
@@ -656,11 +614,12 @@ __device__ __forceinline__ void gemv_q6_k_ring_body(const uint8_t* __restrict__ 
         for (int c = 0; c < 2; ++c) {
             ql0[c] = __builtin_amdgcn_alignbit(t.ql0[c + 1], t.ql0[c], sh);
             ql1[c] = __builtin_amdgcn_alignbit(t.ql1[c + 1], t.ql1[c], sh);
-            qh[c] = __builtin_amdgcn_alignbit(t.qh[c + 1], t.qh[c], sh);
+            // upper bit of each 2-bit field flipped: the sign of q - 32 (q6_quad_signed)
+            qh[c] = __builtin_amdgcn_alignbit(t.qh[c + 1], t.qh[c], sh) ^ 0xAAAAAAAAu;
         }
         const uint32_t sc0 = __builtin_amdgcn_alignbit(t.sc[1], t.sc[0], sh);   // scale bytes 8h .. 8h+3
         const uint32_t sc1 = __builtin_amdgcn_alignbit(t.sc[2], t.sc[1], sh);   // 8h+4 .. 8h+7
-        const float d = f16_bits_to_f32(t.d);
+        const float d = f16_bits_to_f32(t.d) * 0.25f;     // codes enter as 4 (q - 32)
         // int8 scales sc[8h + s + 2k]: bytes s, s+2 of sc0 (k = 0, 1) and of sc1 (k = 2, 3)
         const float sk[4] = {(float)(int8_t)(sc0 >> (8 * s)), (float)(int8_t)(sc0 >> (8 * s + 16)),
                              (float)(int8_t)(sc1 >> (8 * s)), (float)(int8_t)(sc1 >> (8 * s + 16))};
@@ -671,18 +630,16 @@ __device__ __forceinline__ void gemv_q6_k_ring_body(const uint8_t* __restrict__ 
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 const uint32_t src = (k & 1) ? ql1[c] : ql0[c];
-                // bits 2k, 2k+1 of each qh byte -> bits 4, 5
-                const uint32_t hsh = (k == 0) ? (qh[c] << 4) : (k == 1) ? (qh[c] << 2) : (k == 2) ? qh[c] : (qh[c] >> 2);
+                // bits 2k, 2k+1 of each qh byte -> bits 6, 7; the nibble -> bits 2..5
+                const uint32_t hsh = (k == 0) ? (qh[c] << 6) : (k == 1) ? (qh[c] << 4) : (k == 2) ? (qh[c] << 2) : qh[c];
                 float f[4];
-                q6_quad((k >= 2) ? (src >> 4) : src, hsh, f);
+                q6_quad_signed((k >= 2) ? (src >> 2) : (src << 2), hsh, f);
                 a0 = __builtin_fmaf(f[0], xv[k][4 * c + 0], a0);
                 a1 = __builtin_fmaf(f[1], xv[k][4 * c + 1], a1);
                 a0 = __builtin_fmaf(f[2], xv[k][4 * c + 2], a0);
                 a1 = __builtin_fmaf(f[3], xv[k][4 * c + 3], a1);
             }
-            // sum_l (q - 32) x = sum_l q x - 32 sum_l x
-            const float dotk = __builtin_fmaf(-32.0f, xs[k], a0 + a1);
-            pu = __builtin_fmaf(d * sk[k], dotk, pu);
+            pu = __builtin_fmaf(d * sk[k], a0 + a1, pu);
         }
         if constexpr (j + U < R) load1(t, j + U);
         __builtin_amdgcn_sched_barrier(0);                  // keep the rows in ring order
@@ -742,15 +699,12 @@ __global__ void __launch_bounds__(512) gemv_q8_0_kernel(const uint8_t* __restric
     const bool active = blk < nb;
 
     float xv[NE];
-    float sx = 0.0f;
 #pragma unroll
     for (int i = 0; i < NE; i += 4) {
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
         if (active) a = *reinterpret_cast<const float4*>(x + (int64_t)blk * kQ80Elems + o + i);
         xv[i] = a.x; xv[i + 1] = a.y; xv[i + 2] = a.z; xv[i + 3] = a.w;
     }
-#pragma unroll
-    for (int i = 0; i < NE; ++i) sx += xv[i];
 
     const int64_t row0 = (int64_t)blockIdx.x * rows_per_wg;
     const int64_t row_end = row0 + rows_per_wg < n ? row0 + rows_per_wg : n;
@@ -775,18 +729,16 @@ __global__ void __launch_bounds__(512) gemv_q8_0_kernel(const uint8_t* __restric
         float part[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            // int8 q = (q ^ 0x80) - 128 with q ^ 0x80 read as an unsigned byte:
-            // sum q x = sum (q ^ 0x80) x - 128 sum x
+            // int8 q converted signed (no offset to take back out of the sum)
             float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
             for (int c = 0; c < NE / 4; ++c) {
-                const uint32_t v = vxor(qv[u][c], 0x80808080u);
-                a0 = __builtin_fmaf(byte_f(v, 0), xv[4 * c + 0], a0);
-                a1 = __builtin_fmaf(byte_f(v, 1), xv[4 * c + 1], a1);
-                a0 = __builtin_fmaf(byte_f(v, 2), xv[4 * c + 2], a0);
-                a1 = __builtin_fmaf(byte_f(v, 3), xv[4 * c + 3], a1);
+                a0 = __builtin_fmaf(sbf(qv[u][c], 0), xv[4 * c + 0], a0);
+                a1 = __builtin_fmaf(sbf(qv[u][c], 1), xv[4 * c + 1], a1);
+                a0 = __builtin_fmaf(sbf(qv[u][c], 2), xv[4 * c + 2], a0);
+                a1 = __builtin_fmaf(sbf(qv[u][c], 3), xv[4 * c + 3], a1);
             }
-            part[u] = f16_bits_to_f32(dd[u]) * __builtin_fmaf(-128.0f, sx, a0 + a1);
+            part[u] = f16_bits_to_f32(dd[u]) * (a0 + a1);
         }
         row_partials_out<U>(part, rb, row0, row_end, y, red, nwaves, wave, lane);
     }

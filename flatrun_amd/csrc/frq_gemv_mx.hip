@@ -11,10 +11,13 @@
 //     x * 2^(30-e) = m1 + m2 * 2^-30 + r,   m1 = trunc(x 2^(30-e)),
 //     m2 = trunc(frac * 2^30), |m1|, |m2| < 2^30,
 // and m1, m2 each as four balanced base-256 digits (int8). The matrix cores
-// form sum(q * digit) exactly in int32 for all eight digits; the epilogue
-// recombines each level's four sums (two exact 24-bit halves, one fp32
-// rounding), scales by 2^(e-30) / 2^(e-60) (exact) and d*sc_s, and subtracts
-// dmin*m_s * sum(x) (sum(x) in fp32, fixed order).
+// form sum(q * digit) exactly in int32 for all eight digits, and sum(digit)
+// the same way (the digits against an all-ones B); the epilogue recombines
+// each level's four sums exactly in fp64 and forms
+//     T = d*sc_s * sum(q m) - dmin*m_s * sum(m)
+// in fp64 (d*sc_s and dmin*m_s are exact fp32 values, the sums exact
+// integers below 2^39), scales it by 2^(e-30) / 2^(e-60) and adds it to the
+// lane's fp64 sum, which is rounded to fp32 once.
 //
 // Exactness. The split is exact (r = 0) for every x whose lowest set bit is
 // at or above 2^(e-60), which holds for every element within 2^36 of its
@@ -24,9 +27,11 @@
 // (or any inf / NaN) is computed per weight instead, w = fl(fl(d*sc)*q) -
 // fl(dmin*m) then fma(w, x, acc) as in q4_k.h:153-185, so every finite x
 // keeps the fp32 accumulation bound: for each row,
-//     |y - y_exact| <= c * 2^-24 * sum_j (d*sc_j*q_j + dmin*m_j) |x_j|
-// with c a small multiple of the per-row summation depth, and the
-// per-weight blocks are bounded by the same sum over |w_j x_j|.
+//     |y - y_exact| <= c * 2^-24 * sum_j |w_j x_j|
+// with c a small multiple of the per-row summation depth (fp32 sums of the
+// lanes' rounded values). T is formed before any rounding, so the bound
+// holds when d*sc_j*q_j and dmin*m_j cancel (a weight at or near zero)
+// under a large x_j.
 //
 // Work mapping. A workgroup owns TR <= 16 RT output rows, as RT tiles of
 // TT = ceil(TR / RT) <= 16 rows (the MFMA's 16 columns), and a range of KS
@@ -70,7 +75,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMxMaxL = 4;          // blocks per wave
 constexpr int kMxMaxWaves = 16;
 constexpr int kTabBlock = 2048;     // digit bytes per block: 4 MFMAs x 4 k-groups x 8 digits x 16
-constexpr int kSubTab = 16;         // floats per block: 2 halves x 4 sub-blocks x (exponent, sum x)
+constexpr int kSubTab = 8;          // exponents per block: 2 halves x 4 sub-blocks
 
 __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
     return __builtin_amdgcn_perm(s0, s1, sel);
@@ -108,13 +113,11 @@ __device__ __forceinline__ int cvt_i32_sat(float v) {
 
 // x[4t .. 4t+3] of one 256-element block (lane t of a wave): d[0..3] the
 // digits of m1, d[4..7] those of m2; eo = e - 30 for the lane's 32-element
-// sub-block (max |x| < 2^e); s32 = sum of x over the sub-block, the same
-// fp32 bits in its eight lanes; exact = every one of the lane's four values
-// is m1 + m2 2^-30 exactly (scaled by 2^(30-e)) and e <= 30.
+// sub-block (max |x| < 2^e); exact = every one of the lane's four values is
+// m1 + m2 2^-30 exactly (scaled by 2^(30-e)) and e <= 30.
 struct XSplit {
     uint32_t d[8];
     int eo;
-    float s32;
     bool exact;
 };
 __device__ __forceinline__ XSplit x_split(float4 v) {
@@ -126,10 +129,6 @@ __device__ __forceinline__ XSplit x_split(float4 v) {
     mx = max(mx, dpp_u<0xB1>(mx));        // quad_perm [1,0,3,2]
     mx = max(mx, dpp_u<0x4E>(mx));        // quad_perm [2,3,0,1]
     mx = max(mx, dpp_u<0x141>(mx));       // row_half_mirror: max over the 8 lanes
-    float sx = (v.x + v.y) + (v.z + v.w);
-    sx += dpp_mov<0xB1>(sx);
-    sx += dpp_mov<0x4E>(sx);
-    r.s32 = sx + dpp_mov<0x141>(sx);      // 8 lanes = 32 elements
     const int e = __builtin_amdgcn_frexp_expf(__uint_as_float(mx));   // max |x| < 2^e (0 for 0, inf, NaN)
     const int sh = 30 - e;
     const float a[4] = {v.x, v.y, v.z, v.w};
@@ -151,10 +150,22 @@ __device__ __forceinline__ XSplit x_split(float4 v) {
 }
 
 // sum(q m) from four int32 digit sums: (S3 * 256 + S2) * 65536 + (S1 * 256 + S0).
-// 32 elements, q <= 15, |digit| <= 128: |S_i| <= 61440, both halves exact in
-// fp32; one rounding.
-__device__ __forceinline__ float digit_sum(i32x4 s) {
-    return __builtin_fmaf((float)((s[3] << 8) + s[2]), 65536.0f, (float)((s[1] << 8) + s[0]));
+// 32 elements, q <= 15, |digit| <= 128: |S_i| <= 61440, both halves exact;
+// the result (|.| < 2^39) exact in fp64.
+__device__ __forceinline__ double digit_sum(i32x4 s) {
+    return __builtin_fma((double)((s[3] << 8) + s[2]), 65536.0, (double)((s[1] << 8) + s[0]));
+}
+
+// One sub-block and level: T = d*sc * sum(q m) - dmin*m * sum(m) in fp64,
+// added to the lane's fp64 sum scaled by the level's 2^eo. d*sc and dmin*m
+// are exact (an fp16 times a 6-bit integer), the two sums exact integers,
+// so T carries every bit that matters and the lane's sum rounds to fp32 once
+// at the end: the error is 2^-24 of the lane's own sum_j (d*sc*q_j - dmin*m) x_j
+// (up to 2^-52 of its terms), however close d*sc*q_j comes to dmin*m.
+__device__ __forceinline__ double sub_block_add(double acc, double d, double dm, uint32_t sc, uint32_t mn, double dq,
+                                                double dx, double pw) {
+    const double s = d * (double)sc, t = dm * (double)mn;
+    return __builtin_fma(__builtin_fma(s, dq, -(t * dx)), pw, acc);
 }
 
 // The per-weight form of one lane's share of a block (used when the split of
@@ -199,7 +210,7 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
     constexpr int kTabAll = kMxMaxWaves * kWaveTab;
     constexpr int kZero = LMAX * kTabBlock;
     __shared__ __attribute__((aligned(16))) uint8_t lds[kTabAll + kZero];
-    __shared__ __attribute__((aligned(16))) float tab[kMxMaxWaves * LMAX * kSubTab];
+    __shared__ __attribute__((aligned(16))) int etab[kMxMaxWaves * LMAX * kSubTab];
     __shared__ float red[RT * kMxMaxWaves * 64];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
@@ -266,28 +277,25 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
     // half h = (t / 4) % 2, bytes 4 (t % 4) .. +3 of the 16-element group.
     // MFMA m = 2 (s / 4) + s % 2 (load s / 4, low or high nibbles) reads the
     // group in k-group kk = 2 ((s / 2) % 2) + h; table row (m, kk, digit)
-    // holds 16 bytes. The (exponent, sum) table is ordered [p][exp x4, sum x4]
-    // with p = (s / 2) % 2 and position (s % 2) + 2 (s / 4) inside.
+    // holds 16 bytes. The exponent table is ordered [p][position], with
+    // p = (s / 2) % 2 and position (s % 2) + 2 (s / 4).
     uint32_t inexact = 0;                                // bit j: block j of this wave is not exact
     {
         const int s = lane >> 3, h = (lane >> 2) & 1;
         const int m = 2 * (s >> 2) + (s & 1), kk = 2 * ((s >> 1) & 1) + h;
         uint8_t* wl = lds + wave * kWaveTab + (m * 4 + kk) * 128 + 4 * (lane & 3);
-        float* wt = tab + wave * LMAX * kSubTab + 8 * ((s >> 1) & 1) + (s & 1) + 2 * (s >> 2);
+        const int pos = (s & 1) + 2 * (s >> 2), pp = (s >> 1) & 1;
+        int* we = etab + wave * LMAX * kSubTab + 4 * pp + pos;
 #pragma unroll
         for (int j = 0; j < LMAX; ++j) {
             const XSplit dg = x_split(xv[j]);
             uint8_t* p = wl + j * kTabBlock;
 #pragma unroll
             for (int dd = 0; dd < 8; ++dd) *reinterpret_cast<uint32_t*>(p + 16 * dd) = dg.d[dd];
-            if ((lane & 7) == 0) {
-                wt[j * kSubTab] = __int_as_float(dg.eo);
-                wt[j * kSubTab + 4] = dg.s32;
-            }
+            if ((lane & 7) == 0) we[j * kSubTab] = dg.eo;
             if (__builtin_amdgcn_ballot_w64(!dg.exact) != 0) inexact |= 1u << j;
         }
     }
-
     if constexpr (HB) {   // block j's header from lane group j to every lane of the row
 #pragma unroll
         for (int t = 0; t < RT; ++t)
@@ -309,73 +317,70 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
     const uint8_t* abase = ((ar >> 3) == (akk >> 1)) ? lds + wave * kWaveTab + (akk * 8 + (ar & 7)) * 16
                                                      : lds + kTabAll;
     const int p = g >> 1, lev = g & 1;
-    const float* tb = tab + wave * LMAX * kSubTab + 8 * p;
+    const int* eb = etab + wave * LMAX * kSubTab + 4 * p;
+    const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
     const uint32_t s16 = 16u * (uint32_t)p;
-    float acc[RT];
+    double acc[RT];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) acc[t] = 0.0f;
+    for (int t = 0; t < RT; ++t) acc[t] = 0.0;
 #pragma unroll
     for (int j = 0; j < LMAX; ++j) {
         if (j >= lw) continue;                           // wave-uniform
         if (inexact & (1u << j)) {                       // wave-uniform: per-weight fp32 for this block
             const float* xb = x + (int64_t)(kb0 + b0 + j) * kQKElems;
 #pragma unroll
-            for (int t = 0; t < RT; ++t) acc[t] += block_per_weight(hd[t][j], q0[t][j], q1[t][j], xb, g);
+            for (int t = 0; t < RT; ++t) acc[t] += (double)block_per_weight(hd[t][j], q0[t][j], q1[t][j], xb, g);
             continue;
         }
         const uint8_t* ab = abase + j * kTabBlock;
-        const i32x4 A0 = *reinterpret_cast<const i32x4*>(ab + 0);      // MFMA 0: load 0, low nibbles
-        const i32x4 A1 = *reinterpret_cast<const i32x4*>(ab + 512);    // MFMA 1: load 0, high nibbles
-        const i32x4 A2 = *reinterpret_cast<const i32x4*>(ab + 1024);   // MFMA 2: load 1, low nibbles
-        const i32x4 A3 = *reinterpret_cast<const i32x4*>(ab + 1536);   // MFMA 3: load 1, high nibbles
-        const float4 te = *reinterpret_cast<const float4*>(tb + j * kSubTab);       // exponents - 30
-        const float4 ts = *reinterpret_cast<const float4*>(tb + j * kSubTab + 4);   // sums of x
-        const float sxa = lev ? ts.y : ts.x, sxb = lev ? ts.w : ts.z;
+        const int4 te = *reinterpret_cast<const int4*>(eb + j * kSubTab);          // exponents - 30
+        const int el = lev ? -30 : 0;                                              // level 2 carries 2^-30
+        double dt[RT], dmt[RT];
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            const uint4 a = q0[t][j], b = q1[t][j];
-            const i32x4 lo0 = {(int)(a.x & 0x0F0F0F0Fu), (int)(a.y & 0x0F0F0F0Fu), (int)(a.z & 0x0F0F0F0Fu),
-                               (int)(a.w & 0x0F0F0F0Fu)};
-            const i32x4 hi0 = {(int)((a.x >> 4) & 0x0F0F0F0Fu), (int)((a.y >> 4) & 0x0F0F0F0Fu),
-                               (int)((a.z >> 4) & 0x0F0F0F0Fu), (int)((a.w >> 4) & 0x0F0F0F0Fu)};
-            const i32x4 lo1 = {(int)(b.x & 0x0F0F0F0Fu), (int)(b.y & 0x0F0F0F0Fu), (int)(b.z & 0x0F0F0F0Fu),
-                               (int)(b.w & 0x0F0F0F0Fu)};
-            const i32x4 hi1 = {(int)((b.x >> 4) & 0x0F0F0F0Fu), (int)((b.y >> 4) & 0x0F0F0F0Fu),
-                               (int)((b.z >> 4) & 0x0F0F0F0Fu), (int)((b.w >> 4) & 0x0F0F0F0Fu)};
-            const i32x4 z = {0, 0, 0, 0};
-            const i32x4 c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, lo0, z, 0, 0, 0);
-            const i32x4 c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, hi0, z, 0, 0, 0);
-            const i32x4 c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, lo1, z, 0, 0, 0);
-            const i32x4 c3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, hi1, z, 0, 0, 0);
-
-            // sub-blocks [2p, 2p+1, 4+2p, 5+2p] (get_scale_min_k4, gguf.py:135-163):
-            // with Y, Z, W = bytes 2p, 2p+1 of scales[0..3], [4..7], [8..11],
-            // sc_j = Y_j & 63 and m_j = Z_j & 63 for the first two, and
-            // sc = (W_i & 15) | (Y_i >> 6) << 4, m = (W_i >> 4) | (Z_i >> 6) << 4
-            // for the last two (i = 0, 1)
-            const uint4 hdj = hd[t][j];
-            const float d = f16_bits_to_f32(hdj.x), dm = f16_bits_to_f32(hdj.x >> 16);
-            const float dl = __builtin_ldexpf(d, lev ? -30 : 0);      // level 2 carries 2^-30
-            const uint32_t sc0 = __builtin_amdgcn_ubfe(hdj.y, s16, 6);
-            const uint32_t sc1 = __builtin_amdgcn_ubfe(hdj.y, s16 + 8, 6);
-            const uint32_t sc2 = __builtin_amdgcn_ubfe(hdj.w, s16, 4) | (__builtin_amdgcn_ubfe(hdj.y, s16 + 6, 2) << 4);
-            const uint32_t sc3 =
-                __builtin_amdgcn_ubfe(hdj.w, s16 + 8, 4) | (__builtin_amdgcn_ubfe(hdj.y, s16 + 14, 2) << 4);
-            const uint32_t ml = 8u * (uint32_t)lev;           // this lane's two min terms: positions lev, 2 + lev
-            const uint32_t mna = __builtin_amdgcn_ubfe(hdj.z, s16 + ml, 6);
-            const uint32_t mnb =
-                __builtin_amdgcn_ubfe(hdj.w, s16 + ml + 4, 4) | (__builtin_amdgcn_ubfe(hdj.z, s16 + ml + 6, 2) << 4);
-            float part = __builtin_ldexpf(digit_sum(c0), __float_as_int(te.x)) * (dl * (float)sc0);
-            part = __builtin_fmaf(__builtin_ldexpf(digit_sum(c1), __float_as_int(te.y)), dl * (float)sc1, part);
-            part = __builtin_fmaf(__builtin_ldexpf(digit_sum(c2), __float_as_int(te.z)), dl * (float)sc2, part);
-            part = __builtin_fmaf(__builtin_ldexpf(digit_sum(c3), __float_as_int(te.w)), dl * (float)sc3, part);
-            part = __builtin_fmaf(-(dm * (float)mna), sxa, part);
-            part = __builtin_fmaf(-(dm * (float)mnb), sxb, part);
-            acc[t] += part;
+            dt[t] = (double)f16_bits_to_f32(hd[t][j].x);
+            dmt[t] = (double)f16_bits_to_f32(hd[t][j].x >> 16);
         }
+        // MFMA k (0..3): load k / 2, low (k even) or high nibbles; its A operand
+        // at ab + 512 k. Lane (c, g) gets, for row c, the four digit sums of
+        // level g & 1 of sub-block position k of this lane's group p: sub-blocks
+        // [2p, 2p + 1, 4 + 2p, 5 + 2p] (get_scale_min_k4, gguf.py:135-163: with
+        // Y, Z, W = bytes 2p, 2p + 1 of scales[0..3], [4..7], [8..11], sc = Y & 63,
+        // m = Z & 63 for the first two, sc = (W & 15) | (Y >> 6) << 4,
+        // m = (W >> 4) | (Z >> 6) << 4 for the last two).
+        static_for<0, 4>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            const i32x4 A = *reinterpret_cast<const i32x4*>(ab + 512 * k);
+            // sum(m) of this lane's level for the sub-block, exact: the same A
+            // against all-ones B (independent of the row, so once per block)
+            const i32x4 z = {0, 0, 0, 0};
+            const double dx = digit_sum(__builtin_amdgcn_mfma_i32_16x16x64_i8(A, ones, z, 0, 0, 0));
+            const int eo = (k == 0 ? te.x : k == 1 ? te.y : k == 2 ? te.z : te.w) + el;
+            const double pw = __builtin_ldexp(1.0, eo);
+#pragma unroll
+            for (int t = 0; t < RT; ++t) {
+                const uint4 qv = k < 2 ? q0[t][j] : q1[t][j];
+                const uint32_t sh = (k & 1) ? 4u : 0u;
+                const i32x4 b = {(int)((qv.x >> sh) & 0x0F0F0F0Fu), (int)((qv.y >> sh) & 0x0F0F0F0Fu),
+                                 (int)((qv.z >> sh) & 0x0F0F0F0Fu), (int)((qv.w >> sh) & 0x0F0F0F0Fu)};
+                const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, b, z, 0, 0, 0);
+                const uint4 hdj = hd[t][j];
+                uint32_t sc, mn;
+                if constexpr (k < 2) {
+                    sc = __builtin_amdgcn_ubfe(hdj.y, s16 + 8 * k, 6);
+                    mn = __builtin_amdgcn_ubfe(hdj.z, s16 + 8 * k, 6);
+                } else {
+                    sc = __builtin_amdgcn_ubfe(hdj.w, s16 + 8 * (k - 2), 4) |
+                         (__builtin_amdgcn_ubfe(hdj.y, s16 + 8 * (k - 2) + 6, 2) << 4);
+                    mn = __builtin_amdgcn_ubfe(hdj.w, s16 + 8 * (k - 2) + 4, 4) |
+                         (__builtin_amdgcn_ubfe(hdj.z, s16 + 8 * (k - 2) + 6, 2) << 4);
+                }
+                acc[t] = sub_block_add(acc[t], dt[t], dmt[t], sc, mn, digit_sum(c), dx, pw);
+            }
+        });
     }
 #pragma unroll
-    for (int t = 0; t < RT; ++t) red[(t * kMxMaxWaves + wave) * 64 + lane] = acc[t];
+    for (int t = 0; t < RT; ++t) red[(t * kMxMaxWaves + wave) * 64 + lane] = (float)acc[t];
     __syncthreads();
     if (tid < nrows) {
         const int t = tid / TT, cc = tid - t * TT;
@@ -449,16 +454,18 @@ bool plan_gemv_mx(int64_t n, int64_t k, MxPlan* p) {
         if (p->tiles == 2 && p->rows < 2) p->rows = 2;
     }
     if (p->rows < 1 || p->rows > 16 * p->tiles || (p->tiles == 2 && p->rows < 2)) return false;
-    // one block per wavefront: its headers first, in one load, measured faster
-    // (Q4_K 18944 x 3584 12.4 -> 10.9 us); with more blocks the per-block
-    // header loads are faster (3584 x 18944 11.7 vs 13.6 us)
-    if (p->layout < 0) p->layout = p->blocks == 1 ? 1 : 0;
+    // per-block header loads; the one-load header layout (1) measured slower
+    // with the fp64 epilogue for every shape (18944 x 3584: 12.1 vs 11.9 us,
+    // 3584 x 18944: 14.3 vs 12.6 us)
+    if (p->layout < 0) p->layout = 0;
     if (p->layout != 0 && p->layout != 1) return false;
     p->grid = (n + p->rows - 1) / p->rows * p->ksplit;
     return p->grid <= 0x7FFFFFFF;
 }
 
-size_t gemv_mx_slot_bytes(const MxPlan& p, int64_t n) { return p.ksplit == 2 ? (size_t)n * sizeof(uint64_t) : 0; }
+size_t gemv_mx_slot_bytes(const MxPlan& p, int64_t n) {
+    return p.ksplit == 2 ? (size_t)n * sizeof(uint64_t) : 0;
+}
 
 bool gemv_mx_eligible(int qtype, const uint8_t* w, const float* x, int64_t n, int64_t k) {
     // Q4_K with enough rows per workgroup to amortise the per-workgroup x

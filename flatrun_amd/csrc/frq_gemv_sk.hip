@@ -87,7 +87,6 @@ __global__ void __launch_bounds__(256) gemv_q4_k_sk_kernel(const uint8_t* __rest
     load(A, r0);
 
     float xl[NE], xh[NE];
-    float sxl = 0.0f, sxh = 0.0f;
     {
         const float* xb = x + (int64_t)blk * kQKElems + 64 * g + 16 * hh;
 #pragma unroll
@@ -100,8 +99,6 @@ __global__ void __launch_bounds__(256) gemv_q4_k_sk_kernel(const uint8_t* __rest
             xl[i] = a.x; xl[i + 1] = a.y; xl[i + 2] = a.z; xl[i + 3] = a.w;
             xh[i] = c.x; xh[i + 1] = c.y; xh[i + 2] = c.z; xh[i + 3] = c.w;
         }
-#pragma unroll
-        for (int i = 0; i < NE; ++i) { sxl += xl[i]; sxh += xh[i]; }
     }
 
     auto compute = [&](const Q4KRow<CPL>(&t)[U], int64_t rfirst) {
@@ -110,6 +107,9 @@ __global__ void __launch_bounds__(256) gemv_q4_k_sk_kernel(const uint8_t* __rest
             uint32_t sc0, m0, sc1, m1;
             dec(t[u].hd.y, t[u].hd.z, t[u].hd.w, sc0, m0, sc1, m1);
             const float d = f16_bits_to_f32(t[u].hd.x), dm = f16_bits_to_f32(t[u].hd.x >> 16);
+            // per weight: w = fma(s, f, -t) (f = q, or 16 q with s pre-divided by 16)
+            const float s0 = d * (float)sc0, t0 = dm * (float)m0;
+            const float s1 = (d * 0.0625f) * (float)sc1, t1 = dm * (float)m1;
             float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
@@ -119,22 +119,17 @@ __global__ void __launch_bounds__(256) gemv_q4_k_sk_kernel(const uint8_t* __rest
                     const uint32_t lo = vand(qw[wd], 0x0F0F0F0Fu);
                     const uint32_t hi = vand(qw[wd], 0xF0F0F0F0u);   // 16 * high nibble
                     const int e = 16 * c + 4 * wd;
-                    a0 = __builtin_fmaf(byte_f(lo, 0), xl[e + 0], a0);
-                    a1 = __builtin_fmaf(byte_f(lo, 1), xl[e + 1], a1);
-                    a0 = __builtin_fmaf(byte_f(lo, 2), xl[e + 2], a0);
-                    a1 = __builtin_fmaf(byte_f(lo, 3), xl[e + 3], a1);
-                    b0 = __builtin_fmaf(byte_f(hi, 0), xh[e + 0], b0);
-                    b1 = __builtin_fmaf(byte_f(hi, 1), xh[e + 1], b1);
-                    b0 = __builtin_fmaf(byte_f(hi, 2), xh[e + 2], b0);
-                    b1 = __builtin_fmaf(byte_f(hi, 3), xh[e + 3], b1);
+                    a0 = __builtin_fmaf(__builtin_fmaf(s0, byte_f(lo, 0), -t0), xl[e + 0], a0);
+                    a1 = __builtin_fmaf(__builtin_fmaf(s0, byte_f(lo, 1), -t0), xl[e + 1], a1);
+                    a0 = __builtin_fmaf(__builtin_fmaf(s0, byte_f(lo, 2), -t0), xl[e + 2], a0);
+                    a1 = __builtin_fmaf(__builtin_fmaf(s0, byte_f(lo, 3), -t0), xl[e + 3], a1);
+                    b0 = __builtin_fmaf(__builtin_fmaf(s1, byte_f(hi, 0), -t1), xh[e + 0], b0);
+                    b1 = __builtin_fmaf(__builtin_fmaf(s1, byte_f(hi, 1), -t1), xh[e + 1], b1);
+                    b0 = __builtin_fmaf(__builtin_fmaf(s1, byte_f(hi, 2), -t1), xh[e + 2], b0);
+                    b1 = __builtin_fmaf(__builtin_fmaf(s1, byte_f(hi, 3), -t1), xh[e + 3], b1);
                 }
             }
-            const float s0 = d * (float)sc0, t0 = dm * (float)m0;
-            const float s1 = (d * 0.0625f) * (float)sc1, t1 = dm * (float)m1;
-            float pu = s0 * (a0 + a1);
-            pu = __builtin_fmaf(-t0, sxl, pu);
-            pu = __builtin_fmaf(s1, b0 + b1, pu);
-            pu = __builtin_fmaf(-t1, sxh, pu);
+            const float pu = (a0 + a1) + (b0 + b1);
             const float v = wave_sum(pu);
             if (lane == 0 && rfirst + u < r1) {
                 if (S == 1) y[rfirst + u] = v;

@@ -133,28 +133,36 @@ int frq_dev_dequant(int qtype, const void* w, size_t w_bytes, int64_t n_elems, f
  * Q4_K with n > 1280 and k <= 32768 (w and x 16-byte aligned) runs on the
  * matrix cores: int8 MFMA on the 4-bit codes and on x written per
  * 32-element sub-block as a 60-bit fixed-point number relative to the
- * sub-block's max |x| (eight 8-bit digits), exact integer dot products, then
- *   y_i = sum_s [ d*sc_s * sum(q x) - dmin*m_s * sum(x) ]
- * in fp32. Every x within 2^36 of its sub-block's max |x| is carried
- * exactly; a block whose x is not (a wider range, |x| >= 2^30, inf, NaN) is
- * computed per weight in fp32 (w = fl(fl(d*sc)*q) - fl(dmin*m), q4_k.h:153-185).
- * For every finite x the error of row i is therefore within the fp32
- * accumulation bound  c * 2^-24 * sum_j (d*sc_j*q_ij + dmin*m_j) |x_j|  (c a
- * small multiple of the summation depth; sum_j |w_ij x_j| for per-weight
- * blocks), which the tests hold to 1e-5 of sum_j |w_ij x_j| (componentwise)
- * and of max |y| (normwise). Rows longer than 64 blocks, and n <= 4096 with
- * k >= 8192, are split in two halves of k over two workgroups that combine
- * in a fixed order through per-row slots in the stream's scratch. The
- * other shapes and formats run on the element-wise kernels (the same bound,
- * other bits).
+ * sub-block's max |x| (eight 8-bit digits), exact integer sums of q x and
+ * of x, then per sub-block
+ *   T_s = d*sc_s * sum(q x) - dmin*m_s * sum(x)
+ * formed exactly in fp64 and summed per lane in fp64, rounded to fp32 once.
+ * Every x within 2^36 of its sub-block's max |x| is carried exactly; a
+ * block whose x is not (a wider range, |x| >= 2^30, inf, NaN) is computed
+ * per weight in fp32 (w = fl(fl(d*sc)*q) - fl(dmin*m), q4_k.h:153-185).
+ * Rows longer than 64 blocks, and n <= 4096 with k >= 8192, are split in
+ * two halves of k over two workgroups that combine in a fixed order through
+ * per-row slots in the stream's scratch. The other shapes and formats run
+ * on element-wise kernels whose every product is w_j x_j with the weight
+ * itself (Q4_K / Q5_K: w = fma(d*sc, q, -dmin*m), the dequantized bits;
+ * Q6_K / Q8_0: signed codes under the block scale; Q1_0: +-d).
+ * Error: for every finite x, row i is within the fp32 accumulation bound
+ *   c * 2^-24 * sum_j |w_ij x_j|   (c a small multiple of the summation
+ * depth), which the tests hold to 1e-5 of sum_j |w_ij x_j| (componentwise)
+ * and of max |y| (normwise) -- including outliers x_j on weights that are
+ * exactly zero while their scales are not (d*sc*q = dmin*m), where a sum
+ * written as s * sum(q x) - t * sum(x) in fp32 would cancel.
  * batch >= 2 with Q4_K, Q6_K or Q8_0 (x 16-byte aligned, k a multiple of the
  * block) is one fp32-contract GEMM that reads W once per 32 or 64 rows of x:
- * bf16 matrix cores on W's exact integer codes and on x split into three
- * bf16 pieces (all 24 bits of every x with |x| >= 2^-110), fp32 sums per
- * sub-block, then the sub-block scales in fp32 -- the same error bound, other
- * bits than one row at a time. Few output tiles split k over workgroups
- * whose fp32 partials a second kernel adds in a fixed order (scratch of the
- * stream). Q5_K and Q1_0 run one matvec per row. */
+ * bf16 matrix cores on exact integer codes (Q4_K q - c with c the code
+ * nearest dmin*m / d*sc, so every term stays within 3 |w_j x_j|) and on x
+ * split into three bf16 pieces (all 24 bits of every x with
+ * |x| >= 2^-110), fp32 sums per sub-block, then the sub-block scales in
+ * fp32 -- the same error bound, other bits than one row at a time. Two or
+ * three rows of a Q4_K matrix that takes the matrix-core GEMV run one GEMV
+ * per row (each row's bits those of a batch-1 call). Few output tiles split
+ * k over workgroups whose fp32 partials a second kernel adds in a fixed
+ * order (scratch of the stream). Q5_K and Q1_0 run one matvec per row. */
 int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
                  int64_t batch, void* stream);
 

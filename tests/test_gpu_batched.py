@@ -180,3 +180,20 @@ def test_batched_noalloc_fewer_splits(frq):
         w.free()
         xd.free()
         yd.free()
+
+
+@pytest.mark.parametrize("n,k,seq", [(3584, 18944, 2), (3584, 18944, 3), (3584, 18944, 4), (18944, 3584, 3),
+                                     (4096, 4096, 2), (1536, 8960, 3)])
+def test_batched_q4k_few_rows(frq, n, k, seq):
+    """Two or three rows of x on a Q4_K matrix the matrix-core GEMV takes run
+    as one GEMV per row: every row has the bits of a batch-1 call on that
+    row; from four rows on, the GEMM. Either way within the matvec bound,
+    with an outlier of 2^24 in the last row."""
+    raw = synth.make_blocks("Q4_K", n, k, seed=n + seq)
+    xs = synth.make_x(k, seed=seq + 80, batch=seq)
+    xs[seq - 1, 5] = 2.0**24
+    y = dev_batched("Q4_K", raw, xs, n, k)
+    if seq <= 3:
+        for r in range(seq):
+            assert bits_equal(y[r], dev_batched("Q4_K", raw, xs[r:r + 1].copy(), n, k)[0]), r
+    oracle_rows("Q4_K", raw, xs, n, k, y, f"Q4_K {n}x{k} rows {seq}")

@@ -374,3 +374,20 @@ def test_mx_rejects(frq):
     finally:
         for b in (w, xd, yd, q5, q6):
             b.free()
+
+
+@pytest.mark.parametrize("ks", [1, 2])
+def test_mx_outliers_on_cancelling_weights(frq, ks):
+    """An outlier x of 2^24 (and -2^20) on ordinary weight columns, where
+    some rows have d*sc*q close to dmin*m: each sub-block is combined from
+    exact integer sums in fp64 and rounded once, so the error stays within
+    2^-24 of the sub-block's own sum_j w_j x_j and the componentwise bound
+    (1e-5 of sum_j |w_j x_j|) holds for every row."""
+    n, k = 512, 4096 * ks
+    raw = synth.make_blocks("Q4_K", n, k, seed=300 + ks)
+    x = synth.make_x(k, seed=301)
+    x[5] = 2.0**24
+    x[1000] = -(2.0**20)
+    x[777] = 3.0e4
+    y, _ = run_mx(raw, x, n, k, ksplit=ks)
+    oracle_check(y, raw, x, n, k, f"cancelling weights ks={ks}")
