@@ -281,7 +281,7 @@ int gemv_batched(int qtype, const uint8_t* w, const float* x, float* y, int64_t 
             FRQ_HIP(frq::launch_gemm_f32(qtype, w, x, y, batch, n, k, ldy, s, fixed->part, fixed->part_bytes));
             return FRQ_OK;
         }
-        const size_t pb = frq::gemm_f32_scratch(batch, n, k);
+        const size_t pb = frq::gemm_f32_scratch(qtype, batch, n, k);
         float* part = nullptr;
         uint32_t* cnt = nullptr;
         std::lock_guard<std::mutex> lk(g_sk_mu);

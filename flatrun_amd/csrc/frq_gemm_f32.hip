@@ -57,7 +57,7 @@ __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
 __device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
 
-// Codes of one step for one W row: `cnt` (16 or 32) consecutive elements of
+// Codes of one step for one W row: `cnt` (8, 16 or 32) consecutive elements of
 // the step starting at element `k0` of the step, as bf16, plus the row's
 // scales for the step (written by the thread with k0 == 0).
 template <int QT>
@@ -71,15 +71,26 @@ struct CFmt<kTypeQ4K> {
     template <int CNT>
     struct Raw {
         u32x4 h;
-        u32x4 q[CNT / 16];
+        uint32_t q[CNT / 4];
     };
     template <int CNT>
     __device__ static void load(Raw<CNT>& r, const uint8_t* wrow, int step, int k0) {
         const uint8_t* bp = wrow + (int64_t)(step >> 3) * kQ4KBytes;
         const int j = step & 7;
         r.h = *reinterpret_cast<const u32x4*>(bp);
+        const uint8_t* qp = bp + 16 + 32 * (j >> 1) + k0;
+        if constexpr (CNT == 8) {
+            const u32x2 v = *reinterpret_cast<const u32x2*>(qp);
+            r.q[0] = v[0];
+            r.q[1] = v[1];
+        } else {
 #pragma unroll
-        for (int c = 0; c < CNT / 16; ++c) r.q[c] = *reinterpret_cast<const u32x4*>(bp + 16 + 32 * (j >> 1) + k0 + 16 * c);
+            for (int c = 0; c < CNT / 16; ++c) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(qp + 16 * c);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) r.q[4 * c + i] = v[i];
+            }
+        }
     }
     // Centred codes: w = s q - t = s (q - c) - (t - s c) with c = round(t / s)
     // clamped to 0 .. 15, so the code q - c (-15 .. 15, exact in bf16) is 0 on
@@ -99,13 +110,11 @@ struct CFmt<kTypeQ4K> {
         const float cf = fminf(fmaxf(__builtin_rintf(t * __builtin_amdgcn_rcpf(s)), 0.0f), 15.0f);
         const int ci = (int)cf;
 #pragma unroll
-        for (int c = 0; c < CNT / 16; ++c)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t v = (r.q[c][i] >> sh) & 0x0F0F0F0Fu;
-                out[8 * c + 2 * i] = bf16_pair((float)((int)(v & 15u) - ci), (float)((int)((v >> 8) & 15u) - ci));
-                out[8 * c + 2 * i + 1] = bf16_pair((float)((int)((v >> 16) & 15u) - ci), (float)((int)(v >> 24) - ci));
-            }
+        for (int i = 0; i < CNT / 4; ++i) {
+            const uint32_t v = (r.q[i] >> sh) & 0x0F0F0F0Fu;
+            out[2 * i] = bf16_pair((float)((int)(v & 15u) - ci), (float)((int)((v >> 8) & 15u) - ci));
+            out[2 * i + 1] = bf16_pair((float)((int)((v >> 16) & 15u) - ci), (float)((int)(v >> 24) - ci));
+        }
         if (first) {
             scl[0] = s;
             scl[1] = __builtin_fmaf(-s, cf, t);                       // t - s c, one rounding
@@ -188,15 +197,17 @@ struct CFmt<kTypeQ6K> {
     }
 };
 
-template <int QT, int WM, int WN>
-__global__ void __launch_bounds__(256) gemm_f32c_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                        float* __restrict__ y, int M, int N, int K, int64_t ldy, int S,
-                                                        float* __restrict__ part) {
-    static_assert(WM * WN == 4, "four waves");
-    constexpr int BM = 32 * WM, BN = 64 * WN;
-    constexpr int XT = 256 / BM, XV = kCK / XT;      // X staging: threads per row, values per thread
-    constexpr int WT = 256 / BN, WV = kCK / WT;      // W staging: threads per row, codes per thread
-    static_assert((XV == 4 || XV == 8) && (WV == 16 || WV == 32), "staging shapes");
+template <int QT, int WM, int WN, int MI>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_f32c_kernel(const uint8_t* __restrict__ w,
+                                                                 const float* __restrict__ x, float* __restrict__ y,
+                                                                 int M, int N, int K, int64_t ldy, int S,
+                                                                 float* __restrict__ part) {
+    static_assert(WM * WN == 4 || WM * WN == 8, "four or eight waves");
+    constexpr int NT = 64 * WM * WN;                  // threads
+    constexpr int BM = 32 * MI * WM, BN = 64 * WN;    // a wave owns 32 MI x 64 of the tile
+    constexpr int XT = NT / BM, XV = kCK / XT;       // X staging: threads per row, values per thread
+    constexpr int WT = NT / BN, WV = kCK / WT;       // W staging: threads per row, codes per thread
+    static_assert((XV == 4 || XV == 8) && (WV == 8 || WV == 16 || WV == 32), "staging shapes");
     __shared__ __attribute__((aligned(16))) uint16_t xs[2][3][BM * kCRow];
     __shared__ __attribute__((aligned(16))) uint16_t ws[2][BN * kCRow];
     __shared__ __attribute__((aligned(16))) float xsum[2][BM];
@@ -223,14 +234,14 @@ __global__ void __launch_bounds__(256) gemm_f32c_kernel(const uint8_t* __restric
         f32x4 xv[XV / 4];
         typename F::template Raw<WV> wr;
     };
-    Stage st;
-    auto load_step = [&](int s) __attribute__((always_inline)) {
+    Stage stg[2];
+    auto load_step = [&](Stage& st, int s) __attribute__((always_inline)) {
         const int kb = (sbase + s) * kCK;
 #pragma unroll
         for (int i = 0; i < XV / 4; ++i) st.xv[i] = *reinterpret_cast<const f32x4*>(xrow + kb + xk + 4 * i);
         F::template load<WV>(st.wr, wrow, sbase + s, wk);
     };
-    auto stage_step = [&](int buf, int s) __attribute__((always_inline)) {
+    auto stage_step = [&](const Stage& st, int buf, int s) __attribute__((always_inline)) {
         // X: three bf16 pieces per value and the row's sum over the step
         uint32_t p1[XV / 2], p2[XV / 2], p3[XV / 2];
         float sx = 0.0f;
@@ -272,102 +283,162 @@ __global__ void __launch_bounds__(256) gemm_f32c_kernel(const uint8_t* __restric
         for (int i = 0; i < WV / 8; ++i)
             *reinterpret_cast<u32x4*>(&ws[buf][wr * kCRow + wk + 8 * i]) = u32x4{cw[4 * i], cw[4 * i + 1], cw[4 * i + 2],
                                                                                 cw[4 * i + 3]};
+        static_assert(WV % 8 == 0, "whole 16-byte code chunks");
         if (wk == 0) {
             wsc[buf][wr][0] = scl[0];
             wsc[buf][wr][1] = scl[1];
         }
     };
 
-    f32x16 acc[2];
+    f32x16 acc[MI][2];
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[ni][r] = 0.0f;
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
 
-    const int arow = 32 * wm + (lane & 31), kh = 8 * (lane >> 5);
+    const int mbase = 32 * MI * wm, kh = 8 * (lane >> 5);
+    // Per step: the B fragments (both 16-k halves, both column tiles) once;
+    // then each 32-row sub-tile mi in turn with its own A fragments and two
+    // sub-block sums live (cs), scaled into acc when its sub-block ends.
     auto compute = [&](int buf) __attribute__((always_inline)) {
-        f32x16 cs[2];
-        // sum(x) of the lane's 16 rows (Q4_K min term): rows 32 wm + 8 i + 4 (l / 32) + j
-        f32x4 sxr[4];
-        if constexpr (QT == kTypeQ4K) {
+        bf16x8 b[2][2];                                  // [ks][ni]
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                sxr[i] = *reinterpret_cast<const f32x4*>(&xsum[buf][32 * wm + 8 * i + 4 * (lane >> 5)]);
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            bf16x8 a[3], b[2];
-#pragma unroll
-            for (int p = 0; p < 3; ++p)
-                a[p] = *reinterpret_cast<const bf16x8*>(&xs[buf][p][arow * kCRow + 16 * ks + kh]);
+        for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni)
-                b[ni] = *reinterpret_cast<const bf16x8*>(&ws[buf][(64 * wn + 32 * ni + (lane & 31)) * kCRow + 16 * ks + kh]);
+                b[ks][ni] = *reinterpret_cast<const bf16x8*>(
+                    &ws[buf][(64 * wn + 32 * ni + (lane & 31)) * kCRow + 16 * ks + kh]);
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni) {
-                if (QT == kTypeQ6K || ks == 0) {
+        for (int mi = 0; mi < MI; ++mi) {
+            const int row = mbase + 32 * mi + (lane & 31);
+            bf16x8 a[2][3];                              // [ks][piece]
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) cs[ni][r] = 0.0f;
-                }
+            for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-                for (int p = 0; p < 3; ++p) cs[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[p], b[ni], cs[ni], 0, 0, 0);
+                for (int p = 0; p < 3; ++p)
+                    a[ks][p] = *reinterpret_cast<const bf16x8*>(&xs[buf][p][row * kCRow + 16 * ks + kh]);
+            // sum(x) of the lane's 16 rows (Q4_K min term): rows 32 mi + 8 i + 4 (l / 32) + j
+            f32x4 sxr[4];
+            if constexpr (QT == kTypeQ4K) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    sxr[i] = *reinterpret_cast<const f32x4*>(&xsum[buf][mbase + 32 * mi + 8 * i + 4 * (lane >> 5)]);
             }
-            if (QT == kTypeQ6K || ks == 1) {   // one sub-block done: scale it into the accumulators
+            f32x16 cs[2];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni) {
-                    const int nl = 64 * wn + 32 * ni + (lane & 31);
-                    const float s = wsc[buf][nl][QT == kTypeQ6K ? ks : 0];
+                    // a new sub-block starts from a zero C operand (no register clears)
+                    const f32x16 zero = {};
+                    cs[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][0], b[ks][ni],
+                                                                     (QT == kTypeQ6K || ks == 0) ? zero : cs[ni], 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[ni][r] = __builtin_fmaf(s, cs[ni][r], acc[ni][r]);
-                    if constexpr (QT == kTypeQ4K) {
-                        const float t = wsc[buf][nl][1];
+                    for (int p = 1; p < 3; ++p)
+                        cs[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][p], b[ks][ni], cs[ni], 0, 0, 0);
+                }
+                if (QT == kTypeQ6K || ks == 1) {   // one sub-block done: scale it into the accumulators
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[ni][r] = __builtin_fmaf(-t, sxr[r >> 2][r & 3], acc[ni][r]);
+                    for (int ni = 0; ni < 2; ++ni) {
+                        const int nl = 64 * wn + 32 * ni + (lane & 31);
+                        const float sc = wsc[buf][nl][QT == kTypeQ6K ? ks : 0];
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[mi][ni][r] = __builtin_fmaf(sc, cs[ni][r], acc[mi][ni][r]);
+                        if constexpr (QT == kTypeQ4K) {
+                            const float t = wsc[buf][nl][1];
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                acc[mi][ni][r] = __builtin_fmaf(-t, sxr[r >> 2][r & 3], acc[mi][ni][r]);
+                        }
                     }
                 }
             }
         }
     };
 
-    load_step(0);
-    stage_step(0, 0);
-    __syncthreads();
-    for (int s = 0; s < steps; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < steps) load_step(s + 1);
-        compute(buf);
-        if (s + 1 < steps) stage_step(buf ^ 1, s + 1);
+    // Global loads run two steps ahead of the products (32-row wave tiles):
+    // step s + 2 is loaded into staging set s % 2 while step s is computed, and staged
+    // into LDS (buffer (s + 1) % 2) after step s + 1's loads have had a whole
+    // step to arrive. The loop is unrolled by two so each staging set is a
+    // compile-time choice, and loads and stages are unconditional (past the
+    // last step they repeat it into a buffer nothing reads again), so the
+    // compiler's wait before a stage covers one staging set only. An odd
+    // last step is computed after the loop from buffer 0.
+    const int last = steps - 1;
+    if constexpr (MI == 1) {
+        load_step(stg[0], 0);
+        load_step(stg[1], last < 1 ? last : 1);
+        stage_step(stg[0], 0, 0);
         __syncthreads();
+        int s0 = 0;
+        for (; s0 + 1 < steps; s0 += 2) {
+            static_for<0, 2>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;  // s % 2: LDS buffer and staging set of step s
+                const int s = s0 + j;
+                load_step(stg[j], s + 2 < last ? s + 2 : last);
+                compute(j);
+                stage_step(stg[j ^ 1], j ^ 1, s + 1 < last ? s + 1 : last);
+                __syncthreads();
+            });
+        }
+        if (s0 < steps) compute(0);
+    } else {
+        // 64-row wave tiles do twice the products per step, which covers the
+        // load latency with one staging set (the registers of a second do
+        // not fit beside the accumulators)
+        load_step(stg[0], 0);
+        stage_step(stg[0], 0, 0);
+        __syncthreads();
+        for (int s = 0; s < steps; ++s) {
+            const int buf = s & 1;
+            load_step(stg[0], s + 1 < last ? s + 1 : last);
+            compute(buf);
+            stage_step(stg[0], buf ^ 1, s + 1 < last ? s + 1 : last);
+            __syncthreads();
+        }
     }
 
     // S > 1: this split's partial tile goes to plane `split` (rows of N)
     float* out = S == 1 ? y : part + (int64_t)split * M * N;
     const int64_t ld = S == 1 ? ldy : N;
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-        const int n = n0 + 64 * wn + 32 * ni + (lane & 31);
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int m = m0 + 32 * wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (m < M && n < N) out[(int64_t)m * ld + n] = acc[ni][r];
+        for (int ni = 0; ni < 2; ++ni) {
+            const int n = n0 + 64 * wn + 32 * ni + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + mbase + 32 * mi + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < M && n < N) out[(int64_t)m * ld + n] = acc[mi][ni][r];
+            }
         }
-    }
 }
 
 template <int QT>
-void f32c_go(bool small_m, dim3 g, hipStream_t s, const uint8_t* w, const float* x, float* y, int M, int N, int K,
+void f32c_go(int bm, int bn, dim3 g, hipStream_t s, const uint8_t* w, const float* x, float* y, int M, int N, int K,
              int64_t ldy, int S, float* part) {
-    if (small_m)
-        gemm_f32c_kernel<QT, 1, 4><<<g, dim3(256), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
+    if (bm == 32)
+        gemm_f32c_kernel<QT, 1, 4, 1><<<g, dim3(256), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
+    else if (bm == 64)
+        gemm_f32c_kernel<QT, 2, 2, 1><<<g, dim3(256), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
+    else if (bn == 128)
+        gemm_f32c_kernel<QT, 4, 2, 1><<<g, dim3(512), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
     else
-        gemm_f32c_kernel<QT, 2, 2><<<g, dim3(256), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
+        gemm_f32c_kernel<QT, 2, 4, 2><<<g, dim3(512), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
 }
 
-// Tile shape: BM x BN = 32 x 256 for up to 32 rows of X, else 64 x 128.
-void f32c_tile(int64_t m, int* bm, int* bn) {
-    const bool small = m <= 32;
-    *bm = small ? 32 : 64;
-    *bn = small ? 256 : 128;
+// Tile shape: BM x BN = 32 x 256 for up to 32 rows of X, 64 x 128 up to
+// kF32cMidRows rows, else eight waves on 128 rows: 128 x 256 for Q4_K (waves
+// of 64 x 64: each staged x piece serves 256 columns, each W code 128 rows),
+// 128 x 128 for Q6_K and Q8_0 (waves of 32 x 64, loads two steps ahead).
+// Measured at 512 rows: Q4_K 3584 x 18944 303 vs 324 us; Q6_K 4096 x 14336
+// 245 vs 282 us; Q8_0 4096 x 4096 66 vs 72 us (128 x 128 vs 128 x 256).
+constexpr int64_t kF32cMidRows = 64;
+void f32c_tile(int qtype, int64_t m, int* bm, int* bn) {
+    *bm = m <= 32 ? 32 : m <= kF32cMidRows ? 64 : 128;
+    *bn = m <= 32 ? 256 : m <= kF32cMidRows ? 128 : qtype == kTypeQ4K ? 256 : 128;
 }
 
 }  // namespace
@@ -377,30 +448,33 @@ bool gemm_f32_supported(int qtype, int64_t m, int64_t n, int64_t k) {
     if (kq == 0 || m <= 0 || n <= 0 || k <= 0 || k % kq || m > 0x7FFFFFFF || n > 0x7FFFFFFF || k > 0x7FFFFFFF)
         return false;
     int bm, bn;
-    f32c_tile(m, &bm, &bn);
+    f32c_tile(qtype, m, &bm, &bn);
     return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) <= 0x7FFFFFFF;
 }
 
 // K-splits: the largest S in {1, 2, 4, ..., 64} that leaves every split >= 8
-// steps (splits differ by at most one step), keeps the grid within two
-// workgroups per CU and its partial planes within `part_cap` bytes; shapes
-// that fill the GPU are not split.
-int gemm_f32_splits(int64_t m, int64_t n, int64_t k, size_t part_cap) {
+// steps (splits differ by at most one step), keeps the grid within one round
+// of workgroups (per_round) and its partial planes within `part_cap` bytes;
+// shapes that fill the GPU are not split.
+int gemm_f32_splits(int qtype, int64_t m, int64_t n, int64_t k, size_t part_cap) {
     int bm, bn;
-    f32c_tile(m, &bm, &bn);
+    f32c_tile(qtype, m, &bm, &bn);
     const int64_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     const int64_t steps = k / kCK;
     const double plane = (double)m * (double)n * sizeof(float);
+    // one round of workgroups: two 4-wave workgroups per CU, or one 8-wave
+    // 128-row workgroup (85 or 105 KB of LDS)
+    const int64_t per_round = bm == 128 ? 256 : 512;
     int best = 1;
     for (int sp = 2; sp <= 64; sp *= 2) {
-        if (steps / sp < 8 || tiles * sp > 512 || sp * plane > (double)part_cap) break;
+        if (steps / sp < 8 || tiles * sp > per_round || sp * plane > (double)part_cap) break;
         best = sp;
     }
     return best;
 }
 
-size_t gemm_f32_scratch(int64_t m, int64_t n, int64_t k, size_t part_cap) {
-    const int sp = gemm_f32_splits(m, n, k, part_cap);
+size_t gemm_f32_scratch(int qtype, int64_t m, int64_t n, int64_t k, size_t part_cap) {
+    const int sp = gemm_f32_splits(qtype, m, n, k, part_cap);
     return sp > 1 ? (size_t)sp * (size_t)m * (size_t)n * sizeof(float) : 0;
 }
 
@@ -411,17 +485,16 @@ hipError_t launch_gemm_f32(int qtype, const uint8_t* w, const float* x, float* y
     if (reinterpret_cast<uintptr_t>(x) & 15) return hipErrorInvalidValue;
     if (qtype == kTypeQ4K && (reinterpret_cast<uintptr_t>(w) & 15)) return hipErrorInvalidValue;
     if (qtype != kTypeQ4K && (reinterpret_cast<uintptr_t>(w) & 1)) return hipErrorInvalidValue;
-    const int sp = gemm_f32_splits(m, n, k, part ? part_cap : 0);
+    const int sp = gemm_f32_splits(qtype, m, n, k, part ? part_cap : 0);
     int bm, bn;
-    f32c_tile(m, &bm, &bn);
+    f32c_tile(qtype, m, &bm, &bn);
     const int64_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     if (tiles * sp > 0x7FFFFFFF) return hipErrorInvalidValue;
     const dim3 g((unsigned)(tiles * sp));
-    const bool small = bm == 32;
     switch (qtype) {
-        case kTypeQ4K: f32c_go<kTypeQ4K>(small, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
-        case kTypeQ6K: f32c_go<kTypeQ6K>(small, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
-        case kTypeQ80: f32c_go<kTypeQ80>(small, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
+        case kTypeQ4K: f32c_go<kTypeQ4K>(bm, bn, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
+        case kTypeQ6K: f32c_go<kTypeQ6K>(bm, bn, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
+        case kTypeQ80: f32c_go<kTypeQ80>(bm, bn, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
         default: return hipErrorInvalidValue;
     }
     if (sp > 1) return launch_split_reduce(part, y, sp, m, n, ldy, stream);

@@ -141,17 +141,17 @@ hipError_t launch_split_reduce(const float* part, float* y, int splits, int64_t 
 // Batched matvec with the fp32 contract on the matrix cores (frq_gemm_f32.hip):
 // y[m, n] = x[m, k] (fp32, row-major) . W[n, k]^T (raw Q4_K, Q6_K or Q8_0) with
 // W as exact integer codes, x as three bf16 pieces and the sub-block scales in
-// fp32; W is read once per tile of 32 or 64 rows of x; rows of y are ldy >= n
-// floats apart. x 16-byte aligned, w
+// fp32; W is read once per tile of 32, 64 or 128 rows of x; rows of y are
+// ldy >= n floats apart. x 16-byte aligned, w
 // 16-byte (Q4_K) / 2-byte aligned; k a multiple of 256 (Q4_K, Q6_K) or 32
 // (Q8_0). Few output tiles split K (gemm_f32_splits, at most `part_cap`
 // bytes of partials): fp32 partial planes in `part` (gemm_f32_scratch bytes)
 // added in split order by a second kernel; launches sharing `part` must be
-// ordered. The split count is a function of (m, n, k, part capacity) only, so
+// ordered. The split count is a function of (qtype, m, n, k, part capacity) only, so
 // results do not depend on which scratch a call gets beyond its capacity.
 bool gemm_f32_supported(int qtype, int64_t m, int64_t n, int64_t k);
-int gemm_f32_splits(int64_t m, int64_t n, int64_t k, size_t part_cap = SIZE_MAX);
-size_t gemm_f32_scratch(int64_t m, int64_t n, int64_t k, size_t part_cap = SIZE_MAX);
+int gemm_f32_splits(int qtype, int64_t m, int64_t n, int64_t k, size_t part_cap = SIZE_MAX);
+size_t gemm_f32_scratch(int qtype, int64_t m, int64_t n, int64_t k, size_t part_cap = SIZE_MAX);
 hipError_t launch_gemm_f32(int qtype, const uint8_t* w, const float* x, float* y, int64_t m, int64_t n, int64_t k,
                            int64_t ldy, hipStream_t stream, float* part, size_t part_cap);
 
