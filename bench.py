@@ -604,19 +604,26 @@ DEQUANT_SUITE = [("Q8_0", 4864, 896), ("Q4_K", 18944, 3584), ("Q5_K", 18944, 358
                  ("Q5_1", 18944, 3584)]
 
 
+# fp16-output dequant (dequant_handle's default dtype): the big shapes
+DEQUANT_F16_SUITE = [("Q4_K", 18944, 3584), ("Q6_K", 152064, 3584)]
+
+
 def dequant_suite(stream, reps: int = 20) -> dict:
     """Block dequant to fp32 at the workload shapes, and every format at
     18944 x 3584 (271 MB of fp32 out, past the 256 MB last-level cache, so
     the formats compare on HBM): algorithmic bytes = raw blocks read +
-    4 n k written, timed as a graph of `reps` launches over 2 weight copies."""
+    4 n k written (2 n k for the fp16 lines, `_f16`), timed as a graph of
+    `reps` launches over 2 weight copies."""
     out = {}
-    for q, n, k in DEQUANT_SUITE:
+    cases = [(q, n, k, 4) for q, n, k in DEQUANT_SUITE] + [(q, n, k, 2) for q, n, k in DEQUANT_F16_SUITE]
+    for q, n, k, osz in cases:
         raw = synth.make_blocks(q, n, k, seed=50)
         ws = [device.DeviceBuffer.from_host(raw) for _ in range(2)]
-        y = device.DeviceBuffer(4 * n * k)
+        y = device.DeviceBuffer(osz * n * k)
+        step = device.dequant if osz == 4 else device.dequant_f16
         with device.Graph.capture(stream) as cap:
             for i in range(reps):
-                device.dequant(q, ws[i % 2], y, n * k, stream=stream, w_bytes=raw.nbytes)
+                step(q, ws[i % 2], y, n * k, stream=stream, w_bytes=raw.nbytes)
         cap.launch(stream)
         device.synchronize()
         e0, e1 = device.Event(), device.Event()
@@ -629,8 +636,9 @@ def dequant_suite(stream, reps: int = 20) -> dict:
         for b in ws:
             b.free()
         y.free()
-        nbytes = raw.nbytes + 4 * n * k
-        out[f"{q.lower()}_{n}x{k}"] = {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
+        nbytes = raw.nbytes + osz * n * k
+        out[f"{q.lower()}_{n}x{k}" + ("_f16" if osz == 2 else "")] = {
+                                       "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
                                        "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
                                        "algorithmic_bytes": nbytes}
     return out

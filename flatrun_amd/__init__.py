@@ -28,10 +28,12 @@ import numpy as np
 
 from . import _C, _lib
 from ._lib import FrqError, LibraryMissing
+from .loader import dequant_handle
 from .residency import WeightCache
 
 __all__ = [
     "NativeBackend",
+    "dequant_handle",
     "DeviceWeight",
     "Q4K_GEMM_BLOCK",
     "is_available",

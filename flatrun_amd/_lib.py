@@ -75,6 +75,7 @@ SIGNATURES: dict[str, list] = {
     "frq_dequant_q8_0": [_vp, _sz, _i64, _i64, _vp],
     "frq_dequant_q6_k": [_vp, _sz, _i64, _i64, _vp],
     "frq_dequant": [_i32, _vp, _sz, _i64, _vp],
+    "frq_dequant_f16": [_i32, _vp, _sz, _i64, _vp],
     "frq_matmul_q4_k": [_vp, _sz, _vp, _sz, _sz, _sz, _vp],
     "frq_matmul_q4_k_batched": [_vp, _i32, _sz, _sz, _vp, _sz, _sz, _sz, _vp],
     "frq_matmul_q8_0": [_vp, _sz, _vp, _sz, _sz, _sz, _vp],
@@ -83,6 +84,7 @@ SIGNATURES: dict[str, list] = {
     "frq_matmul_q6_k_batched": [_vp, _i32, _sz, _sz, _vp, _sz, _sz, _sz, _vp],
     "frq_matmul": [_i32, _vp, _sz, _vp, _sz, _sz, _sz, _vp],
     "frq_dev_dequant": [_i32, _vp, _sz, _i64, _vp, _vp],
+    "frq_dev_dequant_f16": [_i32, _vp, _sz, _i64, _vp, _vp],
     "frq_dev_gemv": [_i32, _vp, _sz, _vp, _vp, _i64, _i64, _i64, _vp],
     "frq_dev_gemv_noalloc": [_i32, _vp, _sz, _vp, _vp, _i64, _i64, _i64, _vp],
     "frq_dev_gemv_group": [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _vp],

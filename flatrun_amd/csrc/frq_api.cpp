@@ -294,20 +294,29 @@ int gemv_batched(int qtype, const uint8_t* w, const float* x, float* y, int64_t 
     return FRQ_OK;
 }
 
-// Host dequant: stage weight, decode, copy back. n_elems may be ragged.
-int host_dequant(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, float* out) {
+// Host dequant: stage weight, decode (fp32, or fp16 bits), copy back.
+// n_elems may be ragged.
+template <typename T>
+int host_dequant_t(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, T* out) {
     if (n_elems == 0) return FRQ_OK;
     if (int rc = have_device()) return rc;
     std::lock_guard<std::mutex> lk(g_ws.mu);
-    const size_t wb = align256(weight_bytes), yb = align256((size_t)n_elems * 4);
+    const size_t wb = align256(weight_bytes), yb = align256((size_t)n_elems * sizeof(T));
     void* base = nullptr;
     if (int rc = workspace(wb + yb, &base)) return rc;
     uint8_t* dw = static_cast<uint8_t*>(base);
-    float* dy = reinterpret_cast<float*>(dw + wb);
+    T* dy = reinterpret_cast<T*>(dw + wb);
     FRQ_HIP(hipMemcpy(dw, weight, weight_bytes, hipMemcpyHostToDevice));
-    FRQ_HIP(frq::launch_dequant(qtype, dw, dy, n_elems, nullptr));
-    FRQ_HIP(hipMemcpy(out, dy, (size_t)n_elems * 4, hipMemcpyDeviceToHost));
+    if constexpr (sizeof(T) == 2)
+        FRQ_HIP(frq::launch_dequant_f16(qtype, dw, dy, n_elems, nullptr));
+    else
+        FRQ_HIP(frq::launch_dequant(qtype, dw, dy, n_elems, nullptr));
+    FRQ_HIP(hipMemcpy(out, dy, (size_t)n_elems * sizeof(T), hipMemcpyDeviceToHost));
     return FRQ_OK;
+}
+
+int host_dequant(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, float* out) {
+    return host_dequant_t(qtype, weight, weight_bytes, n_elems, out);
 }
 
 // Host matmul over seq rows of x (already validated).
@@ -396,6 +405,20 @@ int matmul_2d(int qtype, const float* x, int x_ndim, size_t seq, size_t x_cols, 
     return host_matmul(qtype, x, seq, weight, weight_bytes, n, k, out);
 }
 
+// Format, element count and byte size of a dequant call (the NumPy
+// decoders' ceil-div block rule, gguf.py:61-73), and non-null buffers.
+int dequant_checks(int qtype, const void* w, size_t w_bytes, int64_t n_elems, const void* y) {
+    Fmt f;
+    if (!fmt_of(qtype, &f)) return fail(FRQ_ERR_INVALID, "unknown quant type %d", qtype);
+    if (n_elems < 0) return fail(FRQ_ERR_SHAPE, "%s: negative element count", f.name);
+    const int64_t nblk = (n_elems + f.belems - 1) / f.belems;
+    if ((int64_t)w_bytes != nblk * f.bbytes)
+        return fail(FRQ_ERR_SIZE, "%s weight byte size mismatch: expected %lld bytes, got %zu", f.name,
+                    (long long)(nblk * f.bbytes), w_bytes);
+    if ((!w && w_bytes) || (!y && n_elems)) return fail(FRQ_ERR_INVALID, "null buffer");
+    return FRQ_OK;
+}
+
 int check_dev_ptrs(int qtype, const void* w, const float* x, const float* y) {
     const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
     const bool k_quant16 = qtype == FRQ_Q4_K || qtype == FRQ_Q5_K;
@@ -438,15 +461,13 @@ int frq_dequant_q8_0(const uint8_t* w, size_t wb, int64_t o, int64_t i, float* o
 int frq_dequant_q6_k(const uint8_t* w, size_t wb, int64_t o, int64_t i, float* out) { return dequant_2d(FRQ_Q6_K, w, wb, o, i, out); }
 
 int frq_dequant(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, float* out) {
-    Fmt f;
-    if (!fmt_of(qtype, &f)) return fail(FRQ_ERR_INVALID, "unknown quant type %d", qtype);
-    if (n_elems < 0) return fail(FRQ_ERR_SHAPE, "%s: negative element count", f.name);
-    const int64_t nblk = (n_elems + f.belems - 1) / f.belems;
-    if ((int64_t)weight_bytes != nblk * f.bbytes)
-        return fail(FRQ_ERR_SIZE, "%s weight byte size mismatch: expected %lld bytes, got %zu", f.name,
-                    (long long)(nblk * f.bbytes), weight_bytes);
-    if ((!weight && weight_bytes) || (!out && n_elems)) return fail(FRQ_ERR_INVALID, "null buffer");
+    if (int rc = dequant_checks(qtype, weight, weight_bytes, n_elems, out)) return rc;
     return host_dequant(qtype, weight, weight_bytes, n_elems, out);
+}
+
+int frq_dequant_f16(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, uint16_t* out) {
+    if (int rc = dequant_checks(qtype, weight, weight_bytes, n_elems, out)) return rc;
+    return host_dequant_t(qtype, weight, weight_bytes, n_elems, out);
 }
 
 int frq_matmul_q4_k(const float* x, size_t xl, const uint8_t* w, size_t wb, size_t n, size_t k, float* out) { return matmul_1d(FRQ_Q4_K, x, xl, w, wb, n, k, out); }
@@ -471,17 +492,20 @@ int frq_matmul(int qtype, const float* x, size_t seq, const uint8_t* weight, siz
 }
 
 int frq_dev_dequant(int qtype, const void* w, size_t w_bytes, int64_t n_elems, float* y, void* stream) {
-    Fmt f;
-    if (!fmt_of(qtype, &f)) return fail(FRQ_ERR_INVALID, "unknown quant type %d", qtype);
-    if (n_elems < 0) return fail(FRQ_ERR_SHAPE, "%s: negative element count", f.name);
-    const int64_t nblk = (n_elems + f.belems - 1) / f.belems;
-    if ((int64_t)w_bytes != nblk * f.bbytes)
-        return fail(FRQ_ERR_SIZE, "%s weight byte size mismatch: expected %lld bytes, got %zu", f.name,
-                    (long long)(nblk * f.bbytes), w_bytes);
+    if (int rc = dequant_checks(qtype, w, w_bytes, n_elems, y)) return rc;
     if (n_elems == 0) return FRQ_OK;
-    if (!w || !y) return fail(FRQ_ERR_INVALID, "null buffer");
     if (int rc = check_dev_ptrs(qtype, w, nullptr, y)) return rc;
     FRQ_HIP(frq::launch_dequant(qtype, static_cast<const uint8_t*>(w), y, n_elems, static_cast<hipStream_t>(stream)));
+    return FRQ_OK;
+}
+
+int frq_dev_dequant_f16(int qtype, const void* w, size_t w_bytes, int64_t n_elems, uint16_t* y, void* stream) {
+    if (int rc = dequant_checks(qtype, w, w_bytes, n_elems, y)) return rc;
+    if (n_elems == 0) return FRQ_OK;
+    if (int rc = check_dev_ptrs(qtype, w, nullptr, nullptr)) return rc;
+    if (reinterpret_cast<uintptr_t>(y) & 1) return fail(FRQ_ERR_ALIGN, "y must be 2-byte aligned");
+    FRQ_HIP(frq::launch_dequant_f16(qtype, static_cast<const uint8_t*>(w), y, n_elems,
+                                    static_cast<hipStream_t>(stream)));
     return FRQ_OK;
 }
 

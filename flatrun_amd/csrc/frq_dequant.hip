@@ -1,4 +1,4 @@
-// GGUF block dequant kernels for gfx950: raw blocks in HBM -> fp32.
+// GGUF block dequant kernels for gfx950: raw blocks in HBM -> fp32, or fp16.
 //
 // Bit-exact contract with the reference NumPy decoders
 // (src/flatrun/dequant/gguf.py), which fixes the rounding sequence:
@@ -15,13 +15,19 @@
 // This translation unit is built with -ffp-contract=off, so none of the
 // products above is fused into the following add.
 //
-// Work mapping: one thread writes four consecutive outputs (one dwordx4
-// store; eight, in two stores, for Q4_K and Q5_K), so a wavefront writes 1-2
-// KiB of contiguous fp32; the kernel is bound by the 4 B/element write
-// stream. A thread's outputs always share one scale, so it decodes one scale
-// pair.
+// Work mapping: one thread writes four consecutive fp32 outputs (one
+// dwordx4 store; eight, in two stores, for Q4_K and Q5_K), so a wavefront
+// writes 1-2 KiB of contiguous fp32; the kernel is bound by the 4 B/element
+// write stream. With fp16 output every thread writes eight (one dwordx4
+// store of 2 B elements: two four-output decodes for the other formats).
+// Four outputs always share one scale, so each decode reads one scale pair.
 // A ragged last block (element count not a multiple of the block) is decoded
 // and the tail trimmed, as the reference's _finish does (gguf.py:61-73).
+// fp16 output: the reference decodes into an fp32 array and _finish casts it
+// (astype, round to nearest even; dequant_handle's default dtype is float16,
+// loader.py:51-88), so each fp32 value above is rounded to fp16 once with
+// v_cvt_f16_f32 (nearest even, overflow to inf, fp16 subnormals kept) and
+// stored as 2 B/element.
 #include "frq_common.h"
 #include "frq_kernels.h"
 
@@ -39,138 +45,212 @@ __device__ __forceinline__ void store4(float* __restrict__ y, int64_t e0, int64_
     }
 }
 
-__device__ __forceinline__ float ub(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
-
-// Q4_K and Q5_K: eight outputs per thread (two dwordx4 stores), all in one
-// 32-element sub-block, so the block header is read and the scale pair
-// decoded once per eight outputs.
-__global__ void __launch_bounds__(256) dequant_q4_k_kernel(const uint8_t* __restrict__ w,
-                                                           float* __restrict__ y, int64_t n) {
-    const int64_t e0 = 8 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
-    if (e0 >= n) return;
-    const int64_t b = e0 / kQKElems;
-    const int o = (int)(e0 % kQKElems);
-    const int j = o >> 5, i = o & 31, g = j >> 1;
-    const uint8_t* blk = w + b * kQ4KBytes;
-    const uint4 hd = *reinterpret_cast<const uint4*>(blk);
-    uint32_t sc, m;
-    k4_scale_min(hd.y, hd.z, hd.w, j, sc, m);
-    const float s = f16_bits_to_f32(hd.x) * (float)sc;
-    const float t = f16_bits_to_f32(hd.x >> 16) * (float)m;
-    const uint2 qq = *reinterpret_cast<const uint2*>(blk + 16 + 32 * g + i);
-    const uint32_t sh = (j & 1) ? 4u : 0u;
-    const uint32_t q0 = (qq.x >> sh) & 0x0F0F0F0Fu, q1 = (qq.y >> sh) & 0x0F0F0F0Fu;
-    store4(y, e0, n, s * ub(q0, 0) - t, s * ub(q0, 1) - t, s * ub(q0, 2) - t, s * ub(q0, 3) - t);
-    store4(y, e0 + 4, n, s * ub(q1, 0) - t, s * ub(q1, 1) - t, s * ub(q1, 2) - t, s * ub(q1, 3) - t);
+// fp16 bits of an fp32 value, rounded to nearest even. The conversion is its
+// own instruction: left to itself the compiler folds "multiply, then
+// convert" into v_fma_mix*_f16, which rounds the exact product once to fp16
+// (the reference rounds to fp32 first) and turns a -0 product into +0.
+__device__ __forceinline__ uint32_t f16_bits(float v) {
+    uint32_t r;
+    asm("v_cvt_f16_f32 %0, %1" : "=v"(r) : "v"(v));
+    return r & 0xFFFFu;
 }
 
-__global__ void __launch_bounds__(256) dequant_q5_k_kernel(const uint8_t* __restrict__ w,
-                                                           float* __restrict__ y, int64_t n) {
-    const int64_t e0 = 8 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
-    if (e0 >= n) return;
-    const int64_t b = e0 / kQKElems;
-    const int o = (int)(e0 % kQKElems);
-    const int j = o >> 5, i = o & 31, g = j >> 1;
-    const uint8_t* blk = w + b * kQ5KBytes;
-    const uint4 hd = *reinterpret_cast<const uint4*>(blk);
-    uint32_t sc, m;
-    k4_scale_min(hd.y, hd.z, hd.w, j, sc, m);
-    const double s = (double)(f16_bits_to_f32(hd.x) * (float)sc);   // fl32(d*sc), widened exactly
-    const double t = (double)(f16_bits_to_f32(hd.x >> 16) * (float)m);
-    const uint2 qq = *reinterpret_cast<const uint2*>(blk + 48 + 32 * g + i);
-    const uint2 hh = *reinterpret_cast<const uint2*>(blk + 16 + i);
-    const uint32_t sh = (j & 1) ? 4u : 0u;
-    const uint32_t qw[2] = {qq.x, qq.y}, hw[2] = {hh.x, hh.y};
-    float v[8];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const uint32_t q = ((qw[p] >> sh) & 0x0F0F0F0Fu) | (((hw[p] >> j) & 0x01010101u) << 4);   // q4 + 16*bit
-#pragma unroll
-        for (int c = 0; c < 4; ++c) v[4 * p + c] = (float)(s * (double)((q >> (8 * c)) & 0xFFu) - t);
+__device__ __forceinline__ void store4(uint16_t* __restrict__ y, int64_t e0, int64_t n, float v0, float v1,
+                                       float v2, float v3) {
+    const uint32_t h0 = f16_bits(v0), h1 = f16_bits(v1), h2 = f16_bits(v2), h3 = f16_bits(v3);
+    if (e0 + 3 < n && ((reinterpret_cast<uintptr_t>(y + e0) & 7) == 0)) {
+        *reinterpret_cast<uint2*>(y + e0) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+    } else {
+        if (e0 + 0 < n) y[e0 + 0] = (uint16_t)h0;
+        if (e0 + 1 < n) y[e0 + 1] = (uint16_t)h1;
+        if (e0 + 2 < n) y[e0 + 2] = (uint16_t)h2;
+        if (e0 + 3 < n) y[e0 + 3] = (uint16_t)h3;
     }
+}
+
+__device__ __forceinline__ void store8(float* __restrict__ y, int64_t e0, int64_t n, const float (&v)[8]) {
     store4(y, e0, n, v[0], v[1], v[2], v[3]);
     store4(y, e0 + 4, n, v[4], v[5], v[6], v[7]);
 }
 
-__global__ void __launch_bounds__(256) dequant_q6_k_kernel(const uint8_t* __restrict__ w,
-                                                           float* __restrict__ y, int64_t n) {
-    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
-    if (e0 >= n) return;
-    const int64_t b = e0 / kQKElems;
-    const int o = (int)(e0 % kQKElems);
-    const int h = o >> 7, k = (o >> 5) & 3, l = o & 31;   // element 128h + 32k + l
-    const uint8_t* blk = w + b * kQ6KBytes;
-    uint32_t nib = ld_u32_a2(blk + 64 * h + 32 * (k & 1) + l);
-    nib = ((k >= 2) ? (nib >> 4) : nib) & 0x0F0F0F0Fu;
-    const uint32_t hb = (ld_u32_a2(blk + 128 + 32 * h + l) >> (2 * k)) & 0x03030303u;
-    const uint32_t q = nib | (hb << 4);
-    const int sc = (int)(int8_t)blk[192 + 8 * h + (l >> 4) + 2 * k];
-    const float s = f16_bits_to_f32(ld_u16(blk + 208)) * (float)sc;
-    store4(y, e0, n, s * (ub(q, 0) - 32.0f), s * (ub(q, 1) - 32.0f), s * (ub(q, 2) - 32.0f),
-           s * (ub(q, 3) - 32.0f));
+__device__ __forceinline__ void store8(uint16_t* __restrict__ y, int64_t e0, int64_t n, const float (&v)[8]) {
+    uint32_t h[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) h[c] = f16_bits(v[c]);
+    if (e0 + 7 < n && ((reinterpret_cast<uintptr_t>(y + e0) & 15) == 0)) {
+        *reinterpret_cast<uint4*>(y + e0) =
+            make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            if (e0 + c < n) y[e0 + c] = (uint16_t)h[c];
+    }
 }
 
-__global__ void __launch_bounds__(256) dequant_q8_0_kernel(const uint8_t* __restrict__ w,
-                                                           float* __restrict__ y, int64_t n) {
-    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
-    if (e0 >= n) return;
-    const int64_t b = e0 / kQ80Elems;
-    const int o = (int)(e0 % kQ80Elems);
-    const uint8_t* blk = w + b * kQ80Bytes;
-    const float d = f16_bits_to_f32(ld_u16(blk));
-    const uint32_t q = ld_u32_a2(blk + 2 + o);
-    float v[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) v[c] = (float)(int)(int8_t)((q >> (8 * c)) & 0xFFu) * d;
-    store4(y, e0, n, v[0], v[1], v[2], v[3]);
-}
+__device__ __forceinline__ float ub(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
 
-__global__ void __launch_bounds__(256) dequant_q1_0_kernel(const uint8_t* __restrict__ w,
-                                                           float* __restrict__ y, int64_t n) {
-    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
-    if (e0 >= n) return;
-    const int64_t b = e0 / kQ10Elems;
-    const int o = (int)(e0 % kQ10Elems);
-    const uint8_t* blk = w + b * kQ10Bytes;
-    const float d = f16_bits_to_f32(ld_u16(blk));
-    const uint32_t bits = (uint32_t)blk[2 + (o >> 3)] >> (o & 7);
-    float v[4];
+// Decoders: v = the elements e0 .. e0 + E - 1 (E = 8 for Q4_K / Q5_K, whose
+// eight share one sub-block, else 4), all inside the allocated blocks for
+// any e0 < n that is a multiple of 8 (every block holds a multiple of 8
+// elements).
+
+// Q4_K and Q5_K: eight outputs, all in one 32-element sub-block, so the
+// block header is read and the scale pair decoded once per eight outputs.
+struct DecQ4K {
+    static constexpr int E = 8;
+    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[8]) {
+        const int64_t b = e0 / kQKElems;
+        const int o = (int)(e0 % kQKElems);
+        const int j = o >> 5, i = o & 31, g = j >> 1;
+        const uint8_t* blk = w + b * kQ4KBytes;
+        const uint4 hd = *reinterpret_cast<const uint4*>(blk);
+        uint32_t sc, m;
+        k4_scale_min(hd.y, hd.z, hd.w, j, sc, m);
+        const float s = f16_bits_to_f32(hd.x) * (float)sc;
+        const float t = f16_bits_to_f32(hd.x >> 16) * (float)m;
+        const uint2 qq = *reinterpret_cast<const uint2*>(blk + 16 + 32 * g + i);
+        const uint32_t sh = (j & 1) ? 4u : 0u;
+        const uint32_t q0 = (qq.x >> sh) & 0x0F0F0F0Fu, q1 = (qq.y >> sh) & 0x0F0F0F0Fu;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) v[c] = ((bits >> c) & 1u) ? d : -d;
-    store4(y, e0, n, v[0], v[1], v[2], v[3]);
-}
+        for (int c = 0; c < 4; ++c) {
+            v[c] = s * ub(q0, c) - t;
+            v[4 + c] = s * ub(q1, c) - t;
+        }
+    }
+};
+
+struct DecQ5K {
+    static constexpr int E = 8;
+    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[8]) {
+        const int64_t b = e0 / kQKElems;
+        const int o = (int)(e0 % kQKElems);
+        const int j = o >> 5, i = o & 31, g = j >> 1;
+        const uint8_t* blk = w + b * kQ5KBytes;
+        const uint4 hd = *reinterpret_cast<const uint4*>(blk);
+        uint32_t sc, m;
+        k4_scale_min(hd.y, hd.z, hd.w, j, sc, m);
+        const double s = (double)(f16_bits_to_f32(hd.x) * (float)sc);   // fl32(d*sc), widened exactly
+        const double t = (double)(f16_bits_to_f32(hd.x >> 16) * (float)m);
+        const uint2 qq = *reinterpret_cast<const uint2*>(blk + 48 + 32 * g + i);
+        const uint2 hh = *reinterpret_cast<const uint2*>(blk + 16 + i);
+        const uint32_t sh = (j & 1) ? 4u : 0u;
+        const uint32_t qw[2] = {qq.x, qq.y}, hw[2] = {hh.x, hh.y};
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t q = ((qw[p] >> sh) & 0x0F0F0F0Fu) | (((hw[p] >> j) & 0x01010101u) << 4);   // q4 + 16*bit
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[4 * p + c] = (float)(s * (double)((q >> (8 * c)) & 0xFFu) - t);
+        }
+    }
+};
+
+struct DecQ6K {
+    static constexpr int E = 4;
+    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[4]) {
+        const int64_t b = e0 / kQKElems;
+        const int o = (int)(e0 % kQKElems);
+        const int h = o >> 7, k = (o >> 5) & 3, l = o & 31;   // element 128h + 32k + l
+        const uint8_t* blk = w + b * kQ6KBytes;
+        uint32_t nib = ld_u32_a2(blk + 64 * h + 32 * (k & 1) + l);
+        nib = ((k >= 2) ? (nib >> 4) : nib) & 0x0F0F0F0Fu;
+        const uint32_t hb = (ld_u32_a2(blk + 128 + 32 * h + l) >> (2 * k)) & 0x03030303u;
+        const uint32_t q = nib | (hb << 4);
+        const int sc = (int)(int8_t)blk[192 + 8 * h + (l >> 4) + 2 * k];
+        const float s = f16_bits_to_f32(ld_u16(blk + 208)) * (float)sc;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = s * (ub(q, c) - 32.0f);
+    }
+};
+
+struct DecQ80 {
+    static constexpr int E = 4;
+    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[4]) {
+        const int64_t b = e0 / kQ80Elems;
+        const int o = (int)(e0 % kQ80Elems);
+        const uint8_t* blk = w + b * kQ80Bytes;
+        const float d = f16_bits_to_f32(ld_u16(blk));
+        const uint32_t q = ld_u32_a2(blk + 2 + o);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = (float)(int)(int8_t)((q >> (8 * c)) & 0xFFu) * d;
+    }
+};
+
+struct DecQ10 {
+    static constexpr int E = 4;
+    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[4]) {
+        const int64_t b = e0 / kQ10Elems;
+        const int o = (int)(e0 % kQ10Elems);
+        const uint8_t* blk = w + b * kQ10Bytes;
+        const float d = f16_bits_to_f32(ld_u16(blk));
+        const uint32_t bits = (uint32_t)blk[2 + (o >> 3)] >> (o & 7);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = ((bits >> c) & 1u) ? d : -d;
+    }
+};
 
 // Q4_0 / Q5_0 / Q5_1: 32-element blocks; byte j of qs holds element j in its
 // low nibble and element j + 16 in its high nibble; for Q5_x the 5th bit of
 // element j (j < 16) is bit j of the little-endian qh word and of element
-// j + 16 bit j + 16. A thread's four outputs are four consecutive elements of
-// one half: bytes 4p .. 4p+3 of qs (p = offset / 4 within the half).
+// j + 16 bit j + 16. Four outputs are four consecutive elements of one half:
+// bytes 4p .. 4p+3 of qs (p = offset / 4 within the half).
 template <int BB, int QS_OFF, bool FIVE, bool MIN>
-__global__ void __launch_bounds__(256) dequant_q32_kernel(const uint8_t* __restrict__ w, float* __restrict__ y,
-                                                          int64_t n) {
-    const int64_t e0 = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
-    if (e0 >= n) return;
-    const int64_t b = e0 / 32;
-    const int o = (int)(e0 % 32);
-    const int half = o >> 4, j0 = o & 15;
-    const uint8_t* blk = w + b * BB;
-    const float d = f16_bits_to_f32(ld_u16(blk));
-    const uint32_t qs = ld_u32_a2(blk + QS_OFF + j0);
-    uint32_t qh = 0;
-    if constexpr (FIVE) qh = ld_u32_a2(blk + (MIN ? 4 : 2)) >> (16 * half + j0);
-    float v[4];
+struct DecQ32 {
+    static constexpr int E = 4;
+    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[4]) {
+        const int64_t b = e0 / 32;
+        const int o = (int)(e0 % 32);
+        const int half = o >> 4, j0 = o & 15;
+        const uint8_t* blk = w + b * BB;
+        const float d = f16_bits_to_f32(ld_u16(blk));
+        const uint32_t qs = ld_u32_a2(blk + QS_OFF + j0);
+        uint32_t qh = 0;
+        if constexpr (FIVE) qh = ld_u32_a2(blk + (MIN ? 4 : 2)) >> (16 * half + j0);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        uint32_t q = (qs >> (8 * c + 4 * half)) & 15u;
-        if constexpr (FIVE) q |= ((qh >> c) & 1u) << 4;
-        if constexpr (MIN) {
-            const float m = f16_bits_to_f32(ld_u16(blk + 2));
-            v[c] = d * (float)q + m;
-        } else {
-            v[c] = (float)((int)q - (FIVE ? 16 : 8)) * d;
+        for (int c = 0; c < 4; ++c) {
+            uint32_t q = (qs >> (8 * c + 4 * half)) & 15u;
+            if constexpr (FIVE) q |= ((qh >> c) & 1u) << 4;
+            if constexpr (MIN) {
+                const float m = f16_bits_to_f32(ld_u16(blk + 2));
+                v[c] = d * (float)q + m;
+            } else {
+                v[c] = (float)((int)q - (FIVE ? 16 : 8)) * d;
+            }
         }
     }
-    store4(y, e0, n, v[0], v[1], v[2], v[3]);
+};
+
+// Outputs per thread: the decoder's E for fp32 (one 16-byte store per four);
+// eight for fp16 (two 4-output decodes, one 16-byte store).
+template <typename Dec, typename T>
+constexpr int per_thread() {
+    return (sizeof(T) == 2 || Dec::E == 8) ? 8 : 4;
+}
+
+template <typename Dec, typename T>
+__global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict__ w, T* __restrict__ y, int64_t n) {
+    constexpr int P = per_thread<Dec, T>();
+    const int64_t e0 = P * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    if (e0 >= n) return;
+    if constexpr (P == 8) {
+        float v[8];
+        if constexpr (Dec::E == 8) {
+            Dec::decode(w, e0, v);
+        } else {
+            float a[4], b[4];
+            Dec::decode(w, e0, a);
+            Dec::decode(w, e0 + 4, b);   // e0 + 4 < the allocated elements (see above)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                v[c] = a[c];
+                v[4 + c] = b[c];
+            }
+        }
+        store8(y, e0, n, v);
+    } else {
+        float v[4];
+        Dec::decode(w, e0, v);
+        store4(y, e0, n, v[0], v[1], v[2], v[3]);
+    }
 }
 
 __global__ void __launch_bounds__(256) fill_kernel(float* __restrict__ y, float v, int64_t n) {
@@ -241,24 +321,36 @@ hipError_t launch_read_xor(const void* src, int64_t bytes, uint32_t* out, hipStr
     return hipGetLastError();
 }
 
-hipError_t launch_dequant(int qtype, const uint8_t* w, float* y, int64_t n, hipStream_t stream) {
+template <typename Dec, typename T>
+void go_dequant(const uint8_t* w, T* y, int64_t n, hipStream_t stream) {
+    constexpr int P = per_thread<Dec, T>();
+    const int64_t threads = (n + P - 1) / P;
+    dequant_kernel<Dec, T><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream>>>(w, y, n);
+}
+
+template <typename T>
+hipError_t launch_dequant_t(int qtype, const uint8_t* w, T* y, int64_t n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    const int64_t threads = (n + 3) / 4;
-    const dim3 block(256);
-    const dim3 grid((unsigned)((threads + 255) / 256));
-    const dim3 grid8((unsigned)(((n + 7) / 8 + 255) / 256));   // Q4_K, Q5_K: eight outputs per thread
     switch (qtype) {
-        case kTypeQ4K: dequant_q4_k_kernel<<<grid8, block, 0, stream>>>(w, y, n); break;
-        case kTypeQ5K: dequant_q5_k_kernel<<<grid8, block, 0, stream>>>(w, y, n); break;
-        case kTypeQ6K: dequant_q6_k_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
-        case kTypeQ80: dequant_q8_0_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
-        case kTypeQ10: dequant_q1_0_kernel<<<grid, block, 0, stream>>>(w, y, n); break;
-        case kTypeQ40: dequant_q32_kernel<kQ40Bytes, 2, false, false><<<grid, block, 0, stream>>>(w, y, n); break;
-        case kTypeQ50: dequant_q32_kernel<kQ50Bytes, 6, true, false><<<grid, block, 0, stream>>>(w, y, n); break;
-        case kTypeQ51: dequant_q32_kernel<kQ51Bytes, 8, true, true><<<grid, block, 0, stream>>>(w, y, n); break;
+        case kTypeQ4K: go_dequant<DecQ4K>(w, y, n, stream); break;
+        case kTypeQ5K: go_dequant<DecQ5K>(w, y, n, stream); break;
+        case kTypeQ6K: go_dequant<DecQ6K>(w, y, n, stream); break;
+        case kTypeQ80: go_dequant<DecQ80>(w, y, n, stream); break;
+        case kTypeQ10: go_dequant<DecQ10>(w, y, n, stream); break;
+        case kTypeQ40: go_dequant<DecQ32<kQ40Bytes, 2, false, false>>(w, y, n, stream); break;
+        case kTypeQ50: go_dequant<DecQ32<kQ50Bytes, 6, true, false>>(w, y, n, stream); break;
+        case kTypeQ51: go_dequant<DecQ32<kQ51Bytes, 8, true, true>>(w, y, n, stream); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_dequant(int qtype, const uint8_t* w, float* y, int64_t n, hipStream_t stream) {
+    return launch_dequant_t(qtype, w, y, n, stream);
+}
+
+hipError_t launch_dequant_f16(int qtype, const uint8_t* w, uint16_t* y, int64_t n, hipStream_t stream) {
+    return launch_dequant_t(qtype, w, y, n, stream);
 }
 
 }  // namespace frq

@@ -41,6 +41,8 @@ constexpr int kReadXorWords = 2048;
 hipError_t launch_read_xor(const void* src, int64_t bytes, uint32_t* out, hipStream_t stream);
 
 hipError_t launch_dequant(int qtype, const uint8_t* w, float* y, int64_t n_elems, hipStream_t stream);
+// The same values rounded to fp16 (nearest even), stored as fp16 bit patterns.
+hipError_t launch_dequant_f16(int qtype, const uint8_t* w, uint16_t* y, int64_t n_elems, hipStream_t stream);
 
 // y[n] = W[n, k] . x[k] with fp32 accumulation. `plan` may be pre-filled
 // (cpl/rows_per_wg/unroll > 0) to override the heuristic; on return it holds

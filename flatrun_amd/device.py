@@ -341,6 +341,14 @@ def dequant(qtype, w, y, n_elems: int, stream=None, w_bytes: int | None = None) 
     check(lib().frq_dev_dequant(q, _addr(w), wb, int(n_elems), _addr(y), _stream(stream)))
 
 
+def dequant_f16(qtype, w, y, n_elems: int, stream=None, w_bytes: int | None = None) -> None:
+    """y[:n_elems] = fp16 bit patterns of dequant(w), rounded to nearest even
+    (enqueued)."""
+    q = qtype_id(qtype)
+    wb = _nbytes(w) if w_bytes is None else int(w_bytes)
+    check(lib().frq_dev_dequant_f16(q, _addr(w), wb, int(n_elems), _addr(y), _stream(stream)))
+
+
 def silu_mul(gateup, out, rows: int, inter: int, ld_in: int = 0, ld_out: int = 0, stream=None) -> None:
     """out[r, :inter] = silu(gate) * up for the grouped gate|up rows of
     gateup (gate first; rows ld_in floats apart, default 2 inter; out rows

@@ -94,6 +94,12 @@ int frq_dequant_q6_k(const uint8_t* weight, size_t weight_bytes, int64_t out_dim
  * Q5_K and Q1_0 formats the native module lacks. */
 int frq_dequant(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, float* out);
 
+/* The same decode with float16 output (fp16 bit patterns in `out`):
+ * dequant_handle's default dtype, loader.py:51-88, whose decoders fill an
+ * fp32 array that _finish casts with astype (gguf.py:61-73): each fp32
+ * value rounded once to nearest even, overflow to inf, subnormals kept. */
+int frq_dequant_f16(int qtype, const uint8_t* weight, size_t weight_bytes, int64_t n_elems, uint16_t* out);
+
 /* matmul_q4_k(x[k], weight, n, k) -> out[n]. _C.cpp:99-132. */
 int frq_matmul_q4_k(const float* x, size_t x_len, const uint8_t* weight, size_t weight_bytes, size_t n, size_t k,
                     float* out);
@@ -127,6 +133,8 @@ int frq_matmul(int qtype, const float* x, size_t seq, const uint8_t* weight, siz
 
 /* y[n_elems] = dequant(w). Same numerics as frq_dequant. */
 int frq_dev_dequant(int qtype, const void* w, size_t w_bytes, int64_t n_elems, float* y, void* stream);
+/* y[n_elems] = fp16(dequant(w)). Same numerics as frq_dequant_f16; y 2-byte aligned. */
+int frq_dev_dequant_f16(int qtype, const void* w, size_t w_bytes, int64_t n_elems, uint16_t* y, void* stream);
 
 /* y[b, n] = W[n, k] . x[b, k] for b < batch: the decode matvec of
  * matmul_<q> / matmul_<q>_batched (_C.cpp:99-283) on device buffers.
