@@ -1288,6 +1288,9 @@ hipError_t launch_q80_ring(int ring, int rows, int waves, int64_t grid, const ui
 // Q1_0 ring kernel: work unit 8 in GemvPlan::cpl (4 lanes per block, 32
 // elements each); needs a 4-byte aligned weight base and an even block count.
 constexpr int kQ10RingUnit = 8;
+// Q1_0 on the matrix cores (frq_gemv_mx.hip): work unit 16; GemvPlan::unroll
+// is the blocks per wavefront, rows_per_wg the rows per workgroup (<= 16).
+constexpr int kQ10MxUnit = 16;
 
 bool q10_ring_ok(const uint8_t* w, int64_t nb) {
     return (reinterpret_cast<uintptr_t>(w) & 3) == 0 && nb % 2 == 0 && nb * 4 <= 1024;
@@ -1377,6 +1380,15 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
         return launch_q6k_ring(p.unroll, p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
     }
     if (qtype == kTypeQ6K && p.cpl == kQ6KRingUnit) return hipErrorInvalidValue;   // layout not eligible
+    if (qtype == kTypeQ10 && (p.cpl == kQ10MxUnit || (p.cpl <= 0 && gemv_q10_mx_default(w, n, k)))) {
+        p.cpl = kQ10MxUnit;
+        if (!gemv_q10_mx_ok(w, k)) return hipErrorInvalidValue;   // layout not eligible
+        if (!plan_gemv_q10_mx(n, k, &p.unroll, &p.rows_per_wg)) return hipErrorInvalidConfiguration;
+        p.waves = (int)((nb + p.unroll - 1) / p.unroll);
+        p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
+        if (plan) *plan = p;
+        return launch_gemv_q10_mx(w, x, y, n, k, p.unroll, p.rows_per_wg, stream);
+    }
     if (qtype == kTypeQ10 && (p.cpl <= 0 || p.cpl == kQ10RingUnit) && q10_ring_ok(w, nb)) {
         p.cpl = kQ10RingUnit;
         p.waves = (int)((nb * 4 + 63) / 64);

@@ -403,6 +403,203 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
     }
 }
 
+// ------------------------------------------------------------------ Q1_0
+// Q1_0 GEMV on the matrix cores. A row's block (18 bytes: d f16, 16 bytes of
+// sign bits, element e = bit e % 8 of byte e / 8, w = +d if set else -d,
+// gguf.py:266-299) contributes d * sum_e (+-x_e). x is written per
+// 32-element group of a block as a 30-bit fixed-point number relative to the
+// group's largest magnitude (max |x| < 2^e): m = trunc(x 2^(30-e)),
+// |m| < 2^30, as four balanced int8 digits. The matrix cores form exactly, in
+// int32, for each row, group and digit i,
+//     C_i = sum over set bits of digit_i(m)     (sign bits as 0/1 bytes)
+//     J_i = sum of digit_i(m)                    (the same A against all-ones B)
+// and the lane forms S = sum_i 256^i (2 C_i - J_i) = sum_e (+-m_e) as two
+// exact int32 halves whose fp32 sum rounds once, then adds
+// ldexp(fl(S * d), e - 30) to its fp32 sum. Truncation loses less than
+// 2^(e-30) <= 2^-29 max |x_g| per element, at most 2^-24 max |x_g| over the
+// group, and every weight has |w| = |d|, so each group is within 2^-24 of
+// its own sum |w_e x_e|; with the fp32 roundings each row keeps
+//     |y - y_exact| <= c * 2^-24 * sum_j |w_j x_j|.
+// A block whose x holds an inf or a NaN is summed weight by weight in fp32
+// (fma(+-d, x_e, acc), the dequant's weights), so those propagate.
+//
+// Mapping. A workgroup owns TR <= 16 rows (the MFMA's 16 columns) and all of
+// k; wave v owns blocks [vL, vL + L). Lane (c, g) (c = l & 15, g = l >> 4)
+// loads sign-bit dword g of row c's blocks: elements 32g .. 32g + 31, byte cc
+// holding elements 32g + 8cc + j. Its B operand for MFMA h (0, 1) is the four
+// dwords (bits >> (4h + jj)) & 0x01010101, jj = 0..3, so byte 4jj + cc is
+// element 32g + 8cc + 4h + jj. A is block diagonal: row 4g + i carries digit
+// i of the same elements of group g and zeros elsewhere, so lane (c, g) of
+// the result receives, for row c, the four digit sums of its own group; it
+// keeps its blocks' sum in one register. The digit table is wave-private LDS
+// (LDS operations of one wave complete in order, so no barrier is needed
+// between a wave's table writes and its reads); one workgroup barrier
+// precedes the per-row reduction over waves and groups, in a fixed order.
+constexpr int kQ10MxWaves = 16;
+constexpr int kQ10MxMaxL = 8;       // blocks per wave
+constexpr int kQ10TabBlock = 512;   // digit bytes per block: 2 MFMAs x 4 groups x 4 digits x 16
+
+template <int L>
+__global__ void __launch_bounds__(1024) gemv_q1_0_mx_kernel(const uint8_t* __restrict__ w,
+                                                            const float* __restrict__ x, float* __restrict__ y,
+                                                            int64_t n, int nb, int TR) {
+    constexpr int kWaveTab = L * kQ10TabBlock + 16;   // the wave's blocks, then 16 zero bytes
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kQ10MxWaves * kWaveTab];
+    __shared__ int etab[kQ10MxWaves * L * 4];
+    __shared__ float red[kQ10MxWaves * 16];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nwaves = blockDim.x >> 6;
+    const int64_t row0 = (int64_t)blockIdx.x * TR;
+    const int nrows = (int)((n - row0 < TR) ? n - row0 : TR);
+    const int b0 = wave * L;
+    const int lw = (nb - b0 < L) ? nb - b0 : L;         // >= 1: nwaves = ceil(nb / L)
+    const int c = lane & 15, g = lane >> 4;
+    const uint32_t row_bytes = (uint32_t)nb * kQ10Bytes;
+    const auto rs = buffer_rsrc(w + row0 * (int64_t)row_bytes, (uint32_t)nrows * row_bytes);
+    uint8_t* tab = lds + wave * kWaveTab;
+
+    // x first (small, cache-resident), then every weight load. Set s of the
+    // wave (4 elements): block s / 32, group (s / 8) % 4, h = (s / 4) % 2,
+    // jj = s % 4, elements 32g + 4h + jj + {0, 8, 16, 24}; lane t owns sets
+    // t + 64i (with L = 1 lanes 32..63 repeat lanes 0..31 and write nothing).
+    constexpr int kSets = L >= 2 ? L / 2 : 1;
+    float xv[kSets][4];
+    {
+        const auto xs = buffer_rsrc(x, (uint32_t)nb * kQ10Elems * 4u);
+#pragma unroll
+        for (int i = 0; i < kSets; ++i) {
+            const int s = L == 1 ? (lane & 31) : lane + 64 * i;
+            const int jb = s >> 5, gg = (s >> 3) & 3, h = (s >> 2) & 1, jj = s & 3;
+            const uint32_t blk = (uint32_t)(b0 + (jb < lw ? jb : lw - 1));
+            const uint32_t o = 4u * (__umul24(blk, kQ10Elems) + 32 * gg + 4 * h + jj);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                xv[i][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xs, (int)(o + 32 * q), 0, 0));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t wlo[L], whi[L], wd[L], wsh[L];
+    {
+        const uint32_t rofs = (uint32_t)(c < nrows ? c : nrows - 1) * row_bytes;   // extra lanes re-read a row
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            const uint32_t blk = (uint32_t)(b0 + (j < lw ? j : lw - 1));
+            const uint32_t at = __umul24(blk, kQ10Bytes) + 2 + 4 * g;   // this lane's sign-bit dword
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(rofs + (at & ~3u)), 0, 0);
+            wlo[j] = v[0];
+            whi[j] = v[1];
+            wsh[j] = 8u * (at & 3u);
+            wd[j] = bload_u16(rs, rofs + __umul24(blk, kQ10Bytes));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- x -> digits into the wave's table: 64 bytes per (block, h, group),
+    // digit d in its 16-byte slot d ^ (2h + group / 2), dword jj of the slot.
+    // The swizzle puts the 32 lanes of a half-wave's write (h, group, jj) on
+    // 32 different banks; a reader's 16 bytes stay contiguous.
+    if (lane < 4) reinterpret_cast<uint32_t*>(tab + L * kQ10TabBlock)[lane] = 0u;
+    uint32_t inexact = 0;                                // bit j: block j holds an inf or a NaN
+#pragma unroll
+    for (int i = 0; i < kSets; ++i) {
+        const int s = L == 1 ? (lane & 31) : lane + 64 * i;
+        const int jb = s >> 5, gg = (s >> 3) & 3, h = (s >> 2) & 1, jj = s & 3;
+        uint32_t mx = 0;                                 // max |x| as bits; >= 0x7F800000 for inf / NaN
+#pragma unroll
+        for (int q = 0; q < 4; ++q) mx = max(mx, __float_as_uint(xv[i][q]) & 0x7FFFFFFFu);
+        mx = max(mx, dpp_u<0xB1>(mx));                   // quad_perm [1,0,3,2]
+        mx = max(mx, dpp_u<0x4E>(mx));                   // quad_perm [2,3,0,1]
+        mx = max(mx, dpp_u<0x141>(mx));                  // row_half_mirror: the group's 8 lanes
+        const bool bad = mx >= 0x7F800000u;
+        const int e = bad ? 0 : __builtin_amdgcn_frexp_expf(__uint_as_float(mx));
+        int m[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) m[q] = cvt_i32_sat(__builtin_ldexpf(xv[i][q], 30 - e));
+        uint32_t dg[4];
+        balanced_digits(m[0], m[1], m[2], m[3], dg);
+        if (L > 1 || lane < 32) {
+            uint8_t* p = tab + ((jb * 2 + h) * 4 + gg) * 64 + 4 * jj;
+            const int t = 2 * h + (gg >> 1);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) *reinterpret_cast<uint32_t*>(p + 16 * (d ^ t)) = dg[d];
+            if ((s & 7) == 0) etab[(wave * L + jb) * 4 + gg] = e - 30;
+        }
+        const uint64_t bl = __builtin_amdgcn_ballot_w64(bad);
+        if constexpr (L == 1) {
+            if (bl) inexact |= 1u;
+        } else {
+            if (bl & 0xFFFFFFFFull) inexact |= 1u << (2 * i);
+            if (bl >> 32) inexact |= 1u << (2 * i + 1);
+        }
+    }
+    __asm__ volatile("" ::: "memory");                   // table writes stay before the reads
+
+    // ---- products. Lane (ar = l & 15, akk = l >> 4) of A carries digit ar % 4
+    // of group akk when ar / 4 == akk, else the zero bytes. Every block's A
+    // operands and exponents are read at once, and the blocks run without
+    // branches (a block past the wave's range gets d = 0), so their LDS
+    // reads, MFMAs and epilogues overlap.
+    const int ar = lane & 15, akk = lane >> 4;
+    const bool diag = (ar >> 2) == akk;
+    const uint8_t* zero = tab + L * kQ10TabBlock;
+    const uint8_t* abase0 = diag ? tab + akk * 64 + ((ar & 3) ^ (akk >> 1)) * 16 : zero;
+    const uint8_t* abase1 = diag ? tab + 256 + akk * 64 + ((ar & 3) ^ (2 + (akk >> 1))) * 16 : zero;
+    const uint32_t astep = diag ? 512u : 0u;            // per block
+    float acc = 0.0f;
+    if (inexact == 0) {                                  // wave-uniform
+        const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+        const i32x4 z = {0, 0, 0, 0};
+        constexpr uint32_t M = 0x01010101u;
+        i32x4 A[L][2];
+        int eo[L];
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            A[j][0] = *reinterpret_cast<const i32x4*>(abase0 + j * astep);
+            A[j][1] = *reinterpret_cast<const i32x4*>(abase1 + j * astep);
+            eo[j] = etab[(wave * L + j) * 4 + g];
+        }
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            const uint32_t bits = __builtin_amdgcn_alignbit(whi[j], wlo[j], wsh[j]);
+            const float d = j < lw ? f16_bits_to_f32(wd[j]) : 0.0f;
+            const i32x4 B0 = {(int)(bits & M), (int)((bits >> 1) & M), (int)((bits >> 2) & M),
+                              (int)((bits >> 3) & M)};
+            const i32x4 B1 = {(int)((bits >> 4) & M), (int)((bits >> 5) & M), (int)((bits >> 6) & M),
+                              (int)((bits >> 7) & M)};
+            i32x4 C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[j][0], B0, z, 0, 0, 0);
+            C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[j][1], B1, C, 0, 0, 0);
+            i32x4 J = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[j][0], ones, z, 0, 0, 0);
+            J = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[j][1], ones, J, 0, 0, 0);
+            // |C_i|, |J_i| <= 32 * 128: both halves below 2^22, exact in fp32
+            const int p01 = 2 * ((C[1] << 8) + C[0]) - ((J[1] << 8) + J[0]);
+            const int p23 = 2 * ((C[3] << 8) + C[2]) - ((J[3] << 8) + J[2]);
+            const float v = __builtin_fmaf((float)p23, 65536.0f, (float)p01);
+            acc += __builtin_ldexpf(v * d, eo[j]);
+        }
+    } else {                                             // an inf or NaN in the wave's x: weight by weight
+        for (int j = 0; j < lw; ++j) {
+            const uint32_t bits = __builtin_amdgcn_alignbit(whi[j], wlo[j], wsh[j]);
+            const float d = f16_bits_to_f32(wd[j]);
+            const float* xg = x + (int64_t)(b0 + j) * kQ10Elems + 32 * g;
+            float sacc = 0.0f;
+#pragma unroll 1
+            for (int e = 0; e < 32; ++e) sacc = __builtin_fmaf(((bits >> e) & 1u) ? d : -d, xg[e], sacc);
+            acc += sacc;
+        }
+    }
+    // row c: (g0 + g1) + (g2 + g3) in the wave, then the waves in order
+    acc += __shfl_xor(acc, 16, 64);
+    acc += __shfl_xor(acc, 32, 64);
+    if (lane < 16) red[wave * 16 + lane] = acc;
+    __syncthreads();
+    if (tid < nrows) {
+        float s = 0.0f;
+        for (int wv = 0; wv < nwaves; ++wv) s += red[wv * 16 + tid];
+        y[row0 + tid] = s;
+    }
+}
+
 template <int LMAX, int RT, int KS>
 void mx_go(bool hb, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, uint64_t* slots,
            int64_t n, int nb, int L, int TR) {
@@ -494,6 +691,61 @@ hipError_t launch_gemv_mx(const uint8_t* w, const float* x, float* y, int64_t n,
         ok = p.tiles == 1 ? mx_by_l<1, 2>(p.blocks, hb, g, b, stream, w, x, y, slots, n, nb, p.rows)
                           : mx_by_l<2, 2>(p.blocks, hb, g, b, stream, w, x, y, slots, n, nb, p.rows);
     if (!ok) return hipErrorInvalidConfiguration;
+    return hipGetLastError();
+}
+
+bool gemv_q10_mx_ok(const uint8_t* w, int64_t k) {
+    if (k <= 0 || k % kQ10Elems) return false;
+    const int64_t nb = k / kQ10Elems;
+    // 4-byte aligned sign-bit windows: an aligned base and an even block count
+    return (reinterpret_cast<uintptr_t>(w) & 3) == 0 && nb % 2 == 0 && nb <= kQ10MxWaves * kQ10MxMaxL;
+}
+
+bool gemv_q10_mx_default(const uint8_t* w, int64_t n, int64_t k) {
+    // Measured against the element-wise ring kernel (graph-replayed launches):
+    // the matrix cores win while one round of workgroups covers the rows and
+    // each workgroup's x split stays short (k <= 4096): 4096 x 4096 4.17 vs
+    // 4.76 us, 3072 x 4096 3.94 vs 5.30, 4096 x 1024 2.79 vs 3.64,
+    // 6144 x 2048 4.00 vs 4.53. They lose for k = 8192 (4096 x 8192 6.52 vs
+    // 6.49, 1024 x 8192 4.89 vs 3.66), below ~1024 rows (512 x 4096 3.42 vs
+    // 3.04) and for several rounds at k = 4096 (14336 x 4096 8.6 vs 7.5).
+    if (!gemv_q10_mx_ok(w, k) || n < 1024) return false;
+    const int64_t nb = k / kQ10Elems;
+    return nb <= 32 && (n <= 4096 || (nb <= 16 && n <= 6144));
+}
+
+bool plan_gemv_q10_mx(int64_t n, int64_t k, int* L, int* TR) {
+    if (n <= 0 || k <= 0 || k % kQ10Elems) return false;
+    const int64_t nb = k / kQ10Elems;
+    if (*L <= 0) {
+        *L = 2;
+        while (*L < kQ10MxMaxL && (nb + *L - 1) / *L > 8) *L *= 2;
+    }
+    if (*L != 1 && *L != 2 && *L != 4 && *L != 8) return false;
+    if ((nb + *L - 1) / *L > kQ10MxWaves) return false;
+    if (*TR <= 0) {
+        const int64_t t = (n + 255) / 256;             // one round of 256 workgroups while rows allow
+        *TR = (int)(t > 16 ? 16 : t);
+    }
+    return *TR >= 1 && *TR <= 16;
+}
+
+hipError_t launch_gemv_q10_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int L, int TR,
+                              hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    if (!gemv_q10_mx_ok(w, k)) return hipErrorInvalidValue;
+    if (L <= 0 || TR <= 0 || !plan_gemv_q10_mx(n, k, &L, &TR)) return hipErrorInvalidConfiguration;
+    const int nb = (int)(k / kQ10Elems);
+    const int64_t grid = (n + TR - 1) / TR;
+    if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    const dim3 gd((unsigned)grid), bd((unsigned)(64 * ((nb + L - 1) / L)));
+    switch (L) {
+        case 1: gemv_q1_0_mx_kernel<1><<<gd, bd, 0, stream>>>(w, x, y, n, nb, TR); break;
+        case 2: gemv_q1_0_mx_kernel<2><<<gd, bd, 0, stream>>>(w, x, y, n, nb, TR); break;
+        case 4: gemv_q1_0_mx_kernel<4><<<gd, bd, 0, stream>>>(w, x, y, n, nb, TR); break;
+        case 8: gemv_q1_0_mx_kernel<8><<<gd, bd, 0, stream>>>(w, x, y, n, nb, TR); break;
+        default: return hipErrorInvalidConfiguration;
+    }
     return hipGetLastError();
 }
 

@@ -78,6 +78,18 @@ bool gemv_mx_eligible(int qtype, const uint8_t* w, const float* x, int64_t n, in
 hipError_t launch_gemv_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, const MxPlan& plan,
                           uint64_t* slots, hipStream_t stream);
 
+// Q1_0 GEMV on the matrix cores (frq_gemv_mx.hip), batch 1: a workgroup owns
+// TR <= 16 rows and all of k, each wavefront L (1, 2, 4 or 8) consecutive
+// 128-element blocks, at most 16 wavefronts. w 4-byte aligned with an even
+// block count (gemv_q10_mx_ok). plan_gemv_q10_mx fills L / TR left <= 0 and
+// checks them.
+bool gemv_q10_mx_ok(const uint8_t* w, int64_t k);
+// The default path's choice between this kernel and the element-wise ring.
+bool gemv_q10_mx_default(const uint8_t* w, int64_t n, int64_t k);
+bool plan_gemv_q10_mx(int64_t n, int64_t k, int* L, int* TR);
+hipError_t launch_gemv_q10_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int L, int TR,
+                              hipStream_t stream);
+
 // Grouped GEMV: y_i[n_i] = W_i[n_i, k] . x[k] for up to kGemvGroupMax
 // matrices sharing x (q/k/v, gate/up), in ONE launch when every W_i is Q4_K
 // (16-byte aligned) or Q6_K (4-byte aligned, even block count) and 8 lanes

@@ -211,7 +211,10 @@ int frq_dev_gemv_noalloc(int qtype, const void* w, size_t w_bytes, const float* 
  *                 wavefront's blocks in one load per row, shared across
  *                 lanes with ds_bpermute). AUTO takes the kernel
  *                 frq_dev_gemv takes.
- *   cpl           work unit per lane (format specific)
+ *   cpl           work unit per lane (format specific); with ROWS and
+ *                 Q1_0, 16 selects the matrix-core Q1_0 kernel (`rows` <=
+ *                 16 per workgroup, `unroll` = 128-element blocks per
+ *                 wavefront: 1, 2, 4 or 8)
  *   rows          rows per work item (SPLITK) / per workgroup (ROWS)
  *   unroll        rows per load batch
  *   slices        K-slices per row: output for SPLITK; 1 for the ROWS
