@@ -276,14 +276,17 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
     // ---- x -> digits. Lane t: x[4t .. 4t+3] of the block = sub-block s = t / 8,
     // half h = (t / 4) % 2, bytes 4 (t % 4) .. +3 of the 16-element group.
     // MFMA m = 2 (s / 4) + s % 2 (load s / 4, low or high nibbles) reads the
-    // group in k-group kk = 2 ((s / 2) % 2) + h; table row (m, kk, digit)
-    // holds 16 bytes. The exponent table is ordered [p][position], with
-    // p = (s / 2) % 2 and position (s % 2) + 2 (s / 4).
+    // group in k-group kk = 2 ((s / 2) % 2) + h; the 128 bytes of (m, kk) hold
+    // its eight digits, digit d in 16-byte slot d ^ (2 kk + m % 2): the 32
+    // lanes of a half-wave writing one digit then cover 32 different banks
+    // (without the swizzle, 4). The exponent table is ordered [p][position],
+    // with p = (s / 2) % 2 and position (s % 2) + 2 (s / 4).
     uint32_t inexact = 0;                                // bit j: block j of this wave is not exact
     {
         const int s = lane >> 3, h = (lane >> 2) & 1;
         const int m = 2 * (s >> 2) + (s & 1), kk = 2 * ((s >> 1) & 1) + h;
         uint8_t* wl = lds + wave * kWaveTab + (m * 4 + kk) * 128 + 4 * (lane & 3);
+        const int sw = (2 * kk + (m & 1)) & 7;
         const int pos = (s & 1) + 2 * (s >> 2), pp = (s >> 1) & 1;
         int* we = etab + wave * LMAX * kSubTab + 4 * pp + pos;
 #pragma unroll
@@ -291,7 +294,7 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
             const XSplit dg = x_split(xv[j]);
             uint8_t* p = wl + j * kTabBlock;
 #pragma unroll
-            for (int dd = 0; dd < 8; ++dd) *reinterpret_cast<uint32_t*>(p + 16 * dd) = dg.d[dd];
+            for (int dd = 0; dd < 8; ++dd) *reinterpret_cast<uint32_t*>(p + 16 * (dd ^ sw)) = dg.d[dd];
             if ((lane & 7) == 0) we[j * kSubTab] = dg.eo;
             if (__builtin_amdgcn_ballot_w64(!dg.exact) != 0) inexact |= 1u << j;
         }
@@ -314,8 +317,11 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
     // zeros otherwise; the digit table and the zero block are read at the
     // same per-MFMA offsets.
     const int ar = lane & 15, akk = lane >> 4;
-    const uint8_t* abase = ((ar >> 3) == (akk >> 1)) ? lds + wave * kWaveTab + (akk * 8 + (ar & 7)) * 16
-                                                     : lds + kTabAll;
+    // (the digit of row ar sits in slot (ar % 8) ^ (2 akk + m % 2) of (m, akk))
+    const bool diag = (ar >> 3) == (akk >> 1);
+    const uint8_t* abase_e = diag ? lds + wave * kWaveTab + akk * 128 + ((ar & 7) ^ (2 * akk)) * 16 : lds + kTabAll;
+    const uint8_t* abase_o = diag ? lds + wave * kWaveTab + akk * 128 + ((ar & 7) ^ (2 * akk + 1)) * 16
+                                  : lds + kTabAll;
     const int p = g >> 1, lev = g & 1;
     const int* eb = etab + wave * LMAX * kSubTab + 4 * p;
     const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
@@ -332,7 +338,8 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
             for (int t = 0; t < RT; ++t) acc[t] += (double)block_per_weight(hd[t][j], q0[t][j], q1[t][j], xb, g);
             continue;
         }
-        const uint8_t* ab = abase + j * kTabBlock;
+        const uint8_t* ab_e = abase_e + j * kTabBlock;
+        const uint8_t* ab_o = abase_o + j * kTabBlock;
         const int4 te = *reinterpret_cast<const int4*>(eb + j * kSubTab);          // exponents - 30
         const int el = lev ? -30 : 0;                                              // level 2 carries 2^-30
         double dt[RT], dmt[RT];
@@ -350,7 +357,7 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
         // m = (W >> 4) | (Z >> 6) << 4 for the last two).
         static_for<0, 4>([&](auto kc) {
             constexpr int k = decltype(kc)::value;
-            const i32x4 A = *reinterpret_cast<const i32x4*>(ab + 512 * k);
+            const i32x4 A = *reinterpret_cast<const i32x4*>((k & 1 ? ab_o : ab_e) + 512 * k);
             // sum(m) of this lane's level for the sub-block, exact: the same A
             // against all-ones B (independent of the row, so once per block)
             const i32x4 z = {0, 0, 0, 0};
