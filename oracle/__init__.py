@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY. Nothing in the shipped package (``flatrun_amd``)
 imports this package. Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import, call or link anything under
-``oracle/``, and only as the checker or the CPU baseline, never as the thing
-measured or shipped.
+``oracle/``, and only to check results or as the CPU baseline, never as the
+thing measured or shipped.
 
 Contents
 --------
