@@ -329,10 +329,10 @@ def test_resident_weights_match_host_path(backend):
 
 
 def test_graph_replay_matches_eager(frq):
-    """A captured sequence of GEMVs (three formats, k = 0 fill included)
+    """A captured sequence of GEMVs (four formats, k = 0 fill included)
     replays to the eager bits every time, with eager work and host syncs
     between the replays."""
-    cases = [("Q4_K", 3584, 9472), ("Q6_K", 300, 3584), ("Q8_0", 500, 896), ("Q4_K", 7, 0)]
+    cases = [("Q4_K", 3584, 9472), ("Q6_K", 300, 3584), ("Q8_0", 500, 896), ("Q1_0", 4096, 4096), ("Q4_K", 7, 0)]
     s = device.Stream()
     bufs = []
     for i, (q, n, k) in enumerate(cases):

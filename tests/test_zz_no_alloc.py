@@ -55,6 +55,7 @@ def _case(q, n, k, batch, seed, stream):
     ("Q4_K", [(300, 33024, 1), (100, 33024, 1)]),       # k > 32768: split-K partials
     ("Q6_K", [(1024, 4096, 1), (512, 4096, 1)]),        # no scratch
     ("Q8_0", [(4864, 896, 1), (1000, 896, 1)]),
+    ("Q1_0", [(4096, 4096, 1), (2048, 4096, 2)]),       # Q1_0 on the matrix cores: no scratch
 ])
 def test_noalloc_equals_dev_gemv_two_calls(frq, q, shapes):
     s = device.Stream()
