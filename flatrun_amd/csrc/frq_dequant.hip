@@ -16,9 +16,8 @@
 // products above is fused into the following add.
 //
 // Work mapping: one thread writes four consecutive fp32 outputs (one
-// dwordx4 store; eight, in two stores, for Q4_K and Q5_K), so a wavefront
-// writes 1-2 KiB of contiguous fp32; the kernel is bound by the 4 B/element
-// write stream. With fp16 output every thread writes eight (one dwordx4
+// dwordx4 store), so each store instruction of a wavefront writes 1 KiB of
+// contiguous fp32; the kernel is bound by the 4 B/element write stream. With fp16 output every thread writes eight (one dwordx4
 // store of 2 B elements: two four-output decodes for the other formats).
 // Four outputs always share one scale, so each decode reads one scale pair.
 // A ragged last block (element count not a multiple of the block) is decoded
@@ -89,54 +88,85 @@ __device__ __forceinline__ void store8(uint16_t* __restrict__ y, int64_t e0, int
 
 __device__ __forceinline__ float ub(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
 
-// Decoders: v = the elements e0 .. e0 + E - 1 (E = 8 for Q4_K / Q5_K, whose
-// eight share one sub-block, else 4), all inside the allocated blocks for
-// any e0 < n that is a multiple of 8 (every block holds a multiple of 8
-// elements).
+// k4_scale_min for a pair index j that differs between the lanes of a wave:
+// both forms computed and one selected, so no branch stands between the
+// block's loads and the whole 16-byte header stays one load.
+__device__ __forceinline__ void k4_scale_min_sel(uint32_t s0, uint32_t s1, uint32_t s2, int j, uint32_t& sc,
+                                                 uint32_t& m) {
+    const uint32_t b = 8u * (uint32_t)(j & 3);
+    const uint32_t lo_sc = (s0 >> b) & 63u, lo_m = (s1 >> b) & 63u;
+    const uint32_t hi_sc = ((s2 >> b) & 15u) | (((s0 >> (b + 6)) & 3u) << 4);
+    const uint32_t hi_m = ((s2 >> (b + 4)) & 15u) | (((s1 >> (b + 6)) & 3u) << 4);
+    sc = j < 4 ? lo_sc : hi_sc;
+    m = j < 4 ? lo_m : hi_m;
+}
 
-// Q4_K and Q5_K: eight outputs, all in one 32-element sub-block, so the
-// block header is read and the scale pair decoded once per eight outputs.
+// Decoders: v = the elements e0 .. e0 + E - 1 (E = 8 for Q4_K / Q5_K with
+// fp16 output, whose eight share one sub-block, else 4), all inside the
+// allocated blocks for any e0 < n that is a multiple of the outputs per
+// thread (every block holds a multiple of 8 elements).
+
+// Q4_K and Q5_K: E = 4 or 8 outputs, all in one 32-element sub-block. fp32
+// output takes E = 4, one 16-byte store per thread, so every store
+// instruction of a wave writes 1 KiB contiguous (E = 8 with two stores per
+// thread measured 79 against 72 us for 18944 x 3584); fp16 output takes
+// E = 8, whose eight halves are one 16-byte store.
+template <int E_>
 struct DecQ4K {
-    static constexpr int E = 8;
-    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[8]) {
+    static constexpr int E = E_;
+    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[E_]) {
         const int64_t b = e0 / kQKElems;
         const int o = (int)(e0 % kQKElems);
         const int j = o >> 5, i = o & 31, g = j >> 1;
         const uint8_t* blk = w + b * kQ4KBytes;
         const uint4 hd = *reinterpret_cast<const uint4*>(blk);
         uint32_t sc, m;
-        k4_scale_min(hd.y, hd.z, hd.w, j, sc, m);
+        k4_scale_min_sel(hd.y, hd.z, hd.w, j, sc, m);
         const float s = f16_bits_to_f32(hd.x) * (float)sc;
         const float t = f16_bits_to_f32(hd.x >> 16) * (float)m;
-        const uint2 qq = *reinterpret_cast<const uint2*>(blk + 16 + 32 * g + i);
         const uint32_t sh = (j & 1) ? 4u : 0u;
-        const uint32_t q0 = (qq.x >> sh) & 0x0F0F0F0Fu, q1 = (qq.y >> sh) & 0x0F0F0F0Fu;
+        if constexpr (E_ == 8) {
+            const uint2 qq = *reinterpret_cast<const uint2*>(blk + 16 + 32 * g + i);
+            const uint32_t q0 = (qq.x >> sh) & 0x0F0F0F0Fu, q1 = (qq.y >> sh) & 0x0F0F0F0Fu;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            v[c] = s * ub(q0, c) - t;
-            v[4 + c] = s * ub(q1, c) - t;
+            for (int c = 0; c < 4; ++c) {
+                v[c] = s * ub(q0, c) - t;
+                v[4 + c] = s * ub(q1, c) - t;
+            }
+        } else {
+            const uint32_t q0 = (*reinterpret_cast<const uint32_t*>(blk + 16 + 32 * g + i) >> sh) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c] = s * ub(q0, c) - t;
         }
     }
 };
 
+template <int E_>
 struct DecQ5K {
-    static constexpr int E = 8;
-    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[8]) {
+    static constexpr int E = E_;
+    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[E_]) {
         const int64_t b = e0 / kQKElems;
         const int o = (int)(e0 % kQKElems);
         const int j = o >> 5, i = o & 31, g = j >> 1;
         const uint8_t* blk = w + b * kQ5KBytes;
         const uint4 hd = *reinterpret_cast<const uint4*>(blk);
         uint32_t sc, m;
-        k4_scale_min(hd.y, hd.z, hd.w, j, sc, m);
+        k4_scale_min_sel(hd.y, hd.z, hd.w, j, sc, m);
         const double s = (double)(f16_bits_to_f32(hd.x) * (float)sc);   // fl32(d*sc), widened exactly
         const double t = (double)(f16_bits_to_f32(hd.x >> 16) * (float)m);
-        const uint2 qq = *reinterpret_cast<const uint2*>(blk + 48 + 32 * g + i);
-        const uint2 hh = *reinterpret_cast<const uint2*>(blk + 16 + i);
         const uint32_t sh = (j & 1) ? 4u : 0u;
-        const uint32_t qw[2] = {qq.x, qq.y}, hw[2] = {hh.x, hh.y};
+        uint32_t qw[2], hw[2];
+        if constexpr (E_ == 8) {
+            const uint2 qq = *reinterpret_cast<const uint2*>(blk + 48 + 32 * g + i);
+            const uint2 hh = *reinterpret_cast<const uint2*>(blk + 16 + i);
+            qw[0] = qq.x, qw[1] = qq.y, hw[0] = hh.x, hw[1] = hh.y;
+        } else {
+            qw[0] = *reinterpret_cast<const uint32_t*>(blk + 48 + 32 * g + i);
+            hw[0] = *reinterpret_cast<const uint32_t*>(blk + 16 + i);
+            qw[1] = hw[1] = 0;
+        }
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
+        for (int p = 0; p < E_ / 4; ++p) {
             const uint32_t q = ((qw[p] >> sh) & 0x0F0F0F0Fu) | (((hw[p] >> j) & 0x01010101u) << 4);   // q4 + 16*bit
 #pragma unroll
             for (int c = 0; c < 4; ++c) v[4 * p + c] = (float)(s * (double)((q >> (8 * c)) & 0xFFu) - t);
@@ -332,8 +362,8 @@ template <typename T>
 hipError_t launch_dequant_t(int qtype, const uint8_t* w, T* y, int64_t n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     switch (qtype) {
-        case kTypeQ4K: go_dequant<DecQ4K>(w, y, n, stream); break;
-        case kTypeQ5K: go_dequant<DecQ5K>(w, y, n, stream); break;
+        case kTypeQ4K: go_dequant<DecQ4K<sizeof(T) == 2 ? 8 : 4>>(w, y, n, stream); break;
+        case kTypeQ5K: go_dequant<DecQ5K<sizeof(T) == 2 ? 8 : 4>>(w, y, n, stream); break;
         case kTypeQ6K: go_dequant<DecQ6K>(w, y, n, stream); break;
         case kTypeQ80: go_dequant<DecQ80>(w, y, n, stream); break;
         case kTypeQ10: go_dequant<DecQ10>(w, y, n, stream); break;
