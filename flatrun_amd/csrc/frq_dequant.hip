@@ -176,21 +176,27 @@ struct DecQ5K {
     }
 };
 
+// Q6_K: E = 4 (fp32 output) or 8 (fp16) consecutive elements 128h + 32k + l
+// .. + E - 1, which share one 16-element scale (l is a multiple of E).
+template <int E_>
 struct DecQ6K {
-    static constexpr int E = 4;
-    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[4]) {
+    static constexpr int E = E_;
+    __device__ static void decode(const uint8_t* __restrict__ w, int64_t e0, float (&v)[E_]) {
         const int64_t b = e0 / kQKElems;
         const int o = (int)(e0 % kQKElems);
         const int h = o >> 7, k = (o >> 5) & 3, l = o & 31;   // element 128h + 32k + l
         const uint8_t* blk = w + b * kQ6KBytes;
-        uint32_t nib = ld_u32_a2(blk + 64 * h + 32 * (k & 1) + l);
-        nib = ((k >= 2) ? (nib >> 4) : nib) & 0x0F0F0F0Fu;
-        const uint32_t hb = (ld_u32_a2(blk + 128 + 32 * h + l) >> (2 * k)) & 0x03030303u;
-        const uint32_t q = nib | (hb << 4);
         const int sc = (int)(int8_t)blk[192 + 8 * h + (l >> 4) + 2 * k];
         const float s = f16_bits_to_f32(ld_u16(blk + 208)) * (float)sc;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[c] = s * (ub(q, c) - 32.0f);
+        for (int p = 0; p < E_ / 4; ++p) {
+            uint32_t nib = ld_u32_a2(blk + 64 * h + 32 * (k & 1) + l + 4 * p);
+            nib = ((k >= 2) ? (nib >> 4) : nib) & 0x0F0F0F0Fu;
+            const uint32_t hb = (ld_u32_a2(blk + 128 + 32 * h + l + 4 * p) >> (2 * k)) & 0x03030303u;
+            const uint32_t q = nib | (hb << 4);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[4 * p + c] = s * (ub(q, c) - 32.0f);
+        }
     }
 };
 
@@ -384,7 +390,7 @@ hipError_t launch_dequant_t(int qtype, const uint8_t* w, T* y, int64_t n, hipStr
     switch (qtype) {
         case kTypeQ4K: go_dequant<DecQ4K<sizeof(T) == 2 ? 8 : 4>>(w, y, n, stream); break;
         case kTypeQ5K: go_dequant<DecQ5K<sizeof(T) == 2 ? 8 : 4>>(w, y, n, stream); break;
-        case kTypeQ6K: go_dequant<DecQ6K>(w, y, n, stream); break;
+        case kTypeQ6K: go_dequant<DecQ6K<sizeof(T) == 2 ? 8 : 4>>(w, y, n, stream); break;
         case kTypeQ80: go_dequant<DecQ80>(w, y, n, stream); break;
         case kTypeQ10: go_dequant<DecQ10>(w, y, n, stream); break;
         case kTypeQ40: go_dequant<DecQ32<kQ40Bytes, 2, false, false>>(w, y, n, stream); break;
