@@ -456,7 +456,7 @@ def prefill_gemm(stream, m: int = 512, n: int = 14336, k: int = 4096, reps: int 
     return out
 
 
-def batched_f32(stream, q: str = "Q4_K", n: int = 3584, k: int = 18944, seqs=(4, 32, 512),
+def batched_f32(stream, q: str = "Q4_K", n: int = 3584, k: int = 18944, seqs=(2, 4, 32, 512),
                 cpu_baseline_on: bool = True) -> dict:
     """The fp32 batched matvec (frq_dev_gemv with batch = seq rows of x), the
     shape of the reference CLI's re-prefill: every generated token multiplies
@@ -465,8 +465,9 @@ def batched_f32(stream, q: str = "Q4_K", n: int = 3584, k: int = 18944, seqs=(4,
     rows. Per seq: mean launch time over a graph-replayed region (weight
     copies rotated past the Infinity Cache), effective GB/s (W once + x + y),
     GFLOP/s (2 seq n k), and the time of seq single-row launches for
-    comparison; cpu: the reference's native batched matmul (1 thread) on 2
-    rows, scaled to seq."""
+    comparison (two to six rows run the small-M matvec, W read once per two
+    or three rows); cpu: the reference's native batched matmul (1 thread) on
+    2 rows, scaled to seq."""
     single = GemvWorkload(q, n, k, seed=300, stream=stream)
     t1 = single.time_throughput(500, warmup=200) / 500
     single.free()

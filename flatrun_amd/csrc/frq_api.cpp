@@ -255,26 +255,42 @@ void gemv_scratch_need(int qtype, const uint8_t* w, const float* x, int64_t n, i
     frq::gemv_sk_scratch(sp, n, part_bytes, &cb);
 }
 
-// Rows of x that take the fp32-contract matrix-core GEMM (W read once per
-// tile of x rows) instead of one GEMV per row: Q4_K, Q6_K and Q8_0 with two
-// or more rows.
+// Rows of x that the fp32-contract matrix-core GEMM (W read once per tile of
+// x rows) can take: Q4_K, Q6_K and Q8_0 with two or more rows.
 bool batched_gemm(int qtype, const uint8_t* w, const float* x, int64_t batch, int64_t n, int64_t k) {
     if (batch < 2 || !frq::gemm_f32_supported(qtype, batch, n, k)) return false;
     const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
     return !(reinterpret_cast<uintptr_t>(x) & 15) && !(qtype == FRQ_Q4_K ? (wa & 15) : (wa & 1));
 }
 
-// Up to this many rows of x, a Q4_K matrix that the matrix-core GEMV takes
-// runs one GEMV per row rather than the GEMM: each GEMV reads the weights
-// again, but its time per row stays below the GEMM's time at a few rows
-// (3584 x 18944: 11.7 us per row against 45 us for the GEMM at 4 rows).
+// Up to this many rows of x (two or more), a Q4_K matrix that the small-M
+// kernel takes (k <= 24576) runs it, one launch per chunk of two or three
+// rows, each reading W once: 3584 x 18944 takes 16.9 us for two rows, 20.1
+// for three, 32.8 / 36.1 / 38.9 us for four / five / six, against 46 us for
+// the GEMM from four rows on (latency-bound there, one K-step of loads in
+// flight per workgroup).
+constexpr int64_t kMrRowsBeforeGemm = 6;
+
+// Up to this many rows of x, a longer Q4_K matrix that the matrix-core GEMV
+// still takes (k up to 32768) runs one GEMV per row rather than the GEMM:
+// each GEMV reads the weights again, but at a few rows its time per row
+// stays below the GEMM's.
 constexpr int64_t kMxRowsBeforeGemm = 3;
 
-// y[b * ldy + i] = (W x_b)[i] for b < batch: the GEMM for two or more rows
-// where batched_gemm allows (past kMxRowsBeforeGemm rows for a Q4_K matrix
-// the matrix-core GEMV takes), else one GEMV per row. Scratch as gemv_device.
+// y[b * ldy + i] = (W x_b)[i] for b < batch: the small-M kernel for two to
+// kMrRowsBeforeGemm rows of Q4_K, else the GEMM for two or more rows where
+// batched_gemm allows (past kMxRowsBeforeGemm rows for a Q4_K matrix the
+// matrix-core GEMV takes), else one GEMV per row. Scratch as gemv_device.
 int gemv_batched(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int64_t batch,
                  int64_t ldy, hipStream_t s, const frq::FixedScratch* fixed = nullptr) {
+    if (qtype == FRQ_Q4_K && batch >= 2 && batch <= kMrRowsBeforeGemm && frq::gemv_q4k_mr_ok(w, x, k)) {
+        for (int64_t b = 0; b < batch;) {   // chunks of 2 or 3 rows: 4 = 2 + 2, 5 = 3 + 2, 6 = 3 + 3
+            const int64_t rem = batch - b, m = rem == 4 ? 2 : (rem < 3 ? rem : 3);
+            FRQ_HIP(frq::launch_gemv_q4k_mr(w, x + b * k, y + b * ldy, n, k, (int)m, ldy, s));
+            b += m;
+        }
+        return FRQ_OK;
+    }
     const bool rows_first = batch <= kMxRowsBeforeGemm && frq::gemv_mx_eligible(qtype, w, x, n, k);
     if (!rows_first && batched_gemm(qtype, w, x, batch, n, k)) {
         if (fixed) {   // as many K-splits as the fixed partial region holds

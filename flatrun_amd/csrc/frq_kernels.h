@@ -90,6 +90,15 @@ bool plan_gemv_q10_mx(int64_t n, int64_t k, int* L, int* TR);
 hipError_t launch_gemv_q10_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int L, int TR,
                               hipStream_t stream);
 
+// Q4_K matvec of m <= kGemvMrMax rows of x at once (frq_gemv_mr.hip):
+// Y[r * ldy + i] = sum_j W[i, j] X[r * k + j]; W read once for the m rows,
+// each row's sums in the single-row element-wise order of operations per
+// weight. w and x 16-byte aligned, k <= 24576 (gemv_q4k_mr_ok).
+constexpr int kGemvMrMax = 3;
+bool gemv_q4k_mr_ok(const uint8_t* w, const float* x, int64_t k);
+hipError_t launch_gemv_q4k_mr(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int m, int64_t ldy,
+                              hipStream_t stream);
+
 // Grouped GEMV: y_i[n_i] = W_i[n_i, k] . x[k] for up to kGemvGroupMax
 // matrices sharing x (q/k/v, gate/up), in ONE launch when every W_i is Q4_K
 // (16-byte aligned) or Q6_K (4-byte aligned, even block count) and 8 lanes

@@ -4,7 +4,8 @@ The reference's batched entry points (matmul_<q>_batched, _C.cpp:154-283)
 multiply every row of x by W with an fp32 matvec. The library runs two or
 more rows of Q4_K, Q6_K or Q8_0 through one matrix-core GEMM that reads W
 once per tile of x rows, with W as exact integer codes and x as three bf16
-pieces, so the contract is the matvec's: 1e-5 of fp64, normwise and
+pieces (two to six rows of Q4_K: the small-M matvec of frq_gemv_mr.hip,
+W read once per two or three rows), so the contract is the matvec's: 1e-5 of fp64, normwise and
 componentwise, for every row. Cases: seq = 4, 32 and 512 (the reference CLI
 re-prefills the whole sequence on every step) at the benchmark shapes,
 ragged row counts around the 32 / 64-row tiles, K-split and unsplit grids,
@@ -182,18 +183,20 @@ def test_batched_noalloc_fewer_splits(frq):
         yd.free()
 
 
-@pytest.mark.parametrize("n,k,seq", [(3584, 18944, 2), (3584, 18944, 3), (3584, 18944, 4), (18944, 3584, 3),
-                                     (4096, 4096, 2), (1536, 8960, 3)])
+@pytest.mark.parametrize("n,k,seq", [(3584, 18944, 2), (3584, 18944, 3), (3584, 18944, 6), (3584, 18944, 7),
+                                     (18944, 3584, 3), (4096, 4096, 2), (1536, 8960, 5)])
 def test_batched_q4k_few_rows(frq, n, k, seq):
-    """Two or three rows of x on a Q4_K matrix the matrix-core GEMV takes run
-    as one GEMV per row: every row has the bits of a batch-1 call on that
-    row; from four rows on, the GEMM. Either way within the matvec bound,
-    with an outlier of 2^24 in the last row."""
+    """Two to six rows of x on a Q4_K matrix run the small-M kernel in
+    launches of two or three rows: each row has the bits it gets in a batch
+    of two (a row's result does not depend on its batch); from seven rows on,
+    the GEMM. Either way within the matvec bound, with an outlier of 2^24 in
+    the last row."""
     raw = synth.make_blocks("Q4_K", n, k, seed=n + seq)
     xs = synth.make_x(k, seed=seq + 80, batch=seq)
     xs[seq - 1, 5] = 2.0**24
     y = dev_batched("Q4_K", raw, xs, n, k)
-    if seq <= 3:
+    if seq <= 6:
         for r in range(seq):
-            assert bits_equal(y[r], dev_batched("Q4_K", raw, xs[r:r + 1].copy(), n, k)[0]), r
+            pair = np.stack([xs[r], xs[(r + 1) % seq]])
+            assert bits_equal(y[r], dev_batched("Q4_K", raw, pair, n, k)[0]), r
     oracle_rows("Q4_K", raw, xs, n, k, y, f"Q4_K {n}x{k} rows {seq}")

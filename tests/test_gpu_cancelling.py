@@ -9,8 +9,8 @@ orders of magnitude (the CPU test beside this one shows it on an fp32
 emulation); the contract -- 1e-5 of sum_j |w_ij x_j| per row, and of max |y|
 -- must hold on every kernel: the defaults per format and shape, each
 explicit launch geometry of the element-wise and split-K kernels, both
-matrix-core GEMV layouts, the batched GEMM, the grouped launch and the
-no-allocation entry point.
+matrix-core GEMV layouts, the batched GEMM, the small-M matvec, the grouped
+launch and the no-allocation entry point.
 """
 
 from __future__ import annotations
@@ -121,11 +121,11 @@ def test_matrix_core_layouts(frq, n, k, kernel):
 
 @pytest.mark.parametrize("q,n,k", [("Q4_K", 3584, 18944), ("Q4_K", 512, 4096), ("Q6_K", 1024, 4096),
                                    ("Q8_0", 4864, 896), ("Q5_K", 128, 4096)])
-@pytest.mark.parametrize("seq", [2, 4, 33])
+@pytest.mark.parametrize("seq", [2, 3, 4, 5, 33])
 def test_batched(frq, q, n, k, seq):
-    """The fp32 GEMM for two or more rows (per-row GEMVs for Q5_K and for a
-    few rows of a matrix-core Q4_K shape), outliers in every row, each row
-    with another outlier set."""
+    """The fp32 GEMM for two or more rows (per-row GEMVs for Q5_K, the
+    small-M matvec for two to six rows of Q4_K), outliers in every row, each
+    row with another outlier set."""
     raw, cols = _input(q, n, k, seed=n + seq)
     xs = np.stack([outlier_x(k, cols, seed=100 + r, big=(2.0**(20 + r % 9), -(2.0**24), 3.0e4)) for r in range(seq)])
     y, _ = _run(q, raw, xs, n, k)
