@@ -263,36 +263,39 @@ bool batched_gemm(int qtype, const uint8_t* w, const float* x, int64_t batch, in
     return !(reinterpret_cast<uintptr_t>(x) & 15) && !(qtype == FRQ_Q4_K ? (wa & 15) : (wa & 1));
 }
 
-// Up to this many rows of x (two or more), a Q4_K matrix that the small-M
-// kernel takes (k <= 24576) runs it, one launch per chunk of two or three
-// rows, each reading W once: 3584 x 18944 takes 16.9 us for two rows, 20.1
-// for three, 32.8 / 36.1 / 38.9 us for four / five / six, against 46 us for
-// the GEMM from four rows on (latency-bound there, one K-step of loads in
-// flight per workgroup).
-constexpr int64_t kMrRowsBeforeGemm = 6;
+// Up to this many rows of x (two or more), a matrix that the small-M kernel
+// takes (gemv_mr_ok) runs it, one launch per chunk of two or three rows,
+// each reading W once, rather than the GEMM (latency-bound at few rows, one
+// K-step of loads in flight per workgroup). Measured (graph-replayed, us):
+//   Q4_K 3584 x 18944: 2 / 3 / 6 rows 17.0 / 20.1 / 38-41; GEMM 46 from 4 rows
+//   Q6_K 4096 x 14336: 2 / 3 / 6 / 10 rows 16.0 / 18.3 / 34.1 / 64; GEMM 70
+//   Q8_0 4096 x 4096: 2 / 3 / 6 / 8 rows 7.8 / 9.3 / 16.9 / 22.9; GEMM 20.7
+int64_t mr_rows_before_gemm(int qtype) {
+    return qtype == FRQ_Q6_K ? 10 : 6;
+}
 
-// Up to this many rows of x, a longer Q4_K matrix that the matrix-core GEMV
-// still takes (k up to 32768) runs one GEMV per row rather than the GEMM:
-// each GEMV reads the weights again, but at a few rows its time per row
-// stays below the GEMM's.
-constexpr int64_t kMxRowsBeforeGemm = 3;
+// Up to this many rows of x, a matrix that the small-M kernel does not take
+// (its alignment, block count or k) runs one GEMV per row rather than the
+// GEMM: each GEMV reads the weights again, but at a few rows its time per
+// row stays below the GEMM's (Q4_K 3584 x 18944: 12.6 us per row against 46;
+// Q6_K 4096 x 14336: 13.3 against 70; Q8_0 4096 x 4096: 5.4 against 20.7).
+constexpr int64_t kRowsBeforeGemm = 3;
 
 // y[b * ldy + i] = (W x_b)[i] for b < batch: the small-M kernel for two to
-// kMrRowsBeforeGemm rows of Q4_K, else the GEMM for two or more rows where
-// batched_gemm allows (past kMxRowsBeforeGemm rows for a Q4_K matrix the
-// matrix-core GEMV takes), else one GEMV per row. Scratch as gemv_device.
+// mr_rows_before_gemm rows, else one GEMV per row up to kRowsBeforeGemm
+// rows, else the GEMM where batched_gemm allows, else one GEMV per row.
+// Scratch as gemv_device.
 int gemv_batched(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int64_t batch,
                  int64_t ldy, hipStream_t s, const frq::FixedScratch* fixed = nullptr) {
-    if (qtype == FRQ_Q4_K && batch >= 2 && batch <= kMrRowsBeforeGemm && frq::gemv_q4k_mr_ok(w, x, k)) {
-        for (int64_t b = 0; b < batch;) {   // chunks of 2 or 3 rows: 4 = 2 + 2, 5 = 3 + 2, 6 = 3 + 3
+    if (batch >= 2 && batch <= mr_rows_before_gemm(qtype) && frq::gemv_mr_ok(qtype, w, x, k)) {
+        for (int64_t b = 0; b < batch;) {   // chunks of 2 or 3 rows: 4 = 2 + 2, 5 = 3 + 2, 7 = 3 + 2 + 2
             const int64_t rem = batch - b, m = rem == 4 ? 2 : (rem < 3 ? rem : 3);
-            FRQ_HIP(frq::launch_gemv_q4k_mr(w, x + b * k, y + b * ldy, n, k, (int)m, ldy, s));
+            FRQ_HIP(frq::launch_gemv_mr(qtype, w, x + b * k, y + b * ldy, n, k, (int)m, ldy, s));
             b += m;
         }
         return FRQ_OK;
     }
-    const bool rows_first = batch <= kMxRowsBeforeGemm && frq::gemv_mx_eligible(qtype, w, x, n, k);
-    if (!rows_first && batched_gemm(qtype, w, x, batch, n, k)) {
+    if (batch > kRowsBeforeGemm && batched_gemm(qtype, w, x, batch, n, k)) {
         if (fixed) {   // as many K-splits as the fixed partial region holds
             FRQ_HIP(frq::launch_gemm_f32(qtype, w, x, y, batch, n, k, ldy, s, fixed->part, fixed->part_bytes));
             return FRQ_OK;

@@ -35,6 +35,7 @@
 
 #include "frq_common.h"
 #include "frq_kernels.h"
+#include "frq_ringrow.h"
 
 namespace frq {
 
@@ -537,27 +538,10 @@ __global__ void __launch_bounds__(512) gemv_q6_k_kernel(const uint8_t* __restric
 // Q6_K, register-ring variant (used when the weight base is 4-byte aligned
 // and a row has an even number of blocks: every block then starts at 0 or
 // 2 mod 4, alternating). Work unit as CPL=2 above: half h of a block and 8
-// consecutive l (l0 = 8p), 32 elements. Each 8-byte field (ql, ql+32, qh,
-// scales) is read as the three aligned dwords around it: even blocks read
-// [f, f+12) -- at most 2 bytes into the next block, which exists because the
-// row's block count is even -- and odd blocks [f-2, f+10), whose first 2
-// bytes are the previous block's; v_alignbit by 0 or 16 bits then extracts
-// the field, so every lane runs the same loads (no divergent alignment
-// branch, no 16-bit load pairs). Rows stream through a ring of U register
+// consecutive l (l0 = 8p), 32 elements; the lane's loads and sums are
+// Q6RingLane's (frq_ringrow.h). Rows stream through a ring of U register
 // slots, the row loop is unrolled over R rows without guards (as in the Q4_K
 // ring kernel), and partials are reduced with DPP into LDS.
-struct Q6Row {
-    uint32_t ql0[3], ql1[3], qh[3], sc[3];
-    uint32_t d;
-};
-
-__device__ __forceinline__ void load_win3(const uint8_t* p, uint32_t (&wv)[3]) {
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-    wv[0] = q[0];
-    wv[1] = q[1];
-    wv[2] = q[2];
-}
-
 template <int U, int R>
 __device__ __forceinline__ void gemv_q6_k_ring_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                     float* __restrict__ y, int64_t n, int nb, int64_t wg) {
@@ -567,83 +551,33 @@ __device__ __forceinline__ void gemv_q6_k_ring_body(const uint8_t* __restrict__ 
     const int blk_raw = tid >> 3, sub = tid & 7;
     const bool active = blk_raw < nb;
     const int blk = active ? blk_raw : 0;
-    const int h = sub >> 2, l0 = 8 * (sub & 3);
-    const int mis = (blk & 1) ? 2 : 0;              // block start mod 4
-    const uint32_t sh = 8u * (uint32_t)mis;
-    const int s = (sub & 3) >> 1;                  // l0 / 16
+    const Q6RingLane ln(blk, sub);
 
     const int64_t row0 = wg * R;
     const int nrows = (int)(n - row0 < R ? n - row0 : R);
     const int64_t row_bytes = (int64_t)nb * kQ6KBytes;
-    const uint32_t boff = (uint32_t)(blk * kQ6KBytes);
-    const uint32_t o_ql0 = boff + 64 * h + l0 - mis, o_ql1 = o_ql0 + 32;
-    const uint32_t o_qh = boff + 128 + 32 * h + l0 - mis, o_sc = boff + 192 + 8 * h - mis, o_d = boff + 208;
 
-    auto load1 = [&](Q6Row& t, int j) {
+    auto load1 = [&](Q6RingRow& t, int j) {
         const uint8_t* rp = w + (row0 + (j < nrows ? j : nrows - 1)) * row_bytes;
-        const auto rs = buffer_rsrc(rp, (uint32_t)row_bytes);
-        bload_b96(rs, o_ql0, t.ql0);
-        bload_b96(rs, o_ql1, t.ql1);
-        bload_b96(rs, o_qh, t.qh);
-        bload_b96(rs, o_sc, t.sc);
-        t.d = bload_u16(rs, o_d);
+        ln.load(buffer_rsrc(rp, (uint32_t)row_bytes), 0, t);
     };
 
-    float xv[4][8];
-    {
-        const float* xb = x + (int64_t)blk * kQKElems + 128 * h + l0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float4 a = *reinterpret_cast<const float4*>(xb + 32 * k);
-            const float4 c = *reinterpret_cast<const float4*>(xb + 32 * k + 4);
-            xv[k][0] = a.x; xv[k][1] = a.y; xv[k][2] = a.z; xv[k][3] = a.w;
-            xv[k][4] = c.x; xv[k][5] = c.y; xv[k][6] = c.z; xv[k][7] = c.w;
-        }
-    }
+    float xv[1][4][8];
+    ln.load_x(x, blk, xv[0]);
     __builtin_amdgcn_sched_barrier(0);
-    Q6Row ring[U];
+    Q6RingRow ring[U];
 #pragma unroll
     for (int i = 0; i < U; ++i) load1(ring[i], i);
     __builtin_amdgcn_sched_barrier(0);
 
     static_for<0, R>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
-        Q6Row& t = ring[j % U];
-        uint32_t ql0[2], ql1[2], qh[2];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            ql0[c] = __builtin_amdgcn_alignbit(t.ql0[c + 1], t.ql0[c], sh);
-            ql1[c] = __builtin_amdgcn_alignbit(t.ql1[c + 1], t.ql1[c], sh);
-            // upper bit of each 2-bit field flipped: the sign of q - 32 (q6_quad_signed)
-            qh[c] = __builtin_amdgcn_alignbit(t.qh[c + 1], t.qh[c], sh) ^ 0xAAAAAAAAu;
-        }
-        const uint32_t sc0 = __builtin_amdgcn_alignbit(t.sc[1], t.sc[0], sh);   // scale bytes 8h .. 8h+3
-        const uint32_t sc1 = __builtin_amdgcn_alignbit(t.sc[2], t.sc[1], sh);   // 8h+4 .. 8h+7
-        const float d = f16_bits_to_f32(t.d) * 0.25f;     // codes enter as 4 (q - 32)
-        // int8 scales sc[8h + s + 2k]: bytes s, s+2 of sc0 (k = 0, 1) and of sc1 (k = 2, 3)
-        const float sk[4] = {(float)(int8_t)(sc0 >> (8 * s)), (float)(int8_t)(sc0 >> (8 * s + 16)),
-                             (float)(int8_t)(sc1 >> (8 * s)), (float)(int8_t)(sc1 >> (8 * s + 16))};
-        float pu = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const uint32_t src = (k & 1) ? ql1[c] : ql0[c];
-                // bits 2k, 2k+1 of each qh byte -> bits 6, 7; the nibble -> bits 2..5
-                const uint32_t hsh = (k == 0) ? (qh[c] << 6) : (k == 1) ? (qh[c] << 4) : (k == 2) ? (qh[c] << 2) : qh[c];
-                float f[4];
-                q6_quad_signed((k >= 2) ? (src >> 2) : (src << 2), hsh, f);
-                a0 = __builtin_fmaf(f[0], xv[k][4 * c + 0], a0);
-                a1 = __builtin_fmaf(f[1], xv[k][4 * c + 1], a1);
-                a0 = __builtin_fmaf(f[2], xv[k][4 * c + 2], a0);
-                a1 = __builtin_fmaf(f[3], xv[k][4 * c + 3], a1);
-            }
-            pu = __builtin_fmaf(d * sk[k], a0 + a1, pu);
-        }
+        Q6RingRow& t = ring[j % U];
+        float pu[1];
+        ln.dot<1>(t, xv, pu);
         if constexpr (j + U < R) load1(t, j + U);
         __builtin_amdgcn_sched_barrier(0);                  // keep the rows in ring order
-        const float v = row16_sum(active ? pu : 0.0f);
+        const float v = row16_sum(active ? pu[0] : 0.0f);
         if ((lane & 15) == 15) red[j * 4 * nwaves + 4 * wave + (lane >> 4)] = v;
     });
     __syncthreads();
@@ -746,24 +680,8 @@ __global__ void __launch_bounds__(512) gemv_q8_0_kernel(const uint8_t* __restric
 }
 
 // Q8_0 register-ring kernel. Lane (block b = t / 2, half u = t % 2) owns
-// the 16 int8 at 34b + 2 + 16u (q8_0.h:36-51 element order). Blocks are 34
-// bytes, so with a 4-aligned row those bytes start at 0 or 2 mod 4: the lane
-// loads the aligned 20-byte window and funnel-shifts four dwords out of it.
-// Each int8 converts exactly with one sign-extending byte-select convert.
-// Rows as in the other ring kernels.
-__device__ __forceinline__ void sbytes8(uint32_t a, uint32_t b, float (&f)[8]) {
-    asm("v_cvt_f32_i32_sdwa %0, sext(%8) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-        "v_cvt_f32_i32_sdwa %1, sext(%8) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
-        "v_cvt_f32_i32_sdwa %2, sext(%8) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
-        "v_cvt_f32_i32_sdwa %3, sext(%8) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
-        "v_cvt_f32_i32_sdwa %4, sext(%9) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-        "v_cvt_f32_i32_sdwa %5, sext(%9) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
-        "v_cvt_f32_i32_sdwa %6, sext(%9) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
-        "v_cvt_f32_i32_sdwa %7, sext(%9) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3"
-        : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]), "=&v"(f[7])
-        : "v"(a), "v"(b));
-}
-
+// the 16 int8 at 34b + 2 + 16u (q8_0.h:36-51 element order); its loads and
+// sums are Q8RingLane's (frq_ringrow.h). Rows as in the other ring kernels.
 template <int U, int R>
 __global__ void __launch_bounds__(1024) gemv_q8_0_ring_kernel(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
@@ -771,69 +689,36 @@ __global__ void __launch_bounds__(1024) gemv_q8_0_ring_kernel(const uint8_t* __r
     static_assert(U <= R, "ring deeper than the row count");
     __shared__ float red[R * 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
-    const int blk_raw = tid >> 1, u = tid & 1;
+    const int blk_raw = tid >> 1;
     const bool active = blk_raw < nb;
     const int blk = active ? blk_raw : 0;
-    const uint32_t at = (uint32_t)(blk * kQ80Bytes + 2 + 16 * u);
-    const uint32_t o_win = at & ~3u, sh = 8u * (at & 3u), o_d = (uint32_t)(blk * kQ80Bytes);
+    const Q8RingLane ln(blk, tid & 1);
 
     const int64_t row0 = (int64_t)blockIdx.x * R;
     const int nrows = (int)(n - row0 < R ? n - row0 : R);
     const int64_t row_bytes = (int64_t)nb * kQ80Bytes;
 
-    struct Row {
-        uint4 q;
-        uint32_t q4, d;
-    };
-    auto load1 = [&](Row& t, int j) {
+    auto load1 = [&](Q8RingRow& t, int j) {
         const uint8_t* rp = w + (row0 + (j < nrows ? j : nrows - 1)) * row_bytes;
-        const auto rs = buffer_rsrc(rp, (uint32_t)row_bytes);
-        t.q = bload_b128(rs, o_win);
-        t.q4 = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(o_win + 16), 0, 0);
-        t.d = bload_u16(rs, o_d);
+        ln.load(buffer_rsrc(rp, (uint32_t)row_bytes), 0, t);
     };
 
-    float xv[16];
-    {
-        const float* xb = x + (int64_t)blk * kQ80Elems + 16 * u;
-#pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-            const float4 a = *reinterpret_cast<const float4*>(xb + i);
-            xv[i] = a.x; xv[i + 1] = a.y; xv[i + 2] = a.z; xv[i + 3] = a.w;
-        }
-    }
+    float xv[1][16];
+    ln.load_x(x, blk, xv[0]);
     __builtin_amdgcn_sched_barrier(0);
-    Row ring[U];
+    Q8RingRow ring[U];
 #pragma unroll
     for (int i = 0; i < U; ++i) load1(ring[i], i);
     __builtin_amdgcn_sched_barrier(0);
 
     static_for<0, R>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
-        Row& t = ring[j % U];
-        const uint32_t w5[5] = {t.q.x, t.q.y, t.q.z, t.q.w, t.q4};
-        uint32_t qd[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) qd[c] = __builtin_amdgcn_alignbit(w5[c + 1], w5[c], sh);
-        const float d = f16_bits_to_f32(t.d);
-        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 4; c += 2) {
-            float f[8];
-            sbytes8(qd[c], qd[c + 1], f);
-            a0 = __builtin_fmaf(f[0], xv[4 * c + 0], a0);
-            a1 = __builtin_fmaf(f[1], xv[4 * c + 1], a1);
-            a2 = __builtin_fmaf(f[2], xv[4 * c + 2], a2);
-            a3 = __builtin_fmaf(f[3], xv[4 * c + 3], a3);
-            a0 = __builtin_fmaf(f[4], xv[4 * c + 4], a0);
-            a1 = __builtin_fmaf(f[5], xv[4 * c + 5], a1);
-            a2 = __builtin_fmaf(f[6], xv[4 * c + 6], a2);
-            a3 = __builtin_fmaf(f[7], xv[4 * c + 7], a3);
-        }
+        Q8RingRow& t = ring[j % U];
+        float pu[1];
+        ln.dot<1>(t, xv, pu);
         if constexpr (j + U < R) load1(t, j + U);
         __builtin_amdgcn_sched_barrier(0);
-        const float pu = d * ((a0 + a1) + (a2 + a3));
-        const float v = row16_sum(active ? pu : 0.0f);
+        const float v = row16_sum(active ? pu[0] : 0.0f);
         if ((lane & 15) == 15) red[j * 4 * nwaves + 4 * wave + (lane >> 4)] = v;
     });
     __syncthreads();

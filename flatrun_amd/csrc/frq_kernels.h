@@ -90,14 +90,17 @@ bool plan_gemv_q10_mx(int64_t n, int64_t k, int* L, int* TR);
 hipError_t launch_gemv_q10_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int L, int TR,
                               hipStream_t stream);
 
-// Q4_K matvec of m <= kGemvMrMax rows of x at once (frq_gemv_mr.hip):
-// Y[r * ldy + i] = sum_j W[i, j] X[r * k + j]; W read once for the m rows,
-// each row's sums in the single-row element-wise order of operations per
-// weight. w and x 16-byte aligned, k <= 24576 (gemv_q4k_mr_ok).
+// Matvec of m <= kGemvMrMax rows of x at once (frq_gemv_mr.hip), Q4_K,
+// Q6_K or Q8_0: Y[r * ldy + i] = sum_j W[i, j] X[r * k + j]; W read once for
+// the m rows. Q4_K: per-weight fp32 arithmetic of the single-row element-wise
+// order; Q6_K / Q8_0: each row with the bits of the single-row ring kernel.
+// Needs x 16-byte aligned; Q4_K: W 16-byte aligned, k <= 24576; Q6_K: W
+// 4-byte aligned, an even block count, k <= 24576; Q8_0: W 4-byte aligned, an
+// even block count, k <= 16384 (gemv_mr_ok).
 constexpr int kGemvMrMax = 3;
-bool gemv_q4k_mr_ok(const uint8_t* w, const float* x, int64_t k);
-hipError_t launch_gemv_q4k_mr(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int m, int64_t ldy,
-                              hipStream_t stream);
+bool gemv_mr_ok(int qtype, const uint8_t* w, const float* x, int64_t k);
+hipError_t launch_gemv_mr(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int m,
+                          int64_t ldy, hipStream_t stream);
 
 // Grouped GEMV: y_i[n_i] = W_i[n_i, k] . x[k] for up to kGemvGroupMax
 // matrices sharing x (q/k/v, gate/up), in ONE launch when every W_i is Q4_K

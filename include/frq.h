@@ -166,14 +166,15 @@ int frq_dev_dequant_f16(int qtype, const void* w, size_t w_bytes, int64_t n_elem
  * nearest dmin*m / d*sc, so every term stays within 3 |w_j x_j|) and on x
  * split into three bf16 pieces (all 24 bits of every x with
  * |x| >= 2^-110), fp32 sums per sub-block, then the sub-block scales in
- * fp32 -- the same error bound, other bits than one row at a time. Two to
- * six rows of a Q4_K matrix with k <= 24576 run the small-M matvec instead
- * (one launch per two or three rows, W read once per launch, per-weight
- * fp32 arithmetic as one row; a row's bits do not depend on its batch); a
- * few rows of a longer Q4_K matrix that takes the matrix-core GEMV run one
- * GEMV per row (each row's bits those of a batch-1 call). Few output tiles split
- * k over workgroups whose fp32 partials a second kernel adds in a fixed
- * order (scratch of the stream). Q5_K and Q1_0 run one matvec per row. */
+ * fp32 -- the same error bound, other bits than one row at a time. A few
+ * rows (Q4_K, Q8_0: up to 6; Q6_K: up to 10) run the small-M matvec instead
+ * when W and k suit it (one launch per two or three rows, W read once per
+ * launch; Q4_K with per-weight fp32 arithmetic as one row, a row's bits
+ * independent of its batch; Q6_K and Q8_0 with the bits of a batch-1 call);
+ * up to 3 rows that it does not take run one GEMV per row. Few output
+ * tiles split k over workgroups whose fp32 partials a second kernel adds in
+ * a fixed order (scratch of the stream). Q5_K and Q1_0 run one matvec per
+ * row. */
 int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float* y, int64_t n, int64_t k,
                  int64_t batch, void* stream);
 

@@ -4,9 +4,9 @@ The reference's batched entry points (matmul_<q>_batched, _C.cpp:154-283)
 multiply every row of x by W with an fp32 matvec. The library runs two or
 more rows of Q4_K, Q6_K or Q8_0 through one matrix-core GEMM that reads W
 once per tile of x rows, with W as exact integer codes and x as three bf16
-pieces (two to six rows of Q4_K: the small-M matvec of frq_gemv_mr.hip,
-W read once per two or three rows), so the contract is the matvec's: 1e-5 of fp64, normwise and
-componentwise, for every row. Cases: seq = 4, 32 and 512 (the reference CLI
+pieces (a few rows: the small-M matvec of frq_gemv_mr.hip, W read once
+per two or three rows), so the contract is the matvec's: 1e-5 of fp64,
+normwise and componentwise, for every row. Cases: seq = 4, 32 and 512 (the reference CLI
 re-prefills the whole sequence on every step) at the benchmark shapes,
 ragged row counts around the 32 / 64-row tiles, K-split and unsplit grids,
 x with outliers on zero-weight columns and massive activations, strided

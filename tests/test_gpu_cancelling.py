@@ -124,8 +124,8 @@ def test_matrix_core_layouts(frq, n, k, kernel):
 @pytest.mark.parametrize("seq", [2, 3, 4, 5, 33])
 def test_batched(frq, q, n, k, seq):
     """The fp32 GEMM for two or more rows (per-row GEMVs for Q5_K, the
-    small-M matvec for two to six rows of Q4_K), outliers in every row, each
-    row with another outlier set."""
+    small-M matvec for a few rows of Q4_K, Q6_K and Q8_0), outliers in every
+    row, each row with another outlier set."""
     raw, cols = _input(q, n, k, seed=n + seq)
     xs = np.stack([outlier_x(k, cols, seed=100 + r, big=(2.0**(20 + r % 9), -(2.0**24), 3.0e4)) for r in range(seq)])
     y, _ = _run(q, raw, xs, n, k)

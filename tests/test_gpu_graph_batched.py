@@ -3,8 +3,8 @@
 A HIP graph replays the kernels a capture recorded with the pointers and
 scratch they were given then. The batched matvec (frq_gemm_f32.hip) writes
 fp32 partial planes into stream scratch and adds them in a second kernel
-when it splits K, the two- to six-row Q4_K route runs one small-M kernel
-launch per two or three rows, and the fp16 dequant is a plain kernel; each
+when it splits K, the few-row route runs one small-M kernel launch per
+two or three rows, and the fp16 dequant is a plain kernel; each
 is captured once, replayed four times with y clobbered before and eager
 launches of other shapes (which reuse the same scratch) between the
 replays, and every replay must give the eager result bit for bit.
@@ -21,9 +21,10 @@ from flatrun_amd import _lib, device, synth
 pytestmark = pytest.mark.gpu
 
 # (format, n, k, rows of x): 32-, 64- and 128-row tiles, split and unsplit
-# grids, and the small-M route for two to six rows.
+# grids, and the small-M route for a few rows.
 CASES = [
     ("Q4_K", 3584, 18944, 7), ("Q4_K", 3584, 18944, 2), ("Q4_K", 1536, 8960, 3), ("Q4_K", 3584, 18944, 5),
+    ("Q6_K", 4096, 14336, 7), ("Q8_0", 4864, 896, 3),
     ("Q4_K", 14336, 4096, 200), ("Q6_K", 1024, 4096, 100), ("Q6_K", 4096, 14336, 40),
     ("Q8_0", 4864, 896, 33), ("Q8_0", 4096, 4096, 512),
 ]
