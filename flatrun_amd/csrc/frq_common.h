@@ -216,6 +216,25 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// load(0) + load(1) + ... + load(S - 1), added in that order (fixed bits),
+// with the loads issued eight at a time before they are added: the sum of S
+// split-K partial planes with eight loads in flight instead of one round
+// trip per plane.
+template <typename V, typename Load>
+__device__ __forceinline__ V sum_planes(Load load, int S) {
+    V v = load(0);
+    int q = 1;
+    for (; q + 8 <= S; q += 8) {
+        V t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = load(q + u);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v += t[u];
+    }
+    for (; q < S; ++q) v += load(q);
+    return v;
+}
+
 // Decoded per-lane constants for the two 6-bit (scale, min) pairs 2g, 2g+1
 // of a K-quant block (get_scale_min_k4, gguf.py:135-163). With s0, s1, s2 the
 // three scale dwords:

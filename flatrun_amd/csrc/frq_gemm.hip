@@ -332,24 +332,8 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
 }
 
 // y[i] = part[0][i] + part[1][i] + ... + part[S-1][i], in that order (the
-// same bits however the splits were scheduled); 4 elements per thread. The
-// planes are loaded eight at a time before they are added, so a thread has
-// eight loads in flight instead of one round trip per plane.
-template <typename V, typename Load>
-__device__ __forceinline__ V sum_planes(Load load, int S) {
-    V v = load(0);
-    int q = 1;
-    for (; q + 8 <= S; q += 8) {
-        V t[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) t[u] = load(q + u);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v += t[u];
-    }
-    for (; q < S; ++q) v += load(q);
-    return v;
-}
-
+// same bits however the splits were scheduled); 4 elements per thread, the
+// planes loaded eight at a time (sum_planes).
 __global__ void __launch_bounds__(256) gemm_split_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
                                                                 int S, int64_t count) {
     const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;

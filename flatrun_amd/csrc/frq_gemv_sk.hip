@@ -31,9 +31,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restr
                                                             int64_t n, int S) {
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= n) return;
-    float acc = part[r];
-    for (int s = 1; s < S; ++s) acc += part[(int64_t)s * n + r];
-    y[r] = acc;
+    y[r] = sum_planes<float>([&](int s) { return part[(int64_t)s * n + r]; }, S);
 }
 
 }  // namespace
