@@ -145,12 +145,15 @@ class GemvWorkload:
     def time_throughput(self, steps: int, warmup: int) -> float:
         """Seconds for `steps` launches replayed back-to-back from one HIP
         graph, after a settle burst (settle) and `warmup` untimed launches;
-        events on the launching stream."""
+        events on the launching stream. The device is synchronized before
+        the warmup launches, which keep it busy while the host submits the
+        timed graph, so the timed region holds the `steps` launches and not
+        the host's submission latency."""
         g_warm, g = self.graph(max(warmup, 1)), self.graph(steps, start=warmup)
         self.settled = self.settle()
-        g_warm.launch(self.stream)
         device.synchronize()
         e0, e1 = device.Event(), device.Event()
+        g_warm.launch(self.stream)
         e0.record(self.stream)
         g.launch(self.stream)
         e1.record(self.stream)
