@@ -1,5 +1,5 @@
 // Matvec of a few rows of x at once: Y[r, i] = sum_j W[i, j] X[r, j] for
-// r < M (M <= 3), the reference's batched entry points (matmul_<q>_batched,
+// r < M (M = 2, 3), the reference's batched entry points (matmul_<q>_batched,
 // _C.cpp:154-283) at small seq, reading W once for the M rows. Q4_K, Q6_K
 // and Q8_0.
 //
@@ -220,7 +220,6 @@ hipError_t mr_go(const uint8_t* w, const float* x, float* y, int64_t n, int nb, 
     const size_t lds = sizeof(float) * (size_t)R * m * 4 * waves;
     const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
     switch (m) {
-        case 1: gemv_mr_kernel<F, 1, 2, T><<<gd, bd, lds, s>>>(w, x, y, n, nb, (int)R, ldy); break;
         case 2: gemv_mr_kernel<F, 2, mr_batch<F>(2), T><<<gd, bd, lds, s>>>(w, x, y, n, nb, (int)R, ldy); break;
         case 3: gemv_mr_kernel<F, 3, mr_batch<F>(3), T><<<gd, bd, lds, s>>>(w, x, y, n, nb, (int)R, ldy); break;
         default: return hipErrorInvalidValue;
@@ -249,8 +248,8 @@ bool gemv_mr_ok(int qtype, const uint8_t* w, const float* x, int64_t k) {
 
 hipError_t launch_gemv_mr(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int m,
                           int64_t ldy, hipStream_t stream) {
-    if (n <= 0 || m <= 0) return hipSuccess;
-    if (m > kGemvMrMax || ldy < n || !gemv_mr_ok(qtype, w, x, k)) return hipErrorInvalidValue;
+    if (n <= 0) return hipSuccess;
+    if (m < 2 || m > kGemvMrMax || ldy < n || !gemv_mr_ok(qtype, w, x, k)) return hipErrorInvalidValue;
     switch (qtype) {
         case kTypeQ4K: return mr_go<Q4KMrLane>(w, x, y, n, (int)(k / kQKElems), m, ldy, stream);
         case kTypeQ6K: return mr_go<Q6KMrLane>(w, x, y, n, (int)(k / kQKElems), m, ldy, stream);

@@ -90,7 +90,7 @@ bool plan_gemv_q10_mx(int64_t n, int64_t k, int* L, int* TR);
 hipError_t launch_gemv_q10_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int L, int TR,
                               hipStream_t stream);
 
-// Matvec of m <= kGemvMrMax rows of x at once (frq_gemv_mr.hip), Q4_K,
+// Matvec of m = 2 .. kGemvMrMax rows of x at once (frq_gemv_mr.hip), Q4_K,
 // Q6_K or Q8_0: Y[r * ldy + i] = sum_j W[i, j] X[r * k + j]; W read once for
 // the m rows. Q4_K: per-weight fp32 arithmetic of the single-row element-wise
 // order; Q6_K / Q8_0: each row with the bits of the single-row ring kernel.
