@@ -6,7 +6,10 @@ Same function names, argument order, argument conversion and return shapes as
 kernels. Arguments are converted the way ``py::array_t<T, c_style |
 forcecast>`` converts them (any ndim, cast to the element type, made
 contiguous). Errors the reference raises as ``std::runtime_error`` arrive as
-:class:`flatrun_amd._lib.FrqError`, a ``RuntimeError``.
+:class:`flatrun_amd._lib.FrqError`, a ``RuntimeError``. A HIP runtime failure
+(a failed launch, allocation or copy) arrives as
+:class:`flatrun_amd._lib.FrqDeviceError`, which is not a ``RuntimeError``, so
+the reference runtime's NumPy fallback does not swallow it.
 
 Additions beyond the reference module, for the formats it lacks:
 ``dequant_q5_k``, ``dequant_q1_0``, ``dequant_q4_0``, ``dequant_q5_0``,

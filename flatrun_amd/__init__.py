@@ -27,7 +27,7 @@ import threading
 import numpy as np
 
 from . import _C, _lib
-from ._lib import FrqError, LibraryMissing
+from ._lib import FrqDeviceError, FrqError, LibraryMissing
 from .loader import dequant_handle
 from .residency import WeightCache
 
@@ -39,6 +39,7 @@ __all__ = [
     "is_available",
     "is_neon",
     "version",
+    "FrqDeviceError",
     "FrqError",
     "LibraryMissing",
 ]
@@ -51,7 +52,7 @@ def is_available() -> bool:
     """True when libfrq_hip.so loads and a HIP device is visible."""
     try:
         return _lib.device_count() > 0
-    except (LibraryMissing, FrqError):
+    except (LibraryMissing, FrqError, FrqDeviceError):
         return False
 
 
@@ -181,10 +182,11 @@ class NativeBackend:
         return {"enabled": True, "capacity": c.capacity, "bytes": c.bytes, "entries": len(c),
                 "hits": c.hits, "misses": c.misses}
 
-    def _cached(self, weight):
+    def _cached(self, weight, held=()):
         """The device copy of a host weight from the attached stream or the
         cache, else None. The caller holds the lock until its launch has
-        finished: a later lookup may evict (free) a cache entry."""
+        finished: a later lookup may evict (free) a cache entry, except the
+        entries in `held` (those the caller's pending launch reads)."""
         if isinstance(weight, DeviceWeight) or (self._cache is None and self._stream_src is None):
             return None
         raw = _raw_bytes(weight).reshape(-1)
@@ -194,7 +196,7 @@ class NativeBackend:
                 return dw
         if self._cache is None:
             return None
-        return self._cache.lookup(raw, DeviceWeight)
+        return self._cache.lookup(raw, DeviceWeight, held=held)
 
     def _scratch_for(self, need: int):
         """The scratch buffer, grown to `need` bytes; the caller holds the lock
@@ -322,7 +324,7 @@ class NativeBackend:
             try:
                 ws = []
                 for q, wgt, n in parts:
-                    cached = self._cached(wgt)
+                    cached = self._cached(wgt, held=ws)
                     if cached is not None:
                         ws.append(cached)
                     elif isinstance(wgt, DeviceWeight):

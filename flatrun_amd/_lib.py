@@ -31,7 +31,7 @@ QTYPES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K, "Q1_0": Q1_0,
 BLOCKS = {Q8_0: (34, 32), Q4_K: (144, 256), Q5_K: (176, 256), Q6_K: (210, 256), Q1_0: (18, 128)}
 
 
-GEMV_AUTO, GEMV_SPLITK, GEMV_ROWS, GEMV_ROWS_LDS, GEMV_MX, GEMV_MX_H = 0, 1, 2, 3, 4, 5
+GEMV_AUTO, GEMV_SPLITK, GEMV_ROWS, GEMV_MX = 0, 1, 2, 4   # frq_gemv_config.kernel (3 and 5 are not used)
 
 
 class GemvConfig(ctypes.Structure):
@@ -49,12 +49,32 @@ class LibraryMissing(RuntimeError):
 
 
 class FrqError(RuntimeError):
-    """A failed libfrq_hip call. Subclasses RuntimeError, the exception the
-    reference runtime catches to fall back (runtime/backend.py:263-268)."""
+    """A libfrq_hip call refused its arguments: a shape, size, alignment or
+    quant type it does not take, or no device. Subclasses RuntimeError, the
+    exception the reference runtime catches to fall back to NumPy for a
+    layout the kernel rejects (runtime/backend.py:259-268)."""
 
     def __init__(self, code: int, message: str):
         super().__init__(f"{STATUS_NAMES.get(code, code)}: {message}")
         self.code = code
+
+
+class FrqDeviceError(Exception):
+    """A HIP runtime failure inside libfrq_hip (FRQ_ERR_HIP): a launch,
+    allocation, copy or synchronization that the runtime reported failed.
+    Deliberately not a RuntimeError: the reference runtime treats any
+    RuntimeError from a kernel as a rejected layout and recomputes in NumPy
+    (runtime/backend.py:259-268), which would turn a device failure into a
+    silent 100-1000x slowdown. This one propagates to the caller."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(code, code)}: {message}")
+        self.code = code
+
+
+def error_for(code: int, message: str) -> Exception:
+    """The exception a failed call with status `code` raises."""
+    return FrqDeviceError(code, message) if code == ERR_HIP else FrqError(code, message)
 
 
 _c = ctypes
@@ -162,9 +182,11 @@ def load_error() -> BaseException | None:
 
 
 def check(rc: int) -> None:
+    """Raise for a failed status: FrqDeviceError for a HIP runtime failure,
+    FrqError (a RuntimeError) for everything else."""
     if rc != OK:
         msg = lib().frq_last_error().decode(errors="replace")
-        raise FrqError(rc, msg)
+        raise error_for(rc, msg)
 
 
 def device_count() -> int:

@@ -37,6 +37,15 @@ int hip_fail(hipError_t e, const char* what) {
     return fail(FRQ_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
 
+// A tuned launch: the launchers refuse a geometry they do not take with
+// hipErrorInvalidValue / hipErrorInvalidConfiguration before launching
+// anything, which is the caller's argument, not a device failure.
+int tuned_fail(hipError_t e, const char* what) {
+    if (e == hipErrorInvalidValue || e == hipErrorInvalidConfiguration)
+        return fail(FRQ_ERR_UNSUPPORTED, "%s: launch geometry not accepted (%s)", what, hipGetErrorString(e));
+    return hip_fail(e, what);
+}
+
 #define FRQ_HIP(call)                                   \
     do {                                                \
         hipError_t e_ = (call);                         \
@@ -281,13 +290,22 @@ int64_t mr_rows_before_gemm(int qtype) {
 // Q6_K 4096 x 14336: 13.3 against 70; Q8_0 4096 x 4096: 5.4 against 20.7).
 constexpr int64_t kRowsBeforeGemm = 3;
 
-// y[b * ldy + i] = (W x_b)[i] for b < batch: the small-M kernel for two to
+// Which kernels a batch of x rows takes: the small-M kernel for two to
 // mr_rows_before_gemm rows, else one GEMV per row up to kRowsBeforeGemm
 // rows, else the GEMM where batched_gemm allows, else one GEMV per row.
-// Scratch as gemv_device.
+enum class BatchRoute { SmallM, Gemm, Rows };
+BatchRoute batch_route(int qtype, const uint8_t* w, const float* x, int64_t batch, int64_t n, int64_t k) {
+    if (batch >= 2 && batch <= mr_rows_before_gemm(qtype) && frq::gemv_mr_ok(qtype, w, x, k)) return BatchRoute::SmallM;
+    if (batch > kRowsBeforeGemm && batched_gemm(qtype, w, x, batch, n, k)) return BatchRoute::Gemm;
+    return BatchRoute::Rows;
+}
+
+// y[b * ldy + i] = (W x_b)[i] for b < batch, by batch_route. Scratch as
+// gemv_device (the small-M kernel uses none).
 int gemv_batched(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int64_t batch,
                  int64_t ldy, hipStream_t s, const frq::FixedScratch* fixed = nullptr) {
-    if (batch >= 2 && batch <= mr_rows_before_gemm(qtype) && frq::gemv_mr_ok(qtype, w, x, k)) {
+    const BatchRoute route = batch_route(qtype, w, x, batch, n, k);
+    if (route == BatchRoute::SmallM) {
         for (int64_t b = 0; b < batch;) {   // chunks of 2 or 3 rows: 4 = 2 + 2, 5 = 3 + 2, 7 = 3 + 2 + 2
             const int64_t rem = batch - b, m = rem == 4 ? 2 : (rem < 3 ? rem : 3);
             FRQ_HIP(frq::launch_gemv_mr(qtype, w, x + b * k, y + b * ldy, n, k, (int)m, ldy, s));
@@ -295,7 +313,7 @@ int gemv_batched(int qtype, const uint8_t* w, const float* x, float* y, int64_t 
         }
         return FRQ_OK;
     }
-    if (batch > kRowsBeforeGemm && batched_gemm(qtype, w, x, batch, n, k)) {
+    if (route == BatchRoute::Gemm) {
         if (fixed) {   // as many K-splits as the fixed partial region holds
             FRQ_HIP(frq::launch_gemm_f32(qtype, w, x, y, batch, n, k, ldy, s, fixed->part, fixed->part_bytes));
             return FRQ_OK;
@@ -557,8 +575,9 @@ static int dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, fl
     const uint8_t* wp = static_cast<const uint8_t*>(w);
     if (fixed) {   // refuse an oversized shape before any row is launched
         size_t sb = 0, pb = 0;
-        if (!batched_gemm(qtype, wp, x, batch, n, k))   // the batched GEMM splits K within what is there
-            gemv_scratch_need(qtype, wp, x, n, k, &sb, &pb);
+        // the small-M kernel needs no scratch and the batched GEMM splits K
+        // within what is there; rows that run one GEMV each need theirs
+        if (batch_route(qtype, wp, x, batch, n, k) == BatchRoute::Rows) gemv_scratch_need(qtype, wp, x, n, k, &sb, &pb);
         if (sb > fixed->slot_bytes || pb > fixed->part_bytes)
             return fail(FRQ_ERR_UNSUPPORTED,
                         "%s gemv n=%lld k=%lld needs %zu slot + %zu partial bytes of scratch; the fixed scratch "
@@ -627,8 +646,10 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     if (n == 0 || k == 0) return fail(FRQ_ERR_SHAPE, "tuned gemv needs n > 0 and k > 0");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const uint8_t* wp = static_cast<const uint8_t*>(w);
-    if (cfg->kernel == FRQ_GEMV_MX || cfg->kernel == FRQ_GEMV_MX_H ||
-        (cfg->kernel == FRQ_GEMV_AUTO && frq::gemv_mx_eligible(qtype, wp, x, n, k))) {
+    if (cfg->kernel != FRQ_GEMV_AUTO && cfg->kernel != FRQ_GEMV_SPLITK && cfg->kernel != FRQ_GEMV_ROWS &&
+        cfg->kernel != FRQ_GEMV_MX)
+        return fail(FRQ_ERR_INVALID, "tuned gemv: unknown kernel %d", cfg->kernel);
+    if (cfg->kernel == FRQ_GEMV_MX || (cfg->kernel == FRQ_GEMV_AUTO && frq::gemv_mx_eligible(qtype, wp, x, n, k))) {
         if (qtype != FRQ_Q4_K) return fail(FRQ_ERR_UNSUPPORTED, "the matrix-core GEMV takes Q4_K");
         if ((reinterpret_cast<uintptr_t>(wp) | reinterpret_cast<uintptr_t>(x)) & 15)
             return fail(FRQ_ERR_ALIGN, "the matrix-core GEMV needs 16-byte aligned weights and x");
@@ -636,20 +657,21 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
         mp.rows = cfg->rows;
         mp.tiles = cfg->cpl;
         mp.ksplit = cfg->slices;
-        mp.layout = cfg->kernel == FRQ_GEMV_MX_H ? 1 : cfg->kernel == FRQ_GEMV_MX ? 0 : -1;
+        mp.depth = cfg->unroll;
         if (!frq::plan_gemv_mx(n, k, &mp))
-            return fail(FRQ_ERR_UNSUPPORTED, "matrix-core GEMV: no plan for n=%lld k=%lld rows=%d tiles=%d ksplit=%d",
-                        (long long)n, (long long)k, cfg->rows, cfg->cpl, cfg->slices);
+            return fail(FRQ_ERR_UNSUPPORTED,
+                        "matrix-core GEMV: no plan for n=%lld k=%lld rows=%d tiles=%d ksplit=%d depth=%d",
+                        (long long)n, (long long)k, cfg->rows, cfg->cpl, cfg->slices, cfg->unroll);
         float* part = nullptr;
         uint32_t* cnt = nullptr;
         std::lock_guard<std::mutex> lk(g_sk_mu);
         if (int rc = sk_scratch_locked(s, 0, frq::gemv_mx_slot_bytes(mp, n), &part, &cnt)) return rc;
         hipError_t e = frq::launch_gemv_mx(wp, x, y, n, k, mp, reinterpret_cast<uint64_t*>(cnt), s);
-        if (e != hipSuccess) return hip_fail(e, "launch_gemv_mx");
-        cfg->kernel = mp.layout == 1 ? FRQ_GEMV_MX_H : FRQ_GEMV_MX;
+        if (e != hipSuccess) return tuned_fail(e, "launch_gemv_mx");
+        cfg->kernel = FRQ_GEMV_MX;
         cfg->cpl = mp.tiles;
         cfg->rows = mp.rows;
-        cfg->unroll = mp.blocks;
+        cfg->unroll = mp.depth;
         cfg->slices = mp.ksplit;
         cfg->waves_per_wg = mp.waves;
         cfg->items = mp.grid;
@@ -669,7 +691,7 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
         std::lock_guard<std::mutex> lk(g_sk_mu);
         if (int rc = sk_scratch_locked(s, pb, cb, &part, &cnt)) return rc;
         hipError_t e = frq::launch_gemv_sk(qtype, wp, x, y, n, k, p, part, cnt, s);
-        if (e != hipSuccess) return hip_fail(e, "launch_gemv_sk");
+        if (e != hipSuccess) return tuned_fail(e, "launch_gemv_sk");
         cfg->kernel = FRQ_GEMV_SPLITK;
         cfg->cpl = p.cpl;
         cfg->rows = p.rows;
@@ -684,13 +706,9 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     p.rows_per_wg = cfg->rows;
     p.unroll = cfg->unroll;
     p.slices = cfg->slices;
-    if (cfg->kernel == FRQ_GEMV_ROWS_LDS) {
-        if (qtype != FRQ_Q4_K) return fail(FRQ_ERR_UNSUPPORTED, "the LDS row ring is a Q4_K kernel");
-        p.lds = cfg->unroll > 0 ? cfg->unroll : 4;
-    }
     hipError_t e = frq::launch_gemv(qtype, wp, x, y, n, k, &p, s);
-    if (e != hipSuccess) return hip_fail(e, "launch_gemv");
-    cfg->kernel = p.lds > 0 ? FRQ_GEMV_ROWS_LDS : FRQ_GEMV_ROWS;
+    if (e != hipSuccess) return tuned_fail(e, "launch_gemv");
+    cfg->kernel = FRQ_GEMV_ROWS;
     cfg->cpl = p.cpl;
     cfg->rows = p.rows_per_wg;
     cfg->unroll = p.unroll;

@@ -219,133 +219,6 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
     }
 }
 
-// ------------------------------------------------------- Q4_K, LDS ring
-// The same per-lane work as gemv_q4_k_body with CPL = 1, fed through a ring
-// of D row slots in LDS instead of registers. Each wave owns blocks
-// [8w, 8w + 8) of every row (its lanes' blocks) and copies exactly those
-// 1152 bytes of row j + D into its own slot with two direct-to-LDS buffer
-// loads (64 x 16 B, then 32 x 4 B), contiguous like a plain streaming copy
-// and with no registers held while they are in flight. Nothing is shared
-// between waves, so no barrier is needed: a wave waits for its own loads
-// (vmcnt, counted at compile time), reads its lane's header and qs with two
-// ds_read_b128 and computes the row. Offsets past the row (the last wave's
-// missing blocks) read as zero through the row's buffer descriptor.
-constexpr int kQ4KLdsWaves = 16;      // slot storage sized for 1024-lane workgroups
-constexpr int kQ4KLdsWaveBytes = 1280;
-
-// Slot K of the ring: a variable of its own, so the compiler's LDS alias
-// scopes tell the slots apart and a read of slot K waits only for the loads
-// into slot K (one array indexed by slot makes every read wait for them all).
-template <int K>
-__device__ __forceinline__ uint8_t* q4k_lds_slot() {
-    __shared__ __attribute__((aligned(16))) uint8_t slot[kQ4KLdsWaves * kQ4KLdsWaveBytes];
-    return slot;
-}
-
-// s_waitcnt with vmcnt <= N and expcnt / lgkmcnt left unconstrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-template <int D, int R>
-__global__ void __launch_bounds__(1024) gemv_q4_k_lds_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                             float* __restrict__ y, int64_t n, int nb) {
-    static_assert(D >= 1 && D <= R, "ring depth");
-    __shared__ float red[R * 64];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
-    const int blk = tid >> 3, sub = tid & 7;
-    const bool active = blk < nb;
-    const int gblk = active ? blk : 0;
-    const int g = sub >> 1, hh = sub & 1;
-    const PairDecode pdec(sub);
-    const bool own_hi = hh;
-    const float hfac = own_hi ? 0.0625f : 1.0f;
-    const uint32_t mask_a = own_hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu, mask_b = ~mask_a;
-
-    const int64_t row0 = (int64_t)blockIdx.x * R;
-    const int nrows = (int)(n - row0 < R ? n - row0 : R);
-    const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
-    const uint32_t wbase = (uint32_t)(wave * 8 * kQ4KBytes);          // the wave's bytes in a row
-    const uint32_t off_a = wbase + 16u * (uint32_t)lane;               // 64 x 16 B
-    const uint32_t off_b = wbase + 1024u + 4u * (uint32_t)(lane & 31); // 32 x 4 B (lanes 32..63 repeat)
-    // lane's block inside the wave's slot (inactive lanes read the wave's block 0)
-    const uint32_t lblk = active ? (uint32_t)((blk & 7) * kQ4KBytes) : 0u;
-    const uint32_t lq = lblk + 16 + 32 * g + 16 * hh;
-
-    auto issue = [&](auto jc) {                                        // row j -> slot j % D
-        constexpr int j = decltype(jc)::value;
-        const uint8_t* rp = w + (row0 + (j < nrows ? j : nrows - 1)) * row_bytes;
-        const auto rs = buffer_rsrc(rp, (uint32_t)row_bytes);
-        uint8_t* slot = q4k_lds_slot<j % D>() + wave * kQ4KLdsWaveBytes;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)slot, 16, off_a, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(slot + 1024), 4, off_b, 0,
-                                                 0, 0);
-    };
-
-    float xl[16], xh[16];
-    {
-        const float* xb = x + (int64_t)gblk * kQKElems + 64 * g + 16 * hh;
-        const float* xa = xb + (own_hi ? 32 : 0);
-        const float* xo = xb + (own_hi ? 0 : 32);
-#pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-            const float4 a = *reinterpret_cast<const float4*>(xa + i);
-            const float4 c = *reinterpret_cast<const float4*>(xo + i);
-            xl[i] = a.x; xl[i + 1] = a.y; xl[i + 2] = a.z; xl[i + 3] = a.w;
-            xh[i] = c.x; xh[i + 1] = c.y; xh[i + 2] = c.z; xh[i + 3] = c.w;
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    static_for<0, D>([&](auto ic) { issue(ic); });
-    __builtin_amdgcn_sched_barrier(0);
-
-    static_for<0, R>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        constexpr int newer = 2 * ((R - 1 - j) < (D - 1) ? (R - 1 - j) : (D - 1));
-        wait_vmcnt<newer>();                                           // this wave's copy of row j landed
-        __builtin_amdgcn_sched_barrier(0);
-        const uint8_t* slot = q4k_lds_slot<j % D>() + wave * kQ4KLdsWaveBytes;
-        const uint4 hd = *reinterpret_cast<const uint4*>(slot + lblk);
-        const uint4 q = *reinterpret_cast<const uint4*>(slot + lq);
-        const float d = f16_bits_to_f32(hd.x), dm = f16_bits_to_f32(hd.x >> 16);
-        uint32_t sc0, m0;
-        pdec(hd.y, hd.z, hd.w, sc0, m0);
-        // per-weight w = fma(s, f, -t), plane B with the neighbour's pair
-        const float sa = (d * hfac) * (float)sc0, ta = dm * (float)m0;
-        const float sb = dpp_mov<0xB1>(sa), tb = dpp_mov<0xB1>(ta);
-        float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
-        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int wd = 0; wd < 4; ++wd) {
-            float f[8];
-            nibbles8(qw[wd], f, mask_a, mask_b);
-            const int e = 4 * wd;
-            a0 = __builtin_fmaf(__builtin_fmaf(sa, f[0], -ta), xl[e + 0], a0);
-            a1 = __builtin_fmaf(__builtin_fmaf(sa, f[1], -ta), xl[e + 1], a1);
-            b0 = __builtin_fmaf(__builtin_fmaf(sb, f[4], -tb), xh[e + 0], b0);
-            b1 = __builtin_fmaf(__builtin_fmaf(sb, f[5], -tb), xh[e + 1], b1);
-            a0 = __builtin_fmaf(__builtin_fmaf(sa, f[2], -ta), xl[e + 2], a0);
-            a1 = __builtin_fmaf(__builtin_fmaf(sa, f[3], -ta), xl[e + 3], a1);
-            b0 = __builtin_fmaf(__builtin_fmaf(sb, f[6], -tb), xh[e + 2], b0);
-            b1 = __builtin_fmaf(__builtin_fmaf(sb, f[7], -tb), xh[e + 3], b1);
-        }
-        // the slot has been read into registers: refill it with row j + D
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (j + D < R) issue(Int<j + D>{});
-        const float pu = (a0 + a1) + (b0 + b1);
-        const float v = row16_sum(active ? pu : 0.0f);
-        if ((lane & 15) == 15) red[j * 4 * nwaves + 4 * wave + (lane >> 4)] = v;
-    });
-    __syncthreads();
-    for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
-        float s = 0.0f;
-        for (int w2 = 0; w2 < 4 * nwaves; ++w2) s += red[r * 4 * nwaves + w2];
-        y[row0 + r] = s;
-    }
-}
-
 template <int CPL, int U, int R>
 __global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_waves_per_eu((CPL == 1 && U <= 3) ? 5 : 1)))
 gemv_q4_k_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int64_t n, int nb) {
@@ -1048,40 +921,6 @@ bool q4k_rows(int rows, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const
     }
 }
 
-template <int D, int R>
-void q4k_lds_go(dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n, int nb) {
-    gemv_q4_k_lds_kernel<(D < R ? D : R), R><<<gd, bd, 0, s>>>(w, x, y, n, nb);
-}
-
-template <int D>
-bool q4k_lds_rows(int rows, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n,
-                  int nb) {
-    switch (rows) {
-        case 1: q4k_lds_go<D, 1>(gd, bd, s, w, x, y, n, nb); return true;
-        case 2: q4k_lds_go<D, 2>(gd, bd, s, w, x, y, n, nb); return true;
-        case 4: q4k_lds_go<D, 4>(gd, bd, s, w, x, y, n, nb); return true;
-        case 7: q4k_lds_go<D, 7>(gd, bd, s, w, x, y, n, nb); return true;
-        case 8: q4k_lds_go<D, 8>(gd, bd, s, w, x, y, n, nb); return true;
-        case 14: q4k_lds_go<D, 14>(gd, bd, s, w, x, y, n, nb); return true;
-        case 16: q4k_lds_go<D, 16>(gd, bd, s, w, x, y, n, nb); return true;
-        default: return false;
-    }
-}
-
-hipError_t launch_q4k_lds(int depth, int rows, int waves, int64_t grid, const uint8_t* w, const float* x, float* y,
-                          int64_t n, int nb, hipStream_t s) {
-    const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
-    bool ok = false;
-    if (depth >= 6)
-        ok = q4k_lds_rows<6>(rows, gd, bd, s, w, x, y, n, nb);
-    else if (depth >= 4)
-        ok = q4k_lds_rows<4>(rows, gd, bd, s, w, x, y, n, nb);
-    else
-        ok = q4k_lds_rows<2>(rows, gd, bd, s, w, x, y, n, nb);
-    if (!ok) return hipErrorInvalidConfiguration;
-    return hipGetLastError();
-}
-
 hipError_t launch_q4k(int cpl, int ring, int rows, int waves, int64_t grid, const uint8_t* w, const float* x,
                       float* y, int64_t n, int nb, hipStream_t s) {
     const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
@@ -1303,20 +1142,6 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
     const int64_t lanes = nb * lanes_per_block(qtype, p.cpl);
     if (lanes > max_lanes(qtype, p.cpl)) return hipErrorInvalidConfiguration;
     p.waves = (int)((lanes + 63) / 64);
-    if (qtype == kTypeQ4K && p.lds > 0) {
-        if ((reinterpret_cast<uintptr_t>(w) & 15) || nb * 8 > 64 * kQ4KLdsWaves) return hipErrorInvalidConfiguration;
-        p.cpl = 1;
-        p.slices = 1;
-        p.waves = (int)((nb * 8 + 63) / 64);
-        if (p.rows_per_wg <= 0) p.rows_per_wg = pick_rows_q4k(n, p.waves);
-        if (!q4k_rows_ok(p.rows_per_wg)) return hipErrorInvalidConfiguration;
-        p.lds = p.lds >= 6 ? 6 : p.lds >= 4 ? 4 : 2;
-        p.unroll = p.lds < p.rows_per_wg ? p.lds : p.rows_per_wg;
-        p.grid = (n + p.rows_per_wg - 1) / p.rows_per_wg;
-        if (p.grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
-        if (plan) *plan = p;
-        return launch_q4k_lds(p.lds, p.rows_per_wg, p.waves, p.grid, w, x, y, n, (int)nb, stream);
-    }
     if (qtype == kTypeQ4K) {
         if (p.slices > 1) return hipErrorInvalidConfiguration;   // every row in one workgroup
         p.slices = 1;

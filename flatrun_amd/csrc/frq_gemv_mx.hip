@@ -201,7 +201,7 @@ __device__ __forceinline__ float block_per_weight(uint4 hd, uint4 q0, uint4 q1, 
     return acc;
 }
 
-template <int LMAX, int RT, int KS, bool HB>
+template <int LMAX, int RT, int KS, int DEPTH>
 __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __restrict__ w,
                                                             const float* __restrict__ x, float* __restrict__ y,
                                                             uint64_t* __restrict__ slots, int64_t n, int nb, int L,
@@ -227,13 +227,20 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
     const uint32_t row_bytes = (uint32_t)nb * kQ4KBytes;
     const auto rs = buffer_rsrc(w + row0 * (int64_t)row_bytes, (uint32_t)nrows * row_bytes);
 
-    for (int i = tid; i < kZero / 16; i += blockDim.x)
-        reinterpret_cast<uint4*>(lds + kTabAll)[i] = make_uint4(0, 0, 0, 0);
-    __syncthreads();
+    // The zero block that the inactive A lanes read is written before any
+    // wave reads it. With loads issued one block ahead (DEPTH < LMAX) every
+    // wave also issues its x loads before that barrier, so x is requested
+    // ahead of the workgroup's weights, and the barrier waits for the LDS
+    // writes only (no fence: the x loads stay in flight).
+    if constexpr (DEPTH >= LMAX) {
+        for (int i = tid; i < kZero / 16; i += blockDim.x)
+            reinterpret_cast<uint4*>(lds + kTabAll)[i] = make_uint4(0, 0, 0, 0);
+        __syncthreads();
+    }
 
     // x first (small, cache-resident): the digit split then waits for x only,
-    // while every weight load is still in flight. Blocks past the wave's
-    // slice re-read an earlier block of the row; their sums are dropped.
+    // while the weight loads are in flight. Blocks past the wave's slice
+    // re-read an earlier block of the row; their sums are dropped.
     float4 xv[LMAX];
 #pragma unroll
     for (int j = 0; j < LMAX; ++j) {
@@ -242,8 +249,13 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
         xv[j] = *reinterpret_cast<const float4*>(x + (int64_t)blk * kQKElems + 4 * lane);
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (DEPTH < LMAX) {
+        for (int i = tid; i < kZero / 16; i += blockDim.x)
+            reinterpret_cast<uint4*>(lds + kTabAll)[i] = make_uint4(0, 0, 0, 0);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    }
     uint4 hd[RT][LMAX], q0[RT][LMAX], q1[RT][LMAX];
-    uint4 hv[RT];   // HB: lane group g holds the header of the wave's block g
     uint32_t roffs[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
@@ -251,25 +263,35 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
         rr = rr < nrows ? rr : nrows - 1;
         roffs[t] = (uint32_t)rr * row_bytes;
     }
-    if constexpr (HB) {
+    // the weight loads of block j for every tile: header, qs 0..63, qs 64..127
+    auto issue = [&](auto jc) {
+        constexpr int j = decltype(jc)::value;
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            int blk = kb0 + b0 + (g < lw ? g : lw - 1);
-            blk = blk < 0 ? 0 : blk;
-            hv[t] = bload_b128(rs, roffs[t] + (uint32_t)blk * kQ4KBytes);
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < RT; ++t) {
-#pragma unroll
-        for (int j = 0; j < LMAX; ++j) {
             int blk = kb0 + b0 + (j < lw ? j : lw - 1);
             blk = blk < 0 ? 0 : blk;                     // past the row: zeros or a neighbour row, dropped
             const uint32_t off = roffs[t] + (uint32_t)blk * kQ4KBytes;
-            if constexpr (!HB) hd[t][j] = bload_b128(rs, off);
+            hd[t][j] = bload_b128(rs, off);
             q0[t][j] = bload_b128(rs, off + 16 + 16 * g);
             q1[t][j] = bload_b128(rs, off + 80 + 16 * g);
         }
+    };
+    if constexpr (DEPTH >= LMAX) {
+        // every block at once, tile-outer / block-inner (the issue order that measured fastest here)
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+#pragma unroll
+            for (int j = 0; j < LMAX; ++j) {
+                int blk = kb0 + b0 + (j < lw ? j : lw - 1);
+                blk = blk < 0 ? 0 : blk;
+                const uint32_t off = roffs[t] + (uint32_t)blk * kQ4KBytes;
+                hd[t][j] = bload_b128(rs, off);
+                q0[t][j] = bload_b128(rs, off + 16 + 16 * g);
+                q1[t][j] = bload_b128(rs, off + 80 + 16 * g);
+            }
+        }
+    } else {
+        static_for<0, DEPTH>([&](auto jc) { issue(jc); });
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -299,19 +321,6 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
             if (__builtin_amdgcn_ballot_w64(!dg.exact) != 0) inexact |= 1u << j;
         }
     }
-    if constexpr (HB) {   // block j's header from lane group j to every lane of the row
-#pragma unroll
-        for (int t = 0; t < RT; ++t)
-#pragma unroll
-            for (int j = 0; j < LMAX; ++j) {
-                const int src = 4 * (c + 16 * j);
-                hd[t][j] = make_uint4((uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)hv[t].x),
-                                      (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)hv[t].y),
-                                      (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)hv[t].z),
-                                      (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)hv[t].w));
-            }
-    }
-
     // ---- products. Lane (ar = l & 15, akk = l >> 4) of the A operand of
     // MFMA m carries digit ar % 8 of k-group akk when ar / 8 == akk / 2, and
     // zeros otherwise; the digit table and the zero block are read at the
@@ -329,14 +338,19 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
     double acc[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) acc[t] = 0.0;
-#pragma unroll
-    for (int j = 0; j < LMAX; ++j) {
-        if (j >= lw) continue;                           // wave-uniform
+    static_for<0, LMAX>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        if constexpr (DEPTH < LMAX && j + DEPTH < LMAX) {   // block j + DEPTH's loads before block j's work
+            __builtin_amdgcn_sched_barrier(0);
+            issue(Int<j + DEPTH>{});
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (j >= lw) return;                             // wave-uniform
         if (inexact & (1u << j)) {                       // wave-uniform: per-weight fp32 for this block
             const float* xb = x + (int64_t)(kb0 + b0 + j) * kQKElems;
 #pragma unroll
             for (int t = 0; t < RT; ++t) acc[t] += (double)block_per_weight(hd[t][j], q0[t][j], q1[t][j], xb, g);
-            continue;
+            return;
         }
         const uint8_t* ab_e = abase_e + j * kTabBlock;
         const uint8_t* ab_o = abase_o + j * kTabBlock;
@@ -385,7 +399,7 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mx_kernel(const uint8_t* __res
                 acc[t] = sub_block_add(acc[t], dt[t], dmt[t], sc, mn, digit_sum(c), dx, pw);
             }
         });
-    }
+    });
 #pragma unroll
     for (int t = 0; t < RT; ++t) red[(t * kMxMaxWaves + wave) * 64 + lane] = (float)acc[t];
     __syncthreads();
@@ -608,24 +622,27 @@ __global__ void __launch_bounds__(1024) gemv_q1_0_mx_kernel(const uint8_t* __res
 }
 
 template <int LMAX, int RT, int KS>
-void mx_go(bool hb, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, uint64_t* slots,
+void mx_go(bool ahead, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, uint64_t* slots,
            int64_t n, int nb, int L, int TR) {
-    if (hb)
-        gemv_q4_k_mx_kernel<LMAX, RT, KS, true><<<gd, bd, 0, s>>>(w, x, y, slots, n, nb, L, TR);
-    else
-        gemv_q4_k_mx_kernel<LMAX, RT, KS, false><<<gd, bd, 0, s>>>(w, x, y, slots, n, nb, L, TR);
+    if constexpr (LMAX > 1) {
+        if (ahead) {
+            gemv_q4_k_mx_kernel<LMAX, RT, KS, 1><<<gd, bd, 0, s>>>(w, x, y, slots, n, nb, L, TR);
+            return;
+        }
+    }
+    gemv_q4_k_mx_kernel<LMAX, RT, KS, LMAX><<<gd, bd, 0, s>>>(w, x, y, slots, n, nb, L, TR);
 }
 
 template <int RT, int KS>
-bool mx_by_l(int L, bool hb, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y,
+bool mx_by_l(int L, bool ahead, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y,
              uint64_t* slots, int64_t n, int nb, int TR) {
     switch (L) {
-        case 1: mx_go<1, RT, KS>(hb, gd, bd, s, w, x, y, slots, n, nb, L, TR); return true;
-        case 2: mx_go<2, RT, KS>(hb, gd, bd, s, w, x, y, slots, n, nb, L, TR); return true;
-        case 3: mx_go<3, RT, KS>(hb, gd, bd, s, w, x, y, slots, n, nb, L, TR); return true;
+        case 1: mx_go<1, RT, KS>(ahead, gd, bd, s, w, x, y, slots, n, nb, L, TR); return true;
+        case 2: mx_go<2, RT, KS>(ahead, gd, bd, s, w, x, y, slots, n, nb, L, TR); return true;
+        case 3: mx_go<3, RT, KS>(ahead, gd, bd, s, w, x, y, slots, n, nb, L, TR); return true;
         case 4:
             if constexpr (RT == 1) {   // two tiles of four blocks do not fit 128 VGPRs (plan_gemv_mx)
-                mx_go<4, RT, KS>(hb, gd, bd, s, w, x, y, slots, n, nb, L, TR);
+                mx_go<4, RT, KS>(ahead, gd, bd, s, w, x, y, slots, n, nb, L, TR);
                 return true;
             }
             return false;
@@ -658,11 +675,15 @@ bool plan_gemv_mx(int64_t n, int64_t k, MxPlan* p) {
         if (p->tiles == 2 && p->rows < 2) p->rows = 2;
     }
     if (p->rows < 1 || p->rows > 16 * p->tiles || (p->tiles == 2 && p->rows < 2)) return false;
-    // per-block header loads; the one-load header layout (1) measured slower
-    // with the fp64 epilogue for every shape (18944 x 3584: 12.1 vs 11.9 us,
-    // 3584 x 18944: 14.3 vs 12.6 us)
-    if (p->layout < 0) p->layout = 0;
-    if (p->layout != 0 && p->layout != 1) return false;
+    // load depth: every block's weight loads issued before the x split, or
+    // one block ahead of the products (the x of every wave requested before
+    // the workgroup's weights). Graph-replayed, us, all loads / one ahead:
+    // 3584 x 18944 12.76 / 12.45, 5120 x 13824 20.8 / 19.0, 3584 x 3584
+    // 4.74 / 4.63, 8192 x 11008 14.6 / 15.3: ahead when a wave holds three
+    // or more blocks of a half row, or of a one-tile row set.
+    if (p->depth <= 0) p->depth = (p->blocks >= 3 && (p->ksplit == 2 || p->tiles == 1)) ? 1 : p->blocks;
+    if (p->depth > p->blocks) p->depth = p->blocks;
+    if (p->depth != 1 && p->depth != p->blocks) return false;
     p->grid = (n + p->rows - 1) / p->rows * p->ksplit;
     return p->grid <= 0x7FFFFFFF;
 }
@@ -690,13 +711,13 @@ hipError_t launch_gemv_mx(const uint8_t* w, const float* x, float* y, int64_t n,
     const int nb = (int)(k / kQKElems);
     const dim3 g((unsigned)p.grid), b(64 * p.waves);
     bool ok = false;
-    const bool hb = p.layout == 1;
+    const bool ahead = p.depth < p.blocks;
     if (p.ksplit == 1)
-        ok = p.tiles == 1 ? mx_by_l<1, 1>(p.blocks, hb, g, b, stream, w, x, y, slots, n, nb, p.rows)
-                          : mx_by_l<2, 1>(p.blocks, hb, g, b, stream, w, x, y, slots, n, nb, p.rows);
+        ok = p.tiles == 1 ? mx_by_l<1, 1>(p.blocks, ahead, g, b, stream, w, x, y, slots, n, nb, p.rows)
+                          : mx_by_l<2, 1>(p.blocks, ahead, g, b, stream, w, x, y, slots, n, nb, p.rows);
     else
-        ok = p.tiles == 1 ? mx_by_l<1, 2>(p.blocks, hb, g, b, stream, w, x, y, slots, n, nb, p.rows)
-                          : mx_by_l<2, 2>(p.blocks, hb, g, b, stream, w, x, y, slots, n, nb, p.rows);
+        ok = p.tiles == 1 ? mx_by_l<1, 2>(p.blocks, ahead, g, b, stream, w, x, y, slots, n, nb, p.rows)
+                          : mx_by_l<2, 2>(p.blocks, ahead, g, b, stream, w, x, y, slots, n, nb, p.rows);
     if (!ok) return hipErrorInvalidConfiguration;
     return hipGetLastError();
 }

@@ -24,7 +24,6 @@ struct GemvPlan {
     int rows_per_wg = 0;    // output rows owned by one workgroup
     int unroll = 0;         // rows whose loads are issued together
     int slices = 0;         // 1: every row in one workgroup (0 = choose; nothing else is accepted)
-    int lds = 0;            // Q4_K: > 0 = row ring of that many rows in LDS instead of registers
     int64_t grid = 0;       // workgroups
 };
 
@@ -66,8 +65,8 @@ struct MxPlan {
     int rows = 0;      // output rows per workgroup (<= 16 * tiles)
     int tiles = 0;     // 16-row MFMA tiles per wavefront: 1 or 2
     int ksplit = 0;    // workgroups per row set: 1 or 2
-    int layout = -1;   // weight loads: 0 header / qs 0..63 / qs 64..127 per block, 1 the headers of a
-                       // wavefront's blocks in one load (frq_gemv_mx.hip); < 0 = choose
+    int depth = 0;     // blocks whose weight loads a wavefront issues before its x split: 1 (then
+                       // block j + 1's loads before block j's products) or all of them; 0 = choose
     int blocks = 0;    // blocks per wavefront (derived, <= 4)
     int waves = 0;     // wavefronts per workgroup (derived)
     int64_t grid = 0;  // workgroups (derived)

@@ -29,6 +29,7 @@ import collections
 import hashlib
 import mmap
 import threading
+import weakref
 
 import numpy as np
 
@@ -46,46 +47,67 @@ def digest(raw: np.ndarray) -> bytes:
     return hashlib.blake2b(flat, digest_size=16).digest()
 
 
-def file_backed(raw: np.ndarray) -> bool:
-    """True when the array's memory belongs to an ``mmap.mmap`` that the
-    array keeps alive (through ``.base`` / ``memoryview.obj`` links)."""
+def _backing_mmap(raw: np.ndarray):
+    """The ``mmap.mmap`` whose memory the array views and keeps alive
+    (through ``.base`` / ``memoryview.obj`` links), else None."""
     o = raw
     for _ in range(16):
         o = o.obj if isinstance(o, memoryview) else getattr(o, "base", None)
         if o is None:
-            return False
+            return None
         if isinstance(o, mmap.mmap):
-            return True
-    return False
+            return o
+    return None
+
+
+def file_backed(raw: np.ndarray) -> bool:
+    """True when the array's memory belongs to an ``mmap.mmap`` that the
+    array keeps alive."""
+    return _backing_mmap(raw) is not None
 
 
 class KeyMemo:
-    """Content keys of file-backed arrays by (address, nbytes). Each entry
-    holds its array, so the mapping behind an address stays in place (and
-    holds those bytes) while the entry lives; at most `limit` entries, least
-    recently used out."""
+    """Content keys of file-backed arrays by (mapping, offset, nbytes).
+
+    The memo holds no array and no mapping: entries are grouped per mapping
+    in a weak-keyed table, so a mapping closed and collected takes its
+    entries with it, and closing a GGUF file is never blocked by the memo.
+    While an array over a mapping lives, the mapping cannot be closed, so the
+    bytes at an offset are the bytes that were hashed -- provided the file
+    is not rewritten on disk while it is mapped (a shared mapping shows such
+    writes, and the memo would then serve the old key). At most `limit`
+    entries per mapping, least recently used out."""
 
     def __init__(self, limit: int = 4096):
         self.limit = int(limit)
-        self._m: collections.OrderedDict = collections.OrderedDict()
+        self._m: "weakref.WeakKeyDictionary[mmap.mmap, collections.OrderedDict]" = weakref.WeakKeyDictionary()
         self._lock = threading.Lock()
 
     def key(self, raw: np.ndarray) -> tuple[int, bytes]:
         flat = raw.reshape(-1)
-        if flat.nbytes and not raw.flags.writeable and file_backed(raw):
-            addr = (int(flat.ctypes.data), int(flat.nbytes))
-            with self._lock:
-                hit = self._m.get(addr)
-                if hit is not None:
-                    self._m.move_to_end(addr)
-                    return hit[1]
-            k = (int(flat.nbytes), digest(flat))
-            with self._lock:
-                self._m[addr] = (raw, k)
-                while len(self._m) > self.limit:
-                    self._m.popitem(last=False)
-            return k
-        return (int(flat.nbytes), digest(flat))
+        mm = _backing_mmap(raw) if flat.nbytes and not raw.flags.writeable else None
+        if mm is None:
+            return (int(flat.nbytes), digest(flat))
+        probe = np.frombuffer(mm, np.uint8, count=1)     # the mapping's base address (a transient export)
+        at = (int(flat.ctypes.data) - int(probe.ctypes.data), int(flat.nbytes))
+        del probe
+        with self._lock:
+            table = self._m.get(mm)
+            hit = table.get(at) if table is not None else None
+            if hit is not None:
+                table.move_to_end(at)
+                return hit
+        k = (int(flat.nbytes), digest(flat))
+        with self._lock:
+            table = self._m.setdefault(mm, collections.OrderedDict())
+            table[at] = k
+            while len(table) > self.limit:
+                table.popitem(last=False)
+        return k
+
+    def entries(self) -> int:
+        with self._lock:
+            return sum(len(t) for t in self._m.values())
 
 
 _memo = KeyMemo()
@@ -108,9 +130,16 @@ class WeightCache:
         self.hits = self.misses = 0
         self._entries: collections.OrderedDict = collections.OrderedDict()
 
-    def lookup(self, raw: np.ndarray, upload):
+    def lookup(self, raw: np.ndarray, upload, held=()):
         """The resident copy of `raw`, made by ``upload(raw)`` on a miss;
-        None if `raw` is empty or larger than the whole cache."""
+        None if `raw` is empty or larger than the whole cache, or if the
+        entries in `held` leave no room for it.
+
+        Eviction frees device memory at once. `held` names the entries the
+        caller has already looked up for a launch it has not run yet (the
+        parts of a grouped call): they are never evicted here, so a group
+        whose parts together exceed the capacity caches what fits and the
+        caller uploads the rest for that call alone."""
         flat = raw.reshape(-1)
         if flat.nbytes == 0 or flat.nbytes > self.capacity:
             return None
@@ -121,10 +150,19 @@ class WeightCache:
             self.hits += 1
             return hit
         self.misses += 1
-        while self._entries and self.bytes + flat.nbytes > self.capacity:
-            _, old = self._entries.popitem(last=False)
-            self.bytes -= old.nbytes
-            old.buffer.free()
+        keep = {id(h) for h in held if h is not None}
+        if self.bytes + flat.nbytes > self.capacity:
+            for old_key in list(self._entries):               # least recently used first
+                if self.bytes + flat.nbytes <= self.capacity:
+                    break
+                old = self._entries[old_key]
+                if id(old) in keep:
+                    continue
+                del self._entries[old_key]
+                self.bytes -= old.nbytes
+                old.buffer.free()
+            if self.bytes + flat.nbytes > self.capacity:
+                return None
         dw = upload(flat)
         self._entries[key] = dw
         self.bytes += flat.nbytes

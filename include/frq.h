@@ -188,10 +188,14 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  * rows are split over two workgroups: n <= 131072) and 3 MiB of split-K
  * partials (n x slices x 4 bytes, rows longer than one workgroup). A batch-1
  * shape that needs more is refused with FRQ_ERR_UNSUPPORTED before anything
- * is launched. The batched GEMM (batch >= 2) splits k only as far as its
- * partials (splits x batch x n x 4 bytes) fit in the 3 MiB, so it never
- * refuses; where that is fewer splits than frq_dev_gemv takes, the bits
- * differ from frq_dev_gemv's within the same bound. Every call on a GPU shares that GPU's array: calls that overlap
+ * is launched. A batch that takes the small-M matvec (2 to 6 rows of Q4_K or
+ * Q8_0, 2 to 10 of Q6_K, on matrices it accepts) needs no scratch; a batch
+ * that takes the batched GEMM (4 or more rows of Q4_K, Q6_K, Q8_0) splits k
+ * only as far as its partials (splits x batch x n x 4 bytes) fit in the
+ * 3 MiB, so neither is refused; where the GEMM splits less than
+ * frq_dev_gemv would, the bits differ from frq_dev_gemv's within the same
+ * bound. Any other batch runs one GEMV per row and is refused as batch 1
+ * would be (for example 2 or 3 rows of Q4_K with k > 24576). Every call on a GPU shares that GPU's array: calls that overlap
  * on one GPU (different streams or threads) race; calls ordered on one
  * stream do not. The first call on a device clears the slots with a kernel
  * on `stream`; every launch leaves them zero. */
@@ -204,17 +208,15 @@ int frq_dev_gemv_noalloc(int qtype, const void* w, size_t w_bytes, const float* 
  *   kernel        FRQ_GEMV_AUTO, FRQ_GEMV_SPLITK (one wavefront per
  *                 (row block, K-slice) work item, deterministic split-K
  *                 fixup) or FRQ_GEMV_ROWS (one workgroup spans all of k)
- *                 or FRQ_GEMV_ROWS_LDS (Q4_K: as ROWS, rows staged through
- *                 an LDS ring of `unroll` rows by direct-to-LDS loads)
  *                 or FRQ_GEMV_MX (the matrix-core kernel, Q4_K, k <= 32768:
  *                 `rows` = output rows per workgroup (<= 16 per tile),
  *                 `cpl` = 16-row tiles per wavefront (1 or 2), `slices` =
- *                 workgroups per row (1: k <= 16384, or 2 halves of k), 0 =
- *                 choose; on return `unroll` = blocks per wavefront)
- *                 or FRQ_GEMV_MX_H (the same with the block headers of a
- *                 wavefront's blocks in one load per row, shared across
- *                 lanes with ds_bpermute). AUTO takes the kernel
- *                 frq_dev_gemv takes.
+ *                 workgroups per row (1: k <= 16384, or 2 halves of k),
+ *                 `unroll` = load depth: 1 = each wavefront issues block
+ *                 j + 1's weight loads before block j's products, >= its
+ *                 blocks = all of them before its x split; 0 = choose).
+ *                 AUTO takes the kernel frq_dev_gemv takes. Other values
+ *                 are refused with FRQ_ERR_INVALID.
  *   cpl           work unit per lane (format specific); with ROWS and
  *                 Q1_0, 16 selects the matrix-core Q1_0 kernel (`rows` <=
  *                 16 per workgroup, `unroll` = 128-element blocks per
@@ -225,8 +227,7 @@ int frq_dev_gemv_noalloc(int qtype, const void* w, size_t w_bytes, const float* 
  *                 kernels (an input of 0 or 1; anything else is rejected)
  *   waves_per_wg  wavefronts per workgroup (output)
  *   items         work items / workgroups launched (output)              */
-enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2, FRQ_GEMV_ROWS_LDS = 3, FRQ_GEMV_MX = 4,
-       FRQ_GEMV_MX_H = 5 };
+enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2, FRQ_GEMV_MX = 4 };
 typedef struct {
     int32_t kernel, cpl, rows, unroll, slices, waves_per_wg;
     int64_t items;

@@ -91,11 +91,11 @@ def test_default_path(frq, q, n, k):
                                    ("Q6_K", 64, 4096), ("Q6_K", 33, 14336), ("Q8_0", 70, 4096),
                                    ("Q8_0", 48, 896)])
 def test_every_geometry(frq, q, n, k):
-    """Element-wise (register and LDS rings) and split-K kernels, each work
+    """Element-wise (register ring) and split-K kernels, each work
     unit size, rows per workgroup and ring depth the library accepts."""
     raw, cols = _input(q, n, k, seed=3 * n + k)
     x = outlier_x(k, cols, seed=k + 1)
-    kernels = [_lib.GEMV_SPLITK, _lib.GEMV_ROWS] + ([_lib.GEMV_ROWS_LDS] if q == "Q4_K" else [])
+    kernels = [_lib.GEMV_SPLITK, _lib.GEMV_ROWS]
     runs = 0
     for kernel in kernels:
         for cpl in (1, 2, 4, 8):
@@ -111,11 +111,11 @@ def test_every_geometry(frq, q, n, k):
 
 
 @pytest.mark.parametrize("n,k", [(2048, 4096), (1536, 8960), (3584, 18944), (18944, 3584)])
-@pytest.mark.parametrize("kernel", ["GEMV_MX", "GEMV_MX_H"])
-def test_matrix_core_layouts(frq, n, k, kernel):
+@pytest.mark.parametrize("depth", [1, 4])
+def test_matrix_core_load_depths(frq, n, k, depth):
     raw, cols = _input("Q4_K", n, k, seed=n)
     x = outlier_x(k, cols, seed=n + 1)
-    y, cfg = _run("Q4_K", raw, x, n, k, kernel=getattr(_lib, kernel))
+    y, cfg = _run("Q4_K", raw, x, n, k, kernel=_lib.GEMV_MX, unroll=depth)
     _check("Q4_K", raw, x, n, k, y, f"Q4_K {n}x{k} {cfg}")
 
 

@@ -142,6 +142,30 @@ def test_facade_matmul_fused(frq):
         nb.matmul_fused(np.zeros(k, np.float32), parts * 2, k)
 
 
+def test_facade_matmul_fused_small_weight_cache(frq):
+    """A weight cache smaller than the group: looking up a later part must
+    not free an earlier part of the same call before the launch. Parts that
+    do not fit beside the held ones go up for the call alone; the result is
+    the uncached one bit for bit, on repeated calls (hits and misses mixed)."""
+    k = 4096
+    parts = [(q, synth.make_blocks(q, n, k, seed=40 + i), n) for i, (q, n) in enumerate(LLAMA_QKV)]
+    sizes = [r.nbytes for _, r, _ in parts]                  # 9.4 MB, 2.4 MB, 3.4 MB
+    plain = NativeBackend(weight_cache=False)
+    small = NativeBackend(weight_cache=sizes[0] + sizes[1] // 2)   # holds q, not q and k
+    x = synth.make_x(k, seed=5)
+    want = plain.matmul_fused(x, parts, k)
+    for rep in range(3):
+        got = small.matmul_fused(x, parts, k)
+        assert bits_equal(got, want), rep
+    st = small.cache_stats()
+    assert st["bytes"] <= st["capacity"] and st["entries"] >= 1
+    gu = [(q, synth.make_blocks(q, n, k, seed=60 + i), n) for i, (q, n) in enumerate(LLAMA_GATE_UP)]
+    one = NativeBackend(weight_cache=gu[0][1].nbytes + 1024)  # gate and up (58.7 MB each) never fit together
+    want = plain.matmul_fused(x, gu, k)
+    for rep in range(2):
+        assert bits_equal(one.matmul_fused(x, gu, k), want), rep
+
+
 def test_group_graph_replay(frq):
     k = 4096
     spec = LLAMA_QKV

@@ -25,17 +25,18 @@ from oracle import gguf_np as G
 pytestmark = pytest.mark.gpu
 
 
-# every forced launch runs each weight layout of the kernel: per block
-# (header, qs 0..63, qs 64..127), and the headers of a wavefront's blocks in
-# one load
-_KERNEL = [_lib.GEMV_MX]
+# every forced launch runs each load depth of the kernel: all of a
+# wavefront's weight loads issued before its x split ("all": unroll >= its
+# blocks), and block j + 1's loads issued before block j's products ("ahead":
+# unroll = 1)
+_MX = {"kernel": _lib.GEMV_MX, "unroll": 4}
 
 
-@pytest.fixture(autouse=True, params=["blocks", "headers"])
-def mx_layout(request):
-    _KERNEL[0] = _lib.GEMV_MX if request.param == "blocks" else _lib.GEMV_MX_H
-    yield _KERNEL[0]
-    _KERNEL[0] = _lib.GEMV_MX
+@pytest.fixture(autouse=True, params=["all", "ahead"])
+def mx_depth(request):
+    _MX["unroll"] = 4 if request.param == "all" else 1
+    yield dict(_MX)
+    _MX["unroll"] = 4
 
 
 def run_mx(raw, x, n, k, rows=0, tiles=0, ksplit=0, stream=None):
@@ -45,7 +46,7 @@ def run_mx(raw, x, n, k, rows=0, tiles=0, ksplit=0, stream=None):
     yd = device.DeviceBuffer(max(4, 4 * n))
     try:
         _lib.check(_lib.lib().frq_memcpy_h2d(yd.ptr, np.full(n, np.nan, np.float32).ctypes.data, 4 * n))
-        cfg = device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_KERNEL[0], rows=rows, cpl=tiles, slices=ksplit,
+        cfg = device.gemv_tuned("Q4_K", w, xd, yd, n, k, **_MX, rows=rows, cpl=tiles, slices=ksplit,
                                 stream=stream)
         device.synchronize()
         return yd.to_host(np.float32)[:n], cfg
@@ -99,7 +100,7 @@ def test_mx_shapes_tiles_rows(frq, n, k):
             except RuntimeError:
                 assert tiles == 2 and -(-((nb + ks - 1) // ks) // 16) > 3      # two tiles need <= 3 blocks per wave
                 continue
-            assert cfg["kernel"] == _KERNEL[0] and cfg["rows"] == rows and cfg["cpl"] == tiles
+            assert cfg["kernel"] == _lib.GEMV_MX and cfg["rows"] == rows and cfg["cpl"] == tiles
             assert cfg["slices"] == ks and cfg["items"] == -(-n // rows) * ks
             if ref is None:
                 oracle_check(y, raw, x, n, k, f"mx {n}x{k} ks={ks}")
@@ -125,7 +126,7 @@ def test_mx_default_path_full_size(frq, q, n, k):
         oracle_check(y, raw, x, n, k, f"default {q} {n}x{k}")
         cfg = device.gemv_tuned(q, w, xd, yd, n, k)
         device.synchronize()
-        assert cfg["kernel"] in (_lib.GEMV_MX, _lib.GEMV_MX_H) and 6 <= cfg["rows"] <= 32
+        assert cfg["kernel"] == _lib.GEMV_MX and 6 <= cfg["rows"] <= 32
         assert bits_equal(yd.to_host(np.float32), y)
     finally:
         w.free()
@@ -268,15 +269,15 @@ def test_mx_repeat_and_graph_replay(frq):
     yd = device.DeviceBuffer(4 * n)
     s = device.Stream()
     try:
-        device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_KERNEL[0], stream=s)
+        device.gemv_tuned("Q4_K", w, xd, yd, n, k, **_MX, stream=s)
         s.synchronize()
         ref = yd.to_host(np.float32)
         for _ in range(10):
-            device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_KERNEL[0], stream=s)
+            device.gemv_tuned("Q4_K", w, xd, yd, n, k, **_MX, stream=s)
         s.synchronize()
         assert bits_equal(yd.to_host(np.float32), ref)
         with device.Graph.capture(s) as cap:
-            device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_KERNEL[0], stream=s)
+            device.gemv_tuned("Q4_K", w, xd, yd, n, k, **_MX, stream=s)
         try:
             for _ in range(3):
                 _lib.check(_lib.lib().frq_memcpy_h2d(yd.ptr, np.full(n, np.nan, np.float32).ctypes.data, 4 * n))
@@ -328,7 +329,7 @@ def test_mx_k_split_halves_any_order(frq):
                          device.DeviceBuffer(4 * n)))
         ref = []
         for n, k, raw, x, w, xd, yd in bufs:
-            cfg = device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_KERNEL[0], slices=2, stream=s)
+            cfg = device.gemv_tuned("Q4_K", w, xd, yd, n, k, **_MX, slices=2, stream=s)
             assert cfg["slices"] == 2
             s.synchronize()
             y = yd.to_host(np.float32)
@@ -336,7 +337,7 @@ def test_mx_k_split_halves_any_order(frq):
             ref.append(y)
         for _ in range(30):
             for n, k, raw, x, w, xd, yd in bufs:
-                device.gemv_tuned("Q4_K", w, xd, yd, n, k, kernel=_KERNEL[0], slices=2, stream=s)
+                device.gemv_tuned("Q4_K", w, xd, yd, n, k, **_MX, slices=2, stream=s)
         s.synchronize()
         for (n, k, *_, yd), r in zip(bufs, ref):
             assert bits_equal(yd.to_host(np.float32), r)
@@ -357,17 +358,17 @@ def test_mx_rejects(frq):
     q6 = device.DeviceBuffer.from_host(synth.make_blocks("Q6_K", 4, 512, seed=1))
     try:
         with pytest.raises(RuntimeError):                      # 129 blocks: beyond 2 halves x 16 waves x 4 blocks
-            device.gemv_tuned("Q4_K", w, xd, yd, 4, 256 * 129, kernel=_KERNEL[0])
+            device.gemv_tuned("Q4_K", w, xd, yd, 4, 256 * 129, **_MX)
         with pytest.raises(RuntimeError):                      # 65 blocks in one workgroup
-            device.gemv_tuned("Q4_K", w, xd, yd, 4, 256 * 65, kernel=_KERNEL[0], slices=1, w_bytes=4 * 65 * 144)
+            device.gemv_tuned("Q4_K", w, xd, yd, 4, 256 * 65, **_MX, slices=1, w_bytes=4 * 65 * 144)
         with pytest.raises(RuntimeError):                      # rows per workgroup above 16 per tile
-            device.gemv_tuned("Q4_K", w, xd, yd, 4, 256, kernel=_KERNEL[0], rows=17, cpl=1, w_bytes=4 * 144)
+            device.gemv_tuned("Q4_K", w, xd, yd, 4, 256, **_MX, rows=17, cpl=1, w_bytes=4 * 144)
         with pytest.raises(RuntimeError):                      # three tiles
-            device.gemv_tuned("Q4_K", w, xd, yd, 4, 256, kernel=_KERNEL[0], cpl=3, w_bytes=4 * 144)
+            device.gemv_tuned("Q4_K", w, xd, yd, 4, 256, **_MX, cpl=3, w_bytes=4 * 144)
         with pytest.raises(RuntimeError):                      # Q4_K only
-            device.gemv_tuned("Q5_K", q5, xd, yd, 4, 512, kernel=_KERNEL[0])
+            device.gemv_tuned("Q5_K", q5, xd, yd, 4, 512, **_MX)
         with pytest.raises(RuntimeError):
-            device.gemv_tuned("Q6_K", q6, xd, yd, 4, 512, kernel=_KERNEL[0])
+            device.gemv_tuned("Q6_K", q6, xd, yd, 4, 512, **_MX)
         # the default path still serves k beyond the matrix-core limits
         device.gemv("Q4_K", w, xd, yd, 4, 256 * 129)
         device.synchronize()

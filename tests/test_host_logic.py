@@ -44,3 +44,43 @@ def test_group_fusable_rule():
     assert fus([("Q4_K", a16), ("Q4_K", a16)], 32768)
     assert not fus([("Q4_K", a16), ("Q4_K", a16)], 32768 + 256)  # row longer than one workgroup
     assert not fus([("Q4_K", a16), ("Q4_K", a16)], 300)          # k not a whole number of blocks
+
+
+def _reference_try_kernel(kernel, fallback):
+    """The reference runtime's dispatch (runtime/backend.py:259-268): call the
+    native kernel, recompute in NumPy on RuntimeError."""
+    try:
+        return kernel()
+    except RuntimeError:
+        return fallback()
+
+
+def test_device_failures_are_not_swallowed_by_the_fallback():
+    """Refused arguments (shape, size, alignment, type, no device) raise
+    FrqError, a RuntimeError, so the reference falls back as it does for its
+    own kernels; a HIP runtime failure raises FrqDeviceError, which the
+    fallback does not catch."""
+    import pytest
+
+    from flatrun_amd import FrqDeviceError, FrqError, _lib
+
+    for code in (_lib.ERR_INVALID, _lib.ERR_SHAPE, _lib.ERR_SIZE, _lib.ERR_UNSUPPORTED, _lib.ERR_NO_DEVICE,
+                 _lib.ERR_ALIGN):
+        e = _lib.error_for(code, "refused")
+        assert isinstance(e, FrqError) and isinstance(e, RuntimeError) and e.code == code
+
+        def refuse(e=e):
+            raise e
+        assert _reference_try_kernel(refuse, lambda: "numpy") == "numpy"
+    e = _lib.error_for(_lib.ERR_HIP, "hipLaunchKernel: an illegal memory access was encountered")
+    assert isinstance(e, FrqDeviceError) and not isinstance(e, RuntimeError) and e.code == _lib.ERR_HIP
+
+    def fail():
+        raise e
+    with pytest.raises(FrqDeviceError, match="FRQ_ERR_HIP"):
+        _reference_try_kernel(fail, lambda: "numpy")
+    if _lib.load_error() is None:             # through check(), with the library's own last-error text
+        with pytest.raises(FrqDeviceError):
+            _lib.check(_lib.ERR_HIP)
+        with pytest.raises(FrqError):
+            _lib.check(_lib.ERR_SHAPE)

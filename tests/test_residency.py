@@ -74,7 +74,30 @@ def test_key_memo_hashes_file_backed_views_once(mapped, monkeypatch):
     assert memo.key(copy) == k1 and memo.key(copy) == k1 and calls == [4096] * 3   # copies: every call
     for off in (4096, 8192, 12288):                          # LRU bound
         memo.key(np.frombuffer(mm, dtype=np.uint8, count=4096, offset=off))
-    assert len(memo._m) == 2
+    assert memo.entries() == 2
+
+
+def test_key_memo_holds_no_mapping(tmp_path):
+    """The memo keeps neither the arrays nor their mapping: once the views
+    are gone the file closes (a GGUF file's close is not blocked), and a
+    collected mapping takes its entries with it."""
+    import gc
+
+    p = tmp_path / "m.bin"
+    p.write_bytes(bytes(range(256)) * 64)
+    f = open(p, "rb")
+    mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+    memo = residency.KeyMemo()
+    v = np.frombuffer(mm, dtype=np.uint8, count=1024, offset=2048)
+    k = memo.key(v)
+    assert k == (1024, residency.digest(np.frombuffer(bytes(range(256)) * 4, dtype=np.uint8)))
+    assert memo.entries() == 1
+    del v
+    mm.close()                                               # no BufferError: nothing of the memo holds it
+    f.close()
+    del mm
+    gc.collect()
+    assert memo.entries() == 0
 
 
 class _FakeBuf:
@@ -109,6 +132,26 @@ def test_weight_cache_by_content():
     assert cache.lookup(np.zeros(0, np.uint8), _FakeDW) is None
     cache.clear()
     assert da.buffer.freed and len(cache) == 0 and cache.bytes == 0
+
+
+def test_weight_cache_keeps_held_entries():
+    """A grouped call looks up each part before its one launch: a later
+    part's lookup must not evict (free) an earlier part of the same call,
+    even when the parts together exceed the capacity; it then returns None
+    (the caller uploads that part for the call alone) and frees nothing."""
+    rng = np.random.default_rng(3)
+    a, b, c = (rng.integers(0, 256, 1000, dtype=np.uint8) for _ in range(3))
+    cache = residency.WeightCache(1500)
+    da = cache.lookup(a, _FakeDW)
+    assert cache.lookup(b, _FakeDW, held=[da]) is None          # no room beside the held entry
+    assert not da.buffer.freed and len(cache) == 1 and cache.bytes == 1000
+    db = cache.lookup(b, _FakeDW)                               # nothing held: a is evicted
+    assert da.buffer.freed and len(cache) == 1
+    cache2 = residency.WeightCache(2500)
+    d1, d2 = cache2.lookup(a, _FakeDW), cache2.lookup(b, _FakeDW)
+    d3 = cache2.lookup(c, _FakeDW, held=[d1])                   # evicts the unheld b, keeps a
+    assert d3 is not None and not d1.buffer.freed and d2.buffer.freed and cache2.bytes == 2000
+    assert db is not None
 
 
 def _drive(plan, p):

@@ -108,16 +108,19 @@ def test_noalloc_refuses_oversized_scratch(frq):
     for b in (pw, px, py):
         b.free()
     slices = cfg["slices"]
-    cases.append(("Q4_K", (3 << 20) // (4 * slices) + 64, 33024))
-    for q, n, k in cases:
+    cases.append(("Q4_K", (3 << 20) // (4 * slices) + 64, 33024, 1))
+    # two rows of a matrix the small-M kernel does not take (k > 24576) run
+    # one GEMV per row: the same per-row scratch, refused the same way
+    cases.append(("Q4_K", (3 << 20) // (4 * slices) + 64, 33024, 2))
+    for q, n, k, batch in (c if len(c) == 4 else c + (1,) for c in cases):
         wbytes = synth.nbytes(q, n, k)
         w = device.DeviceBuffer(wbytes)
-        xd = device.DeviceBuffer(4 * k)
-        yd = device.DeviceBuffer(4 * n)
+        xd = device.DeviceBuffer(4 * k * batch)
+        yd = device.DeviceBuffer(4 * n * batch)
         try:
-            mark = np.full(n, 7.0, np.float32)
+            mark = np.full(n * batch, 7.0, np.float32)
             _lib.check(_lib.lib().frq_memcpy_h2d(yd.ptr, mark.ctypes.data, mark.nbytes))
-            rc = _noalloc(q, w, xd, yd, n, k)
+            rc = _noalloc(q, w, xd, yd, n, k, batch=batch)
             assert rc == _lib.ERR_UNSUPPORTED, rc
             assert "fixed scratch" in _lib.lib().frq_last_error().decode()
             device.synchronize()
