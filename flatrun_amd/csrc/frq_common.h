@@ -174,6 +174,11 @@ __device__ __forceinline__ float dpp_mov(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_add(float acc, float v) {
     // acc + v[src lane]; rows outside ROW_MASK keep acc unchanged (old = 0).

@@ -22,6 +22,17 @@
 // CFmt<Q4_K>::codes) or equal to it, so every row's error is bounded like
 // the matvec kernels':  |y - y_exact| <= c * 2^-24 * sum_j |w_j x_j|,
 // c a small multiple of the summation depth (tested at 1e-5 against fp64).
+// That holds for x in {0} U [2^-100, 2^100], where all three pieces are
+// normal bf16 and no product or sum overflows. Every value of x is checked:
+// the workgroups of one tile of x rows stage the same values, so the one
+// whose column tile is the step index modulo the column-tile count checks
+// that step. A row of x with any value outside (tiny, subnormal, huge, inf,
+// NaN) is flagged in a word per row, tagged with a per-launch number (no
+// clearing between launches), and a second kernel computes its outputs
+// again weight by weight in fp64 (w the exact dequantized fp32 value,
+// products exact, one rounding to fp32 at the end; inf and NaN propagate as
+// IEEE arithmetic has them): the split-adding kernel when K is split, else
+// a per-row kernel that returns at once for rows without the flag.
 //
 // Tiling: a workgroup of 4 waves owns a BM x BN tile of Y (WM x WN waves of
 // 32 x 64, two 32 x 32 MFMA tiles each) and walks K in steps of 32. Each
@@ -35,6 +46,8 @@
 // D register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #include "frq_common.h"
 #include "frq_kernels.h"
+
+#include <atomic>
 
 namespace frq {
 namespace {
@@ -197,11 +210,45 @@ struct CFmt<kTypeQ6K> {
     }
 };
 
+// Element j of a W row as the dequantizer gives it (fp32, gguf.py op order):
+// Q4_K fl(d sc q) - fl(dmin m), Q6_K d sc (q - 32), Q8_0 d q.
+template <int QT>
+__device__ float weight_at(const uint8_t* __restrict__ wrow, int j) {
+    if constexpr (QT == kTypeQ4K) {
+        const uint8_t* bp = wrow + (int64_t)(j >> 8) * kQ4KBytes;
+        const int e = j & 255, sb = e >> 5, l = e & 31;
+        const uint4 h = *reinterpret_cast<const uint4*>(bp);
+        uint32_t sc, mn;
+        k4_scale_min(h.y, h.z, h.w, sb, sc, mn);
+        const uint32_t q = (bp[16 + 32 * (sb >> 1) + l] >> (4 * (sb & 1))) & 15u;
+        return f16_bits_to_f32(h.x) * (float)sc * (float)q - f16_bits_to_f32(h.x >> 16) * (float)mn;
+    } else if constexpr (QT == kTypeQ6K) {
+        const uint8_t* bp = wrow + (int64_t)(j >> 8) * kQ6KBytes;
+        const int e = j & 255, hh = e >> 7, ks = (e >> 5) & 3, l = e & 31;
+        const uint32_t ql = (bp[64 * hh + 32 * (ks & 1) + l] >> (ks >= 2 ? 4 : 0)) & 15u;
+        const uint32_t qh = (bp[128 + 32 * hh + l] >> (2 * ks)) & 3u;
+        const float sc = (float)(int)(int8_t)bp[192 + 8 * hh + (l >> 4) + 2 * ks];
+        return f16_bits_to_f32(ld_u16(bp + 208)) * sc * (float)((int)(ql | (qh << 4)) - 32);
+    } else {
+        const uint8_t* bp = wrow + (int64_t)(j >> 5) * kQ80Bytes;
+        return f16_bits_to_f32(ld_u16(bp)) * (float)(int)(int8_t)bp[2 + (j & 31)];
+    }
+}
+
+// sum_j w[j] x[j] in fp64 (products of fp32 values exact), rounded to fp32 once.
+template <int QT>
+__device__ float row_dot_exact(const uint8_t* __restrict__ wrow, const float* __restrict__ xrow, int K) {
+    double acc = 0.0;
+    for (int j = 0; j < K; ++j) acc = __builtin_fma((double)weight_at<QT>(wrow, j), (double)xrow[j], acc);
+    return (float)acc;
+}
+
 template <int QT, int WM, int WN, int MI>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_f32c_kernel(const uint8_t* __restrict__ w,
                                                                  const float* __restrict__ x, float* __restrict__ y,
                                                                  int M, int N, int K, int64_t ldy, int S,
-                                                                 float* __restrict__ part) {
+                                                                 float* __restrict__ part,
+                                                                 uint32_t* __restrict__ flags, uint32_t epoch) {
     static_assert(WM * WN == 4 || WM * WN == 8, "four or eight waves");
     constexpr int NT = 64 * WM * WN;                  // threads
     constexpr int BM = 32 * MI * WM, BN = 64 * WN;    // a wave owns 32 MI x 64 of the tile
@@ -226,6 +273,12 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_f32c_kernel(const uint8_t* 
     const int steps = (int)((int64_t)(split + 1) * total / S) - sbase;
 
     const int xr = tid / XT, xk = (tid % XT) * XV;    // X staging: row xr, elements xk .. xk + XV - 1
+    // over the steps this workgroup checks (its row xr is the same in all):
+    // |x| without its sign as bits << 1, the exponent in the top byte (inf
+    // and NaN above every finite value): the largest, and the smallest
+    // nonzero as (bits << 1) - 1, where 0 wraps to the top and drops out
+    uint32_t xr_max = 0, xr_min1 = 0xFFFFFFFFu;
+    const int ntiles = (N + BN - 1) / BN;
     const float* xrow = x + (int64_t)(m0 + xr < M ? m0 + xr : M - 1) * K;
     const int wr = tid / WT, wk = (tid % WT) * WV;    // W staging: row wr, codes wk .. wk + WV - 1
     const uint8_t* wrow = w + (int64_t)(n0 + wr < N ? n0 + wr : N - 1) * row_bytes;
@@ -245,6 +298,14 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_f32c_kernel(const uint8_t* 
         // X: three bf16 pieces per value and the row's sum over the step
         uint32_t p1[XV / 2], p2[XV / 2], p3[XV / 2];
         float sx = 0.0f;
+        if ((sbase + s) % ntiles == nt % ntiles) {        // workgroup-uniform
+#pragma unroll
+            for (int i = 0; i < XV; ++i) {
+                const uint32_t u = __float_as_uint(st.xv[i >> 2][i & 3]) << 1;
+                xr_max = max(xr_max, u);
+                xr_min1 = min(xr_min1, u - 1u);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < XV / 2; ++i) {
             const float a = st.xv[i >> 1][2 * (i & 1)], b = st.xv[i >> 1][2 * (i & 1) + 1];
@@ -400,6 +461,9 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_f32c_kernel(const uint8_t* 
         }
     }
 
+    // every value checked here 0 or in [2^-100, 2^100] (exponent fields
+    // 27 .. 227; inf and NaN have 255), else flag the row (rare)
+    if ((xr_max > (227u << 24) || xr_min1 < (27u << 24) - 1u) && m0 + xr < M) flags[m0 + xr] = epoch;
     // S > 1: this split's partial tile goes to plane `split` (rows of N)
     float* out = S == 1 ? y : part + (int64_t)split * M * N;
     const int64_t ld = S == 1 ? ldy : N;
@@ -416,18 +480,72 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_f32c_kernel(const uint8_t* 
         }
 }
 
+// Unsplit launches: the rows flagged for this launch, weight by weight in
+// fp64 (one workgroup per row of x; the others return at once).
+template <int QT>
+__global__ void __launch_bounds__(256) gemm_f32_fixup_kernel(float* __restrict__ y, int N, int64_t ldy,
+                                                             const uint32_t* __restrict__ flags, uint32_t epoch,
+                                                             const uint8_t* __restrict__ w,
+                                                             const float* __restrict__ x, int K) {
+    const int m = (int)blockIdx.x;
+    if (flags[m] != epoch) return;
+    const int64_t row_bytes = (int64_t)(K / CFmt<QT>::kElems) * CFmt<QT>::kBytes;
+    for (int n = threadIdx.x; n < N; n += blockDim.x)
+        y[(int64_t)m * ldy + n] = row_dot_exact<QT>(w + (int64_t)n * row_bytes, x + (int64_t)m * K, K);
+}
+
+// Split-K sums: y = the planes added in split order, except rows flagged
+// for this launch (x outside the pieces' range), which are computed weight
+// by weight in fp64. Row blockIdx.x, four columns per thread.
+template <int QT>
+__global__ void __launch_bounds__(256) gemm_f32_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
+                                                              int S, int M, int N, int64_t ldy,
+                                                              const uint32_t* __restrict__ flags, uint32_t epoch,
+                                                              const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x, int K) {
+    const int m = (int)blockIdx.x;
+    const int n0 = 4 * ((int)blockIdx.y * (int)blockDim.x + (int)threadIdx.x);
+    if (n0 >= N) return;
+    const int64_t count = (int64_t)M * N, base = (int64_t)m * N;
+    float* yr = y + (int64_t)m * ldy;
+    if (flags[m] == epoch) {                             // workgroup-uniform
+        const int64_t row_bytes = (int64_t)(K / CFmt<QT>::kElems) * CFmt<QT>::kBytes;
+        for (int n = n0; n < n0 + 4 && n < N; ++n)
+            yr[n] = row_dot_exact<QT>(w + (int64_t)n * row_bytes, x + (int64_t)m * K, K);
+        return;
+    }
+    if (n0 + 4 <= N && ((N | ldy) & 3) == 0 && !(reinterpret_cast<uintptr_t>(y) & 15)) {
+        const f32x4 v = sum_planes<f32x4>(
+            [&](int q) { return *reinterpret_cast<const f32x4*>(part + q * count + base + n0); }, S);
+        *reinterpret_cast<f32x4*>(yr + n0) = v;
+    } else {
+        for (int n = n0; n < n0 + 4 && n < N; ++n)
+            yr[n] = sum_planes<float>([&](int q) { return part[q * count + base + n]; }, S);
+    }
+}
+
 template <int QT>
 void f32c_go(int bm, int bn, dim3 g, hipStream_t s, const uint8_t* w, const float* x, float* y, int M, int N, int K,
-             int64_t ldy, int S, float* part) {
+             int64_t ldy, int S, float* part, uint32_t* flags, uint32_t epoch) {
     if (bm == 32)
-        gemm_f32c_kernel<QT, 1, 4, 1><<<g, dim3(256), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
+        gemm_f32c_kernel<QT, 1, 4, 1><<<g, dim3(256), 0, s>>>(w, x, y, M, N, K, ldy, S, part, flags, epoch);
     else if (bm == 64)
-        gemm_f32c_kernel<QT, 2, 2, 1><<<g, dim3(256), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
+        gemm_f32c_kernel<QT, 2, 2, 1><<<g, dim3(256), 0, s>>>(w, x, y, M, N, K, ldy, S, part, flags, epoch);
     else if (bn == 128)
-        gemm_f32c_kernel<QT, 4, 2, 1><<<g, dim3(512), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
+        gemm_f32c_kernel<QT, 4, 2, 1><<<g, dim3(512), 0, s>>>(w, x, y, M, N, K, ldy, S, part, flags, epoch);
     else
-        gemm_f32c_kernel<QT, 2, 4, 2><<<g, dim3(512), 0, s>>>(w, x, y, M, N, K, ldy, S, part);
+        gemm_f32c_kernel<QT, 2, 4, 2><<<g, dim3(512), 0, s>>>(w, x, y, M, N, K, ldy, S, part, flags, epoch);
+    if (S > 1) {
+        gemm_f32_reduce_kernel<QT><<<dim3((unsigned)M, (unsigned)((N + 1023) / 1024)), dim3(256), 0, s>>>(
+            part, y, S, M, N, ldy, flags, epoch, w, x, K);
+    } else {
+        gemm_f32_fixup_kernel<QT><<<dim3((unsigned)M), dim3(256), 0, s>>>(y, N, ldy, flags, epoch, w, x, K);
+    }
 }
+
+// One flag word per row of x, after the partial planes of a K-split launch
+// (at the start of the scratch when K is not split).
+size_t flag_bytes(int64_t m) { return ((size_t)m * sizeof(uint32_t) + 255) & ~(size_t)255; }
 
 // Tile shape: BM x BN = 32 x 256 for up to 32 rows of X, 64 x 128 up to
 // kF32cMidRows rows, else eight waves on 128 rows: 128 x 256 for Q4_K (waves
@@ -461,13 +579,13 @@ int gemm_f32_splits(int qtype, int64_t m, int64_t n, int64_t k, size_t part_cap)
     f32c_tile(qtype, m, &bm, &bn);
     const int64_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     const int64_t steps = k / kCK;
-    const double plane = (double)m * (double)n * sizeof(float);
+    const double plane = (double)m * (double)n * sizeof(float), flagb = (double)flag_bytes(m);
     // one round of workgroups: two 4-wave workgroups per CU, or one 8-wave
     // 128-row workgroup (85 or 105 KB of LDS)
     const int64_t per_round = bm == 128 ? 256 : 512;
     int best = 1;
     for (int sp = 2; sp <= 64; sp *= 2) {
-        if (steps / sp < 8 || tiles * sp > per_round || sp * plane > (double)part_cap) break;
+        if (steps / sp < 8 || tiles * sp > per_round || sp * plane + flagb > (double)part_cap) break;
         best = sp;
     }
     return best;
@@ -475,7 +593,7 @@ int gemm_f32_splits(int qtype, int64_t m, int64_t n, int64_t k, size_t part_cap)
 
 size_t gemm_f32_scratch(int qtype, int64_t m, int64_t n, int64_t k, size_t part_cap) {
     const int sp = gemm_f32_splits(qtype, m, n, k, part_cap);
-    return sp > 1 ? (size_t)sp * (size_t)m * (size_t)n * sizeof(float) : 0;
+    return (sp > 1 ? (size_t)sp * (size_t)m * (size_t)n * sizeof(float) : 0) + flag_bytes(m);
 }
 
 hipError_t launch_gemm_f32(int qtype, const uint8_t* w, const float* x, float* y, int64_t m, int64_t n, int64_t k,
@@ -491,13 +609,24 @@ hipError_t launch_gemm_f32(int qtype, const uint8_t* w, const float* x, float* y
     const int64_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     if (tiles * sp > 0x7FFFFFFF) return hipErrorInvalidValue;
     const dim3 g((unsigned)(tiles * sp));
+    // per-launch tag of the row flags (never 0, the value of fresh scratch)
+    static std::atomic<uint32_t> launches{0};
+    uint32_t epoch = ++launches;
+    if (epoch == 0) epoch = ++launches;
+    if (!part || part_cap < gemm_f32_scratch(qtype, m, n, k, part_cap)) return hipErrorInvalidValue;
+    uint32_t* flags = reinterpret_cast<uint32_t*>(part + (sp > 1 ? (size_t)sp * (size_t)m * (size_t)n : 0));
     switch (qtype) {
-        case kTypeQ4K: f32c_go<kTypeQ4K>(bm, bn, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
-        case kTypeQ6K: f32c_go<kTypeQ6K>(bm, bn, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
-        case kTypeQ80: f32c_go<kTypeQ80>(bm, bn, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part); break;
+        case kTypeQ4K:
+            f32c_go<kTypeQ4K>(bm, bn, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part, flags, epoch);
+            break;
+        case kTypeQ6K:
+            f32c_go<kTypeQ6K>(bm, bn, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part, flags, epoch);
+            break;
+        case kTypeQ80:
+            f32c_go<kTypeQ80>(bm, bn, g, stream, w, x, y, (int)m, (int)n, (int)k, ldy, sp, part, flags, epoch);
+            break;
         default: return hipErrorInvalidValue;
     }
-    if (sp > 1) return launch_split_reduce(part, y, sp, m, n, ldy, stream);
     return hipGetLastError();
 }
 

@@ -170,9 +170,11 @@ hipError_t launch_split_reduce(const float* part, float* y, int splits, int64_t 
 // ldy >= n floats apart. x 16-byte aligned, w
 // 16-byte (Q4_K) / 2-byte aligned; k a multiple of 256 (Q4_K, Q6_K) or 32
 // (Q8_0). Few output tiles split K (gemm_f32_splits, at most `part_cap`
-// bytes of partials): fp32 partial planes in `part` (gemm_f32_scratch bytes)
-// added in split order by a second kernel; launches sharing `part` must be
-// ordered. The split count is a function of (qtype, m, n, k, part capacity) only, so
+// bytes of partials): fp32 partial planes in `part` added in split order by
+// a second kernel; `part` also holds one flag word per row of x (rows with
+// values outside the bf16 pieces' range, computed again by the second
+// kernel in fp64), so it is never null (gemm_f32_scratch bytes); launches
+// sharing `part` must be ordered. The split count is a function of (qtype, m, n, k, part capacity) only, so
 // results do not depend on which scratch a call gets beyond its capacity.
 bool gemm_f32_supported(int qtype, int64_t m, int64_t n, int64_t k);
 int gemm_f32_splits(int qtype, int64_t m, int64_t n, int64_t k, size_t part_cap = SIZE_MAX);

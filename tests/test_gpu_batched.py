@@ -200,3 +200,110 @@ def test_batched_q4k_few_rows(frq, n, k, seq):
             pair = np.stack([xs[r], xs[(r + 1) % seq]])
             assert bits_equal(y[r], dev_batched("Q4_K", raw, pair, n, k)[0]), r
     oracle_rows("Q4_K", raw, xs, n, k, y, f"Q4_K {n}x{k} rows {seq}")
+
+
+_F32_MAX = float(np.finfo(np.float32).max)
+
+
+def _extreme_batch(k, seq, seed, W):
+    """x rows of every class the three bf16 pieces cannot carry unscaled,
+    plus ordinary rows, repeated to `seq` rows. Returns (xs, class names).
+    The largest row is scaled from W so that every sum_j |w_ij x_j| stays
+    below FLT_MAX / 8: its exact results are finite, and no fp32 summation
+    order overflows."""
+    rng = np.random.default_rng(seed)
+
+    def large(v):
+        top = float(np.max(np.abs(W) @ np.abs(v)))
+        return v * 2.0 ** np.floor(np.log2(_F32_MAX / (8.0 * top)))
+    sign = lambda: rng.choice(np.array([-1.0, 1.0]), k)  # noqa: E731
+    classes = {
+        "normal": lambda: rng.standard_normal(k),
+        "x 2^-120": lambda: rng.standard_normal(k) * 2.0**-120,          # normal fp32, pieces below bf16's range
+        "x 2^-140": lambda: rng.standard_normal(k) * 2.0**-140,          # subnormal fp32
+        "subnormal": lambda: sign() * rng.integers(1, 1 << 23, k) * 2.0**-149,
+        "x 2^110": lambda: rng.standard_normal(k) * 2.0**110,
+        "large (sums near FLT_MAX / 8)": lambda: large(rng.standard_normal(k)),
+        "tiny among normal": lambda: np.where(rng.random(k) < 0.05, sign() * 2.0**-125, rng.standard_normal(k)),
+        "zeros": lambda: np.zeros(k),
+        "inf": lambda: (lambda v: (v.__setitem__(rng.integers(0, k, 3), [np.inf, np.inf, -np.inf]), v)[1])(
+            rng.standard_normal(k)),
+        "+inf only": lambda: (lambda v: (v.__setitem__(rng.integers(0, k, 2), np.inf), v)[1])(rng.standard_normal(k)),
+        "nan": lambda: (lambda v: (v.__setitem__(int(rng.integers(0, k)), np.nan), v)[1])(rng.standard_normal(k)),
+    }
+    names = list(classes)
+    xs = np.empty((seq, k), np.float32)
+    tags = []
+    for r in range(seq):
+        nm = names[r % len(names)]
+        xs[r] = classes[nm]().astype(np.float32)
+        tags.append(nm)
+    return xs, tags
+
+
+def _check_extreme_row(y, W, x, what):
+    """fp32 result of W x against the exact one (fp64, per weight).
+    Finite x: |dy_i| <= 1e-5 sum_j |w_ij x_j| + k 2^-150 (the second term is
+    what any fp32 result with at most k roundings into the subnormal range can
+    add: it matters only for rows whose terms lie near 2^-149, and no fp32
+    path, single-row or batched, meets 1e-5 componentwise there). Non-finite
+    x: the IEEE result of the per-weight sum, bit for bit in class (NaN, +inf,
+    -inf)."""
+    x64 = x.astype(np.float64)
+    if np.all(np.isfinite(x64)):
+        y64 = W @ x64
+        a64 = np.abs(W) @ np.abs(x64)
+        tol = 1e-5 * a64 + W.shape[1] * 2.0**-150
+        over = np.abs(y64) > _F32_MAX
+        assert np.all(np.isinf(y[over]) & (np.sign(y[over]) == np.sign(y64[over]))), what
+        ok = ~over
+        err = np.abs(y[ok].astype(np.float64) - y64[ok])
+        assert np.all(err <= tol[ok]), f"{what}: worst {np.max(err / tol[ok]):.3g} x the bound"
+        return
+    # per weight: NaN from any NaN x, any 0 * inf, or opposite infinities; else the infinity's sign
+    bad = ~np.isfinite(x64)
+    Wb, xb = W[:, bad], x64[bad]
+    with np.errstate(invalid="ignore"):
+        prods = Wb * xb[None, :]
+    want_nan = np.any(np.isnan(prods), axis=1) | (np.any(prods == np.inf, axis=1) & np.any(prods == -np.inf, axis=1))
+    want = np.where(want_nan, np.nan, np.where(np.any(prods == np.inf, axis=1), np.inf, -np.inf))
+    assert np.array_equal(np.isnan(y), np.isnan(want)), f"{what}: NaN pattern"
+    fin = ~np.isnan(want)
+    assert np.array_equal(y[fin], want[fin]), f"{what}: infinities"
+
+
+@pytest.mark.parametrize("q,n,k", [("Q4_K", 512, 4096), ("Q6_K", 256, 4096), ("Q8_0", 384, 2048)])
+@pytest.mark.parametrize("seq", [4, 32, 512])
+def test_batched_extreme_x_rows(frq, q, n, k, seq):
+    """Rows of x at 2^-120, 2^-140 (subnormal), all-subnormal, 2^110, as large
+    as the row's sums allow (~2^120 here), tiny values among normal ones,
+    zeros, +-inf and NaN, through the
+    small-M matvec (seq 4) and the fp32-contract GEMM (32, 512 rows, K-split
+    and not). Every row meets the contract of _check_extreme_row; the same
+    rows computed one at a time (batch 1) give the same non-finite classes;
+    an ordinary row's bits do not depend on the rows beside it."""
+    raw = synth.make_blocks(q, n, k, seed=7 * n + seq)
+    W = G.DEQUANT[q](raw, (n, k), np.float32).astype(np.float64)
+    xs, tags = _extreme_batch(k, seq, seed=seq + k, W=W)
+    y = dev_batched(q, raw, xs, n, k)
+    for r in range(seq):
+        _check_extreme_row(y[r], W, xs[r], f"{q} {n}x{k} seq {seq} row {r} ({tags[r]})")
+    # batch 1, one row per class
+    seen = set()
+    for r in range(seq):
+        if tags[r] in seen:
+            continue
+        seen.add(tags[r])
+        y1 = dev_batched(q, raw, xs[r:r + 1], n, k)[0]
+        _check_extreme_row(y1, W, xs[r], f"{q} batch 1 ({tags[r]})")
+        assert np.array_equal(np.isnan(y1), np.isnan(y[r])), tags[r]
+        assert np.array_equal(np.isinf(y1), np.isinf(y[r])), tags[r]
+    # ordinary rows: the same bits with every other row ordinary too
+    calm = xs.copy()
+    normal = [r for r in range(seq) if tags[r] == "normal"]
+    rng = np.random.default_rng(3)
+    for r in range(seq):
+        if tags[r] != "normal":
+            calm[r] = rng.standard_normal(k).astype(np.float32)
+    yc = dev_batched(q, raw, calm, n, k)
+    assert bits_equal(y[normal], yc[normal])
