@@ -88,6 +88,45 @@ def effective_bytes(q: str, n: int, k: int, batch: int = 1) -> int:
     return synth.nbytes(q, n, k) + 4 * k * batch + 4 * n * batch
 
 
+def graph_time(stream, launch, steps: int, warmup: int) -> float:
+    """Seconds for `steps` calls launch(i) (i = warmup .. warmup + steps - 1)
+    after `warmup` untimed ones. Two graphs, each replayed once after a device
+    synchronization and bracketed by events: A = the warmup and the timed
+    launches, B = the warmup launches alone. A - B is the time of exactly the
+    `steps` timed launches: the fixed start of a graph replay on the device
+    (~9 us here, which a timed region opened between two graphs would hold)
+    and the host's submission are in both and cancel. HIP cannot time
+    events recorded inside a graph."""
+    def capture(count):
+        with device.Graph.capture(stream) as cap:
+            for i in range(count):
+                launch(i)
+        return cap.graph
+
+    ga, gb = capture(warmup + steps), capture(warmup) if warmup else None
+    e0, e1 = device.Event(), device.Event()
+
+    def run(g):
+        if g is None:
+            return 0.0
+        device.synchronize()
+        e0.record(stream)
+        g.launch(stream)
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / 1e3
+
+    tb = run(gb)
+    ta = run(ga)
+    device.synchronize()
+    ga.destroy()
+    if gb is not None:
+        gb.destroy()
+    e0.destroy()
+    e1.destroy()
+    return ta - tb
+
+
 class GemvWorkload:
     """Rotating device copies of one seeded weight, x and y resident in HBM."""
 
@@ -143,25 +182,16 @@ class GemvWorkload:
         return {"launches": launches, "ms": round(ms, 3)}
 
     def time_throughput(self, steps: int, warmup: int) -> float:
-        """Seconds for `steps` launches replayed back-to-back from one HIP
-        graph, after a settle burst (settle) and `warmup` untimed launches;
-        events on the launching stream. The device is synchronized before
-        the warmup launches, which keep it busy while the host submits the
-        timed graph, so the timed region holds the `steps` launches and not
-        the host's submission latency."""
-        g_warm, g = self.graph(max(warmup, 1)), self.graph(steps, start=warmup)
+        """Seconds for `steps` launches replayed back-to-back, after a settle
+        burst (settle) and `warmup` untimed launches. Warmup, start event,
+        the `steps` launches and end event are one HIP graph, replayed once
+        after a device synchronization: the events bracket exactly the
+        `steps` launches, with neither the host's submission nor the gap
+        between two graphs inside (that gap, ~9 us here, spread over a short
+        timed region of separately launched graphs, read as 0.45 us more per
+        launch at 20 steps)."""
         self.settled = self.settle()
-        device.synchronize()
-        e0, e1 = device.Event(), device.Event()
-        g_warm.launch(self.stream)
-        e0.record(self.stream)
-        g.launch(self.stream)
-        e1.record(self.stream)
-        e1.synchronize()
-        device.synchronize()
-        g.destroy()
-        g_warm.destroy()
-        return e0.elapsed_ms(e1) / 1e3
+        return graph_time(self.stream, self.launch, steps, max(warmup, 1))
 
     def time_eager(self, steps: int) -> float:
         """Seconds for `steps` launches issued one by one from Python."""
@@ -305,7 +335,9 @@ def run_suite(stream, steps: int, only: set | None = None, cpu: bool = True) -> 
         if not want(name):
             continue
         w = GemvWorkload(q, n, k, seed=100 + idx, stream=stream, kernel=kernel)
-        t = w.time_throughput(steps, warmup=1000)   # ~10 ms and more: the part settles
+        # after the settle burst: 200 untimed launches, then `steps` (>= 500)
+        # timed ones, two graphs differenced (graph_time)
+        t = w.time_throughput(steps, warmup=200)
         te = w.time_eager(min(steps, 200))
         tk = t / steps
         out[name] = {"gbs": round(w.bytes / tk / 1e9, 1), "kernel_us": round(tk * 1e6, 2),
@@ -317,6 +349,7 @@ def run_suite(stream, steps: int, only: set | None = None, cpu: bool = True) -> 
     extra = [("llama3_8b_decode_resident", lambda: decode_sweep_resident(stream, steps=max(3, min(steps // 50, 20)),
                                                                          cpu_baseline_on=cpu)),
              ("llama3_8b_decode_streamed", lambda: decode_sweep_streamed(stream)),
+             ("llama3_8b_decode_scheduler_hook", lambda: decode_scheduler_hook(stream)),
              ("prefill_gemm_q4_k_bf16_512x14336x4096", lambda: prefill_gemm(stream, cpu_baseline_on=cpu)),
              ("llama3_8b_prefill_layer_512", lambda: prefill_layer(stream)),
              ("batched_f32_q4_k_3584x18944", lambda: batched_f32(stream, cpu_baseline_on=cpu)),
@@ -408,6 +441,107 @@ def decode_sweep_streamed(stream, layers: int = 32, depth: int = 3, steps: int =
     return {"ms_per_step": round(ms, 3), "weight_bytes_per_step": total, "ring_slots": depth,
             "h2d_gbs": round(total / (ms / 1e3) / 1e9, 2),
             "note": "pinned host -> device over PCIe, overlapped with the GEMVs of earlier layers"}
+
+
+def decode_scheduler_hook(stream, layers: int = 8, depth: int = 3, passes: int = 3) -> dict:
+    """The reference scheduler's prefetch-hook path at Llama-3-8B shapes:
+    a synthetic GGUF of `layers` decoder layers (the Q4_K_M mix, 139 MB per
+    layer), bound through SchedulerStream (ring of `depth` device slots fed
+    from the file mapping through two pinned staging slots). A restatement of
+    LayerScheduler's call order (runtime/scheduler.py:222-242, 270-319) runs
+    `passes` sweeps over the layers: per layer the hook, then the forwarder's
+    seven projections through NativeBackend.matmul_* on host x (1-D), each
+    weight handed over as the handle returns it. Two handles:
+      copying    the reference's MmapTensorHandle.view (core/tensor.py:227-250):
+                 an array over mmap[a:b], a fresh bytes copy per call, so every
+                 call pays that copy and a content hash to find the weight;
+      zero-copy  a view of the mapping itself (np.frombuffer), keyed once.
+    Reported per layer and scaled to the 32 layers of a decode step."""
+    import mmap as _mmap
+    import tempfile
+
+    from flatrun_amd import NativeBackend, gguf, residency
+    from flatrun_amd.streaming import SchedulerStream
+
+    host = {name: synth.make_blocks(q, n, k, seed=i) for i, (name, q, n, k) in enumerate(LLAMA_LAYER)}
+    meth = {"Q4_K": "matmul_q4k", "Q6_K": "matmul_q6k", "Q8_0": "matmul_q8_0"}
+    xs = {k: synth.make_x(k, seed=k) for k in {k for *_, k in LLAMA_LAYER}}
+    out = {"layers_in_file": layers, "ring_slots": depth, "passes": passes}
+    with tempfile.TemporaryDirectory() as d:
+        path = Path(d) / "llama3_8b_layers.gguf"
+        stored = {L: [f"blk.{L}.{GGUF_PROJ[nm]}.weight" for nm, *_ in LLAMA_LAYER] for L in range(layers)}
+        gguf.write_gguf(path, [(stored[L][i], (n, k), q, host[nm].tobytes()) for L in range(layers)
+                               for i, (nm, q, n, k) in enumerate(LLAMA_LAYER)],
+                        {"general.architecture": "llama", "llama.block_count": layers})
+        names = {L: [gguf.translate_gguf_name(t) for t in stored[L]] for L in range(layers)}   # the reader's names
+        f = gguf.GGUFFile(path)
+        fd = open(path, "rb")
+        mm = _mmap.mmap(fd.fileno(), 0, access=_mmap.ACCESS_READ)
+        infos = {nm: f.info(nm) for L in range(layers) for nm in names[L]}
+
+        def copying(nm):
+            i = infos[nm]
+            a = np.ndarray(shape=(i.nbytes,), dtype=np.uint8, buffer=mm[i.offset:i.offset + i.nbytes])
+            a.flags.writeable = False
+            return a
+
+        def zero_copy(nm):
+            i = infos[nm]
+            return np.frombuffer(mm, dtype=np.uint8, count=i.nbytes, offset=i.offset)
+
+        class _Layer:                                    # utils/types.py:124-138
+            def __init__(self, index, tensor_names):
+                self.index, self.tensor_names = index, tensor_names
+
+        lay = [_Layer(L, tuple(names[L])) for L in range(layers)]
+        for label, handle in (("copying", copying), ("zero_copy", zero_copy)):
+            nb = NativeBackend()
+            st = SchedulerStream(f, lay, depth=depth)
+            nb.attach_stream(st)
+            hook = st.hook
+
+            def run_layer(L):
+                hook(lay[L])
+                for (nm, q, n, k), tname in zip(LLAMA_LAYER, names[L]):
+                    getattr(nb, meth[q])(xs[k], handle(tname), n, k)
+
+            for L in range(layers):                      # one untimed pass: caches, keys, pipeline
+                run_layer(L)
+            t0 = time.perf_counter()
+            for _ in range(passes):
+                for L in range(layers):
+                    run_layer(L)
+            dt = (time.perf_counter() - t0) / (passes * layers)
+            stats = dict(st.stats)
+            nb.attach_stream(None)
+            st.close()
+            # what the copy and the hash cost alone, per layer
+            t0 = time.perf_counter()
+            arrs = [handle(tname) for tname in names[0]]
+            t_handle = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            for arr in arrs:
+                residency.content_key(arr)
+            t_hash = time.perf_counter() - t0
+            del arrs, arr
+            layer_bytes = sum(infos[t].nbytes for t in names[0])
+            out[label] = {"ms_per_layer": round(dt * 1e3, 3), "ms_per_step_32_layers": round(dt * 32e3, 1),
+                          "h2d_gbs_effective": round(layer_bytes / dt / 1e9, 2),
+                          "handle_ms_per_layer": round(t_handle * 1e3, 3),
+                          "hash_ms_per_layer": round(t_hash * 1e3, 3),
+                          "hash_ms_per_step_32_layers": round(t_hash * 32e3, 1),
+                          "lookups_hit": stats["hits"], "lookups_missed": stats["misses"],
+                          "layers_streamed": stats["layers_streamed"]}
+        out["layer_bytes"] = layer_bytes
+        out["note"] = ("host x and y per call (the drop-in call shape); copying handles pay the mmap[a:b] copy "
+                       "and the content hash on every call, zero-copy handles neither")
+        try:
+            mm.close()
+        except BufferError:
+            pass                    # a view still alive: the mapping goes with it
+        fd.close()
+        f.close()
+    return out
 
 
 def prefill_gemm(stream, m: int = 512, n: int = 14336, k: int = 4096, reps: int = 200,
@@ -614,37 +748,29 @@ DEQUANT_F16_SUITE = [("Q4_K", 18944, 3584), ("Q6_K", 152064, 3584)]
 
 def dequant_suite(stream, reps: int = 20) -> dict:
     """Block dequant to fp32 at the workload shapes, and every format at
-    18944 x 3584 (271 MB of fp32 out, past the 256 MB last-level cache, so
-    the formats compare on HBM): algorithmic bytes = raw blocks read +
-    4 n k written (2 n k for the fp16 lines, `_f16`), timed as a graph of
-    `reps` launches over 2 weight copies."""
+    18944 x 3584: algorithmic bytes = raw blocks read + 4 n k written
+    (2 n k for the fp16 lines, `_f16`), timed as a graph of at least `reps`
+    launches, each on its own (weight copy, output) pair out of >= 1 GiB of
+    them, so no launch finds its inputs or outputs in the 256 MB last-level
+    cache."""
     out = {}
     cases = [(q, n, k, 4) for q, n, k in DEQUANT_SUITE] + [(q, n, k, 2) for q, n, k in DEQUANT_F16_SUITE]
     for q, n, k, osz in cases:
         raw = synth.make_blocks(q, n, k, seed=50)
-        ws = [device.DeviceBuffer.from_host(raw) for _ in range(2)]
-        y = device.DeviceBuffer(osz * n * k)
+        pairs = max(2, math.ceil(ROTATE_BYTES / (raw.nbytes + osz * n * k)))
+        ws = [device.DeviceBuffer.from_host(raw) for _ in range(pairs)]
+        ys = [device.DeviceBuffer(osz * n * k) for _ in range(pairs)]
+        reps_q = max(reps, pairs)
         step = device.dequant if osz == 4 else device.dequant_f16
-        with device.Graph.capture(stream) as cap:
-            for i in range(reps):
-                step(q, ws[i % 2], y, n * k, stream=stream, w_bytes=raw.nbytes)
-        cap.launch(stream)
-        device.synchronize()
-        e0, e1 = device.Event(), device.Event()
-        e0.record(stream)
-        cap.launch(stream)
-        e1.record(stream)
-        e1.synchronize()
-        us = e0.elapsed_ms(e1) / reps * 1e3
-        cap.destroy()
-        for b in ws:
+        us = graph_time(stream, lambda i: step(q, ws[i % pairs], ys[i % pairs], n * k, stream=stream,
+                                                   w_bytes=raw.nbytes), reps_q, reps_q) / reps_q * 1e6
+        for b in ws + ys:
             b.free()
-        y.free()
         nbytes = raw.nbytes + osz * n * k
         out[f"{q.lower()}_{n}x{k}" + ("_f16" if osz == 2 else "")] = {
                                        "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
                                        "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-                                       "algorithmic_bytes": nbytes}
+                                       "algorithmic_bytes": nbytes, "pairs_rotated": pairs}
     return out
 
 
@@ -654,18 +780,7 @@ def copy_ceiling(stream, mib: int = 512, reps: int = 20) -> dict:
     the GEMV against."""
     nbytes = mib << 20
     src, dst = device.DeviceBuffer(nbytes), device.DeviceBuffer(nbytes)
-    with device.Graph.capture(stream) as cap:
-        for _ in range(reps):
-            device.copy(dst, src, nbytes, stream=stream)
-    cap.launch(stream)
-    device.synchronize()
-    e0, e1 = device.Event(), device.Event()
-    e0.record(stream)
-    cap.launch(stream)
-    e1.record(stream)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / reps
-    cap.destroy()
+    ms = graph_time(stream, lambda i: device.copy(dst, src, nbytes, stream=stream), reps, reps) / reps * 1e3
     src.free()
     dst.free()
     return {"bytes_moved": 2 * nbytes, "us": round(ms * 1e3, 2), "gbs": round(2 * nbytes / (ms / 1e3) / 1e9, 1)}
@@ -682,18 +797,8 @@ def read_ceiling(stream, nbytes: int, reps: int = 200, bufs=None) -> dict:
         bufs = [device.DeviceBuffer(nbytes) for _ in range(max(2, math.ceil(ROTATE_BYTES / nbytes)))]
     out = device.DeviceBuffer(4 * device.READ_XOR_WORDS)
     reps = max(reps, len(bufs))
-    with device.Graph.capture(stream) as cap:
-        for i in range(reps):
-            device.read_xor(bufs[i % len(bufs)], nbytes, out, stream=stream)
-    cap.launch(stream)
-    device.synchronize()
-    e0, e1 = device.Event(), device.Event()
-    e0.record(stream)
-    cap.launch(stream)
-    e1.record(stream)
-    e1.synchronize()
-    us = e0.elapsed_ms(e1) * 1e3 / reps
-    cap.destroy()
+    us = graph_time(stream, lambda i: device.read_xor(bufs[i % len(bufs)], nbytes, out, stream=stream),
+                    reps, reps) / reps * 1e6
     out.free()
     if own:
         for b in bufs:
@@ -909,7 +1014,7 @@ def main() -> int:
         dst.free()
     if not a.no_suite:
         only = {c for c in a.configs.split(",") if c}
-        rec["configs"] = run_suite(stream, steps=min(a.steps, 500), only=only, cpu=not a.no_cpu)
+        rec["configs"] = run_suite(stream, steps=500, only=only, cpu=not a.no_cpu)
         if "llama3_8b_decode_resident" in rec["configs"]:
             rec["decode_step_ms_resident"] = rec["configs"]["llama3_8b_decode_resident"]["ms_per_step"]
     if not a.no_cpu:

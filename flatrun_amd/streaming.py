@@ -308,6 +308,7 @@ class SchedulerStream:
             if not self._layers:
                 raise ValueError("SchedulerStream needs at least one layer")
             self._pos = {key: p for p, (key, _, _) in enumerate(self._layers)}
+            self._sizes = [frozenset(nb for _, _, nb in plan) for _, plan, _ in self._layers]
             self.slot_bytes = max(ALIGN, max(b for _, _, b in self._layers))
             self.depth = max(1, min(int(depth), len(self._layers)))
             self._slots = [device.DeviceBuffer(self.slot_bytes) for _ in range(self.depth)]
@@ -369,12 +370,20 @@ class SchedulerStream:
     # ------------------------------------------------------------- backend
     def lookup(self, raw: np.ndarray):
         """The device copy of host weight `raw` if it is a tensor of the
-        current layer (after that layer's copy has finished), else None."""
+        current layer (after that layer's copy has finished), else None.
+        A weight whose byte count no tensor of the current layer has (the
+        embedding, the LM head, another layer's odd-sized tensor) returns
+        None before any hashing; the others are identified by content."""
         from .residency import content_key
 
         with self._cv:
             if self._plan.cur is None or self._closed:
                 return None
+            p = self._plan.seq[self._plan.cur] if self._plan.cur < len(self._plan.seq) else None
+        if p is not None and int(raw.nbytes) not in self._sizes[p]:
+            with self._cv:
+                self.stats["misses"] += 1
+            return None
         key = content_key(raw.reshape(-1))
         with self._cv:
             t = self._plan.cur
