@@ -306,14 +306,15 @@ def cpu_rates(q: str, n: int, k: int, raw: np.ndarray, x: np.ndarray, nbytes: in
     return out
 
 
-# (name, quant, out, in, kernel): kernel None = the default device path;
-# GEMV_ROWS forces the element-wise fp32 kernel (dequant and dot in one pass)
+# (name, quant, out, in, kernel): kernel None = the default device path
+# (for these Q4_K shapes the element-wise fp32 kernel: dequant and dot in one
+# pass); GEMV_MX forces the matrix-core kernel beside it
 SUITE = [
     ("q8_0_4864x896", "Q8_0", 4864, 896, None),
     ("q4_k_18944x3584", "Q4_K", 18944, 3584, None),
     ("q4_k_3584x18944", "Q4_K", 3584, 18944, None),
-    ("q4_k_3584x18944_elementwise", "Q4_K", 3584, 18944, _lib.GEMV_ROWS),
-    ("q4_k_18944x3584_elementwise", "Q4_K", 18944, 3584, _lib.GEMV_ROWS),
+    ("q4_k_3584x18944_matrix_cores", "Q4_K", 3584, 18944, _lib.GEMV_MX),
+    ("q4_k_18944x3584_matrix_cores", "Q4_K", 18944, 3584, _lib.GEMV_MX),
     ("q6_k_152064x3584", "Q6_K", 152064, 3584, None),
     ("q1_0_4096x4096", "Q1_0", 4096, 4096, None),
 ]

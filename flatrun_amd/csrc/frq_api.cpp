@@ -196,15 +196,16 @@ void sk_release_stream(hipStream_t stream) {
     }
 }
 
-// One GEMV on device buffers: the matrix-core Q4_K kernel where eligible,
-// else the whole-row kernel when a row fits one workgroup, else split-K.
+// One GEMV on device buffers: the matrix-core Q4_K kernel where it is the
+// faster one (gemv_mx_default), else the whole-row kernel when a row fits one
+// workgroup, else split-K.
 // Scratch (the matrix-core kernel's per-row exchange slots when rows are
 // split over two workgroups, the split-K partials) comes from the stream's
 // registry, or from `fixed` when given (nothing is allocated then; a shape
 // that needs more than `fixed` holds is refused before anything launches).
 int gemv_device(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t s,
                 const frq::FixedScratch* fixed = nullptr) {
-    if (frq::gemv_mx_eligible(qtype, w, x, n, k)) {
+    if (frq::gemv_mx_default(qtype, w, x, n, k)) {
         frq::MxPlan mp;
         frq::plan_gemv_mx(n, k, &mp);
         const size_t need = frq::gemv_mx_slot_bytes(mp, n);
@@ -251,7 +252,7 @@ int gemv_device(int qtype, const uint8_t* w, const float* x, float* y, int64_t n
 void gemv_scratch_need(int qtype, const uint8_t* w, const float* x, int64_t n, int64_t k, size_t* slot_bytes,
                        size_t* part_bytes) {
     *slot_bytes = *part_bytes = 0;
-    if (frq::gemv_mx_eligible(qtype, w, x, n, k)) {
+    if (frq::gemv_mx_default(qtype, w, x, n, k)) {
         frq::MxPlan mp;
         frq::plan_gemv_mx(n, k, &mp);
         *slot_bytes = frq::gemv_mx_slot_bytes(mp, n);
@@ -649,7 +650,7 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     if (cfg->kernel != FRQ_GEMV_AUTO && cfg->kernel != FRQ_GEMV_SPLITK && cfg->kernel != FRQ_GEMV_ROWS &&
         cfg->kernel != FRQ_GEMV_MX)
         return fail(FRQ_ERR_INVALID, "tuned gemv: unknown kernel %d", cfg->kernel);
-    if (cfg->kernel == FRQ_GEMV_MX || (cfg->kernel == FRQ_GEMV_AUTO && frq::gemv_mx_eligible(qtype, wp, x, n, k))) {
+    if (cfg->kernel == FRQ_GEMV_MX || (cfg->kernel == FRQ_GEMV_AUTO && frq::gemv_mx_default(qtype, wp, x, n, k))) {
         if (qtype != FRQ_Q4_K) return fail(FRQ_ERR_UNSUPPORTED, "the matrix-core GEMV takes Q4_K");
         if ((reinterpret_cast<uintptr_t>(wp) | reinterpret_cast<uintptr_t>(x)) & 15)
             return fail(FRQ_ERR_ALIGN, "the matrix-core GEMV needs 16-byte aligned weights and x");

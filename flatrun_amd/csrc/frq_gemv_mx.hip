@@ -702,6 +702,24 @@ bool gemv_mx_eligible(int qtype, const uint8_t* w, const float* x, int64_t n, in
     return plan_gemv_mx(n, k, &p);
 }
 
+bool gemv_mx_default(int qtype, const uint8_t* w, const float* x, int64_t n, int64_t k) {
+    // The matrix cores against the element-wise fp32 kernel, same process,
+    // graph-replayed (us, matrix cores / element-wise): they win by 5 % or
+    // more only where every row is whole in one workgroup and one round of
+    // at most 256 workgroups covers the rows:
+    //   one round, whole rows: 4096x4096 4.91 / 5.18, 8192x4096 6.69 / 7.25,
+    //     3584x3584 4.69 / 4.99, 8192x11008 14.29 / 15.98;
+    //   several rounds: 14336x4096 9.48 / 9.68, 8960x1536 5.47 / 5.64,
+    //     18944x3584 11.73 / 11.43, 5120x13824 18.02 / 16.59;
+    //   halves of rows: 3584x18944 12.18 / 12.29, 4096x14336 11.17 / 10.68,
+    //     2048x8192 6.38 / 5.33, 1536x8960 7.45 / 6.12.
+    // Elsewhere the element-wise kernel is the default.
+    if (!gemv_mx_eligible(qtype, w, x, n, k)) return false;
+    MxPlan p;
+    plan_gemv_mx(n, k, &p);
+    return p.ksplit == 1 && p.grid <= 256;
+}
+
 hipError_t launch_gemv_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, const MxPlan& p,
                           uint64_t* slots, hipStream_t stream) {
     if (n <= 0) return hipSuccess;

@@ -59,8 +59,10 @@ bool gemv_supported(int qtype, int64_t n, int64_t k);
 // slot per row that must be zero before a launch; every launch leaves it
 // zero, and launches sharing slots must be ordered, e.g. one stream).
 // Wavefronts own `blocks` consecutive 256-element blocks of the range.
-// plan_gemv_mx fills the fields left <= 0 and checks the rest. The default
-// path takes it (gemv_mx_eligible) for Q4_K with n > 1280.
+// plan_gemv_mx fills the fields left <= 0 and checks the rest. It runs for
+// Q4_K with n > 1280 (gemv_mx_eligible); the default path takes it where it
+// measured 5 % or more faster than the element-wise kernel: whole rows in one
+// round of <= 256 workgroups (gemv_mx_default).
 struct MxPlan {
     int rows = 0;      // output rows per workgroup (<= 16 * tiles)
     int tiles = 0;     // 16-row MFMA tiles per wavefront: 1 or 2
@@ -74,6 +76,7 @@ struct MxPlan {
 bool plan_gemv_mx(int64_t n, int64_t k, MxPlan* plan);
 size_t gemv_mx_slot_bytes(const MxPlan& plan, int64_t n);
 bool gemv_mx_eligible(int qtype, const uint8_t* w, const float* x, int64_t n, int64_t k);
+bool gemv_mx_default(int qtype, const uint8_t* w, const float* x, int64_t n, int64_t k);
 hipError_t launch_gemv_mx(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, const MxPlan& plan,
                           uint64_t* slots, hipStream_t stream);
 

@@ -138,8 +138,10 @@ int frq_dev_dequant_f16(int qtype, const void* w, size_t w_bytes, int64_t n_elem
 
 /* y[b, n] = W[n, k] . x[b, k] for b < batch: the decode matvec of
  * matmul_<q> / matmul_<q>_batched (_C.cpp:99-283) on device buffers.
- * Q4_K with n > 1280 and k <= 32768 (w and x 16-byte aligned) runs on the
- * matrix cores: int8 MFMA on the 4-bit codes and on x written per
+ * Q4_K with n > 1280, k <= 16384 or so (whole rows in one workgroup) and
+ * rows that one round of at most 256 workgroups covers (w and x 16-byte
+ * aligned) runs on the matrix cores, where they measured 5 % or more faster
+ * than the element-wise kernel: int8 MFMA on the 4-bit codes and on x written per
  * 32-element sub-block as a 60-bit fixed-point number relative to the
  * sub-block's max |x| (eight 8-bit digits), exact integer sums of q x and
  * of x, then per sub-block
@@ -148,10 +150,10 @@ int frq_dev_dequant_f16(int qtype, const void* w, size_t w_bytes, int64_t n_elem
  * Every x within 2^36 of its sub-block's max |x| is carried exactly; a
  * block whose x is not (a wider range, |x| >= 2^30, inf, NaN) is computed
  * per weight in fp32 (w = fl(fl(d*sc)*q) - fl(dmin*m), q4_k.h:153-185).
- * Rows longer than 64 blocks, and n <= 4096 with k >= 8192, are split in
- * two halves of k over two workgroups that combine in a fixed order through
- * per-row slots in the stream's scratch. The other shapes and formats run
- * on element-wise kernels whose every product is w_j x_j with the weight
+ * (frq_dev_gemv_tuned can also run it on rows split in two halves of k over
+ * two workgroups that combine in a fixed order through per-row slots in the
+ * stream's scratch.) The other shapes and formats run on element-wise
+ * kernels whose every product is w_j x_j with the weight
  * itself (Q4_K / Q5_K: w = fma(d*sc, q, -dmin*m), the dequantized bits;
  * Q6_K / Q8_0: signed codes under the block scale; Q1_0: +-d).
  * Error: for every finite x, row i is within the fp32 accumulation bound
@@ -164,9 +166,12 @@ int frq_dev_dequant_f16(int qtype, const void* w, size_t w_bytes, int64_t n_elem
  * block) is one fp32-contract GEMM that reads W once per 32 or 64 rows of x:
  * bf16 matrix cores on exact integer codes (Q4_K q - c with c the code
  * nearest dmin*m / d*sc, so every term stays within 3 |w_j x_j|) and on x
- * split into three bf16 pieces (all 24 bits of every x with
- * |x| >= 2^-110), fp32 sums per sub-block, then the sub-block scales in
- * fp32 -- the same error bound, other bits than one row at a time. A few
+ * split into three bf16 pieces (all 24 bits of every x in {0} U
+ * [2^-100, 2^100]), fp32 sums per sub-block, then the sub-block scales in
+ * fp32 -- the same error bound, other bits than one row at a time. A row of
+ * x with any value outside that range (tiny, subnormal, huge, inf, NaN) is
+ * computed again weight by weight in fp64 (one rounding; inf and NaN as
+ * IEEE arithmetic has them) by a second kernel. A few
  * rows (Q4_K, Q8_0: up to 6; Q6_K: up to 10) run the small-M matvec instead
  * when W and k suit it (one launch per two or three rows, W read once per
  * launch; Q4_K with per-weight fp32 arithmetic as one row, a row's bits
@@ -185,14 +190,15 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  * that frq_dev_gemv grows per stream is one fixed device array of
  * FRQ_NOALLOC_SCRATCH_BYTES per GPU instead (held until the process ends):
  * 1 MiB of row-exchange slots (8 bytes per output row of a Q4_K matrix whose
- * rows are split over two workgroups: n <= 131072) and 3 MiB of split-K
- * partials (n x slices x 4 bytes, rows longer than one workgroup). A batch-1
- * shape that needs more is refused with FRQ_ERR_UNSUPPORTED before anything
- * is launched. A batch that takes the small-M matvec (2 to 6 rows of Q4_K or
- * Q8_0, 2 to 10 of Q6_K, on matrices it accepts) needs no scratch; a batch
- * that takes the batched GEMM (4 or more rows of Q4_K, Q6_K, Q8_0) splits k
- * only as far as its partials (splits x batch x n x 4 bytes) fit in the
- * 3 MiB, so neither is refused; where the GEMM splits less than
+ * rows are split over two workgroups: n <= 131072; no default shape splits
+ * rows so today) and 3 MiB of split-K partials (n x slices x 4 bytes, rows
+ * longer than one workgroup). A batch-1 shape that needs more is refused
+ * with FRQ_ERR_UNSUPPORTED before anything is launched. A batch that takes
+ * the small-M matvec (2 to 6 rows of Q4_K or Q8_0, 2 to 10 of Q6_K, on
+ * matrices it accepts) needs no scratch; a batch that takes the batched
+ * GEMM (4 or more rows of Q4_K, Q6_K, Q8_0) keeps one flag word per row of x
+ * in the 3 MiB and splits k only as far as its partials (splits x batch x n
+ * x 4 bytes) fit beside them, so neither is refused (up to 786432 rows); where the GEMM splits less than
  * frq_dev_gemv would, the bits differ from frq_dev_gemv's within the same
  * bound. Any other batch runs one GEMV per row and is refused as batch 1
  * would be (for example 2 or 3 rows of Q4_K with k > 24576). Every call on a GPU shares that GPU's array: calls that overlap

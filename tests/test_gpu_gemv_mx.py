@@ -109,11 +109,15 @@ def test_mx_shapes_tiles_rows(frq, n, k):
                 assert bits_equal(y, ref), (tiles, rows, ks)   # the row tiling never changes a row's sums
 
 
-@pytest.mark.parametrize("q,n,k", [("Q4_K", 3584, 18944), ("Q4_K", 18944, 3584), ("Q4_K", 4096, 4096),
-                                   ("Q4_K", 1536, 8960), ("Q4_K", 2000, 2048)])
-def test_mx_default_path_full_size(frq, q, n, k):
-    """frq_dev_gemv takes the matrix-core kernel for these shapes; the tuned
-    entry's AUTO mode reports it and gives the same bits."""
+@pytest.mark.parametrize("q,n,k,mx", [("Q4_K", 3584, 18944, False), ("Q4_K", 18944, 3584, False),
+                                      ("Q4_K", 4096, 4096, True), ("Q4_K", 1536, 8960, False),
+                                      ("Q4_K", 2000, 2048, True), ("Q4_K", 8192, 11008, True),
+                                      ("Q4_K", 14336, 4096, False)])
+def test_default_path_kernel_choice_full_size(frq, q, n, k, mx):
+    """frq_dev_gemv takes the matrix-core kernel where it measured 5 % or more
+    faster (whole rows, one round of <= 256 workgroups), the element-wise
+    kernel elsewhere; the tuned entry's AUTO mode reports the same choice and
+    gives the same bits; both meet the oracle."""
     raw = synth.make_blocks(q, n, k, seed=n ^ k)
     x = synth.make_x(k, seed=k + 7)
     w = device.DeviceBuffer.from_host(raw)
@@ -126,7 +130,10 @@ def test_mx_default_path_full_size(frq, q, n, k):
         oracle_check(y, raw, x, n, k, f"default {q} {n}x{k}")
         cfg = device.gemv_tuned(q, w, xd, yd, n, k)
         device.synchronize()
-        assert cfg["kernel"] == _lib.GEMV_MX and 6 <= cfg["rows"] <= 32
+        if mx:
+            assert cfg["kernel"] == _lib.GEMV_MX and cfg["slices"] == 1 and cfg["items"] <= 256, cfg
+        else:
+            assert cfg["kernel"] == _lib.GEMV_ROWS, cfg
         assert bits_equal(yd.to_host(np.float32), y)
     finally:
         w.free()

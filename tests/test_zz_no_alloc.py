@@ -4,9 +4,10 @@ The no-allocation entry point runs the same kernels as frq_dev_gemv with
 its scratch in one fixed device array per GPU, so its results must equal
 frq_dev_gemv's bit for bit. Each case makes two calls in a row, the second
 on a smaller shape (the array keeps the first call's contents), covering
-every scratch user: the matrix-core Q4_K kernel with rows split over two
-workgroups (exchange slots), split-K rows (partials), and a kernel with no
-scratch. Shapes whose scratch would not fit are refused before any launch.
+every scratch user of the default path: split-K rows (partials), the
+batched GEMM (K-split partial planes and its per-row flags), and kernels
+with no scratch. Shapes whose scratch would not fit are refused before any
+launch.
 """
 
 from __future__ import annotations
@@ -50,8 +51,10 @@ def _case(q, n, k, batch, seed, stream):
 
 
 @pytest.mark.parametrize("q,shapes", [
-    ("Q4_K", [(3584, 18944, 1), (2048, 18944, 1)]),     # matrix cores, rows in two halves: slots
-    ("Q4_K", [(4096, 14336, 1), (1536, 8960, 2)]),      # two halves, then a batched call
+    ("Q4_K", [(3584, 18944, 1), (2048, 18944, 1)]),     # element-wise, no scratch
+    ("Q4_K", [(8192, 4096, 1), (4096, 4096, 1)]),       # matrix cores, whole rows: no scratch
+    ("Q4_K", [(4096, 14336, 1), (1536, 8960, 2)]),      # then a batched call (small-M matvec)
+    ("Q4_K", [(512, 4096, 40), (128, 4096, 8)]),        # batched GEMM: K-split partials and row flags
     ("Q4_K", [(300, 33024, 1), (100, 33024, 1)]),       # k > 32768: split-K partials
     ("Q6_K", [(1024, 4096, 1), (512, 4096, 1)]),        # no scratch
     ("Q8_0", [(4864, 896, 1), (1000, 896, 1)]),
@@ -95,10 +98,12 @@ def test_noalloc_graph_replay(frq):
 
 
 def test_noalloc_refuses_oversized_scratch(frq):
-    """More rows than the 1 MiB of slots hold (140000 > 131072), and split-K
-    partials past 3 MiB: refused with FRQ_ERR_UNSUPPORTED, nothing launched
-    (the output keeps its contents). The buffers are real, of full size."""
-    cases = [("Q4_K", 140000, 256 * 65)]
+    """Split-K partials past 3 MiB (one row of x, and two rows that run one
+    GEMV each): refused with FRQ_ERR_UNSUPPORTED, nothing launched (the
+    output keeps its contents). The buffers are real, of full size. (The
+    default path no longer splits matrix-core rows in halves, so no default
+    shape needs the row-exchange slots.)"""
+    cases = []
     # split-K: learn the slice count for k = 33024, then ask for enough rows
     probe_raw = synth.make_blocks("Q4_K", 4, 33024, seed=1)
     pw, px, py = (device.DeviceBuffer.from_host(probe_raw), device.DeviceBuffer.from_host(synth.make_x(33024, seed=2)),
