@@ -33,33 +33,80 @@ from __future__ import annotations
 import argparse
 import collections
 import json
+import re
+import shutil
 import sqlite3
 import statistics
+import subprocess
 import sys
 
 COPY_KERNEL = "copy16_kernel"
 
 
-def _dispatches(con):
+def _short_names(raw: list[str]) -> dict[str, str]:
+    """Mangled kernel symbol -> ``kernel<template args>`` (namespace, return
+    type, argument list and ``.kd`` dropped), through ``c++filt`` when the
+    host has it; otherwise the symbols unchanged."""
+    tool = shutil.which("c++filt")
+    if not tool or not raw:
+        return {r: r for r in raw}
+    stripped = [r[:-3] if r.endswith(".kd") else r for r in raw]
+    try:
+        out = subprocess.run([tool], input="\n".join(stripped), capture_output=True, text=True,
+                             check=True).stdout.split("\n")
+    except (OSError, subprocess.CalledProcessError):
+        return {r: r for r in raw}
+    short = {}
+    for r, d in zip(raw, out):
+        d = re.sub(r"^void ", "", d.strip())
+        d = d.replace("(anonymous namespace)::", "")
+        depth, cut = 0, len(d)
+        for i, ch in enumerate(d):               # drop the argument list after the template arguments
+            if ch == "<":
+                depth += 1
+            elif ch == ">":
+                depth -= 1
+            elif ch == "(" and depth == 0:
+                cut = i
+                break
+        short[r] = d[:cut] or r
+    return short
+
+
+def _dispatches(con, by_grid: bool = False):
+    """event id -> (key, duration in ns). The key is the kernel's name, and
+    with ``by_grid`` also its launch shape, ``name [wg GXxGY]`` (workgroups
+    per dimension), so that one kernel launched on several matrix shapes
+    gives one row per shape."""
     names = {r[0]: r[1] for r in con.execute("select id, kernel_name from rocpd_info_kernel_symbol")}
-    return {eid: (names.get(kid, "?"), end - start)
-            for eid, kid, start, end in con.execute(
-                "select event_id, kernel_id, start, end from rocpd_kernel_dispatch")}
+    short = _short_names(list(names.values()))
+    names = {k: short[v] for k, v in names.items()}
+    out = {}
+    for eid, kid, start, end, gx, gy, wx, wy in con.execute(
+            "select event_id, kernel_id, start, end, grid_size_x, grid_size_y, workgroup_size_x, "
+            "workgroup_size_y from rocpd_kernel_dispatch"):
+        key = names.get(kid, "?")
+        if by_grid:
+            key = f"{key} [wg {gx // max(wx, 1)}x{gy // max(wy, 1)}]"
+        out[eid] = (key, end - start)
+    return out
 
 
-def kernel_durations(db: str) -> dict[str, list[float]]:
-    """Kernel name -> durations in microseconds, dispatch order."""
+def kernel_durations(db: str, by_grid: bool = False) -> dict[str, list[float]]:
+    """Kernel name (or name and launch shape) -> durations in microseconds,
+    dispatch order."""
     con = sqlite3.connect(db)
     out: dict[str, list[float]] = collections.defaultdict(list)
-    for _, (name, dur) in sorted(_dispatches(con).items()):
+    for _, (name, dur) in sorted(_dispatches(con, by_grid).items()):
         out[name].append(dur / 1e3)
     return out
 
 
-def pmc_means(db: str) -> dict[str, dict[str, float]]:
-    """Kernel name -> {counter: mean per dispatch (summed over instances)}."""
+def pmc_means(db: str, by_grid: bool = False) -> dict[str, dict[str, float]]:
+    """Kernel name (or name and launch shape) -> {counter: mean per dispatch
+    (summed over instances)}."""
     con = sqlite3.connect(db)
-    disp = _dispatches(con)
+    disp = _dispatches(con, by_grid)
     counters = {r[0]: r[1] for r in con.execute("select id, name from rocpd_info_pmc")}
     per_event: dict[int, dict[str, float]] = collections.defaultdict(lambda: collections.defaultdict(float))
     for eid, pid, val in con.execute("select event_id, pmc_id, value from rocpd_pmc_event"):
@@ -74,11 +121,11 @@ def pmc_means(db: str) -> dict[str, dict[str, float]]:
 CU_NUM, SIMD_NUM = 256, 1024          # MI355X
 
 
-def pmc_reduced(db: str) -> dict[str, dict[str, float]]:
-    """Kernel name -> {counter: mean per dispatch}, instances summed (SQ) or
-    reduced by max (GRBM)."""
+def pmc_reduced(db: str, by_grid: bool = False) -> dict[str, dict[str, float]]:
+    """Kernel name (or name and launch shape) -> {counter: mean per
+    dispatch}, instances summed (SQ) or reduced by max (GRBM)."""
     con = sqlite3.connect(db)
-    disp = _dispatches(con)
+    disp = _dispatches(con, by_grid)
     counters = {r[0]: r[1] for r in con.execute("select id, name from rocpd_info_pmc")}
     per_event: dict[int, dict[str, float]] = collections.defaultdict(dict)
     for eid, pid, val in con.execute("select event_id, pmc_id, value from rocpd_pmc_event"):
@@ -109,15 +156,17 @@ def derived(c: dict[str, float]) -> dict[str, float]:
     return out
 
 
-def _pick(table: dict, match: str) -> str:
-    hits = [k for k in table if match in k]
+def _pick(table: dict, match) -> str:
+    """The one key of ``table`` that contains every string of ``match``."""
+    parts = [match] if isinstance(match, str) else list(match)
+    hits = [k for k in table if all(m in k for m in parts)]
     if len(hits) != 1:
-        raise SystemExit(f"'{match}' matches {len(hits)} kernels: {hits}")
+        raise SystemExit(f"{parts} match {len(hits)} kernels: {hits}")
     return hits[0]
 
 
-def traffic(fetch_db: str, write_db: str, match: str, copy_bytes: int) -> dict:
-    f, w = pmc_means(fetch_db), pmc_means(write_db)
+def traffic(fetch_db: str, write_db: str, match, copy_bytes: int, by_grid: bool = False) -> dict:
+    f, w = pmc_means(fetch_db, by_grid), pmc_means(write_db, by_grid)
     k_f, k_w = _pick(f, match), _pick(w, match)
     c_f, c_w = _pick(f, COPY_KERNEL), _pick(w, COPY_KERNEL)
     scale_f = copy_bytes / (f[c_f]["FETCH_SIZE"] * 1024.0)
@@ -143,23 +192,29 @@ def main(argv=None) -> int:
     tr = sub.add_parser("traffic")
     tr.add_argument("--fetch", required=True)
     tr.add_argument("--write", required=True)
-    tr.add_argument("--match", required=True)
+    tr.add_argument("--match", required=True, action="append",
+                    help="substring of the kernel's key; repeat to require several")
     tr.add_argument("--copy-bytes", type=int, default=256 << 20)
+    for p in (t, cn, tr):
+        p.add_argument("--by-grid", action="store_true",
+                       help="one row per kernel and launch shape (workgroups per dimension)")
     a = ap.parse_args(argv)
     if a.cmd == "trace":
         rows = []
-        for name, d in kernel_durations(a.db).items():
+        for name, d in kernel_durations(a.db, a.by_grid).items():
             if a.match in name:
                 rows.append((statistics.fmean(d), name, d))
-        print(f"{'kernel':72s} {'n':>6s} {'mean_us':>9s} {'median_us':>9s} {'min_us':>8s}")
+        width = 100 if a.by_grid else 72
+        print(f"{'kernel':{width}s} {'n':>6s} {'mean_us':>9s} {'median_us':>9s} {'min_us':>8s}")
         for mean, name, d in sorted(rows, reverse=True):
-            print(f"{name[:72]:72s} {len(d):6d} {mean:9.3f} {statistics.median(d):9.3f} {min(d):8.3f}")
+            short = name if len(name) <= width else name[:width - 22] + "~" + name[-21:]
+            print(f"{short:{width}s} {len(d):6d} {mean:9.3f} {statistics.median(d):9.3f} {min(d):8.3f}")
     elif a.cmd == "counters":
-        table = pmc_reduced(a.db)
+        table = pmc_reduced(a.db, a.by_grid)
         out = {name: {"counters": c, "derived": derived(c)} for name, c in table.items() if a.match in name}
         print(json.dumps(out, indent=1))
     else:
-        print(json.dumps(traffic(a.fetch, a.write, a.match, a.copy_bytes), indent=1))
+        print(json.dumps(traffic(a.fetch, a.write, a.match, a.copy_bytes, a.by_grid), indent=1))
     return 0
 
 
