@@ -31,7 +31,7 @@ QTYPES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K, "Q1_0": Q1_0,
 BLOCKS = {Q8_0: (34, 32), Q4_K: (144, 256), Q5_K: (176, 256), Q6_K: (210, 256), Q1_0: (18, 128)}
 
 
-GEMV_AUTO, GEMV_SPLITK, GEMV_ROWS, GEMV_MX = 0, 1, 2, 4   # frq_gemv_config.kernel (3 and 5 are not used)
+GEMV_AUTO, GEMV_SPLITK, GEMV_ROWS, GEMV_MX, GEMV_MB = 0, 1, 2, 4, 8   # frq_gemv_config.kernel (3 and 5 are not used)
 
 
 class GemvConfig(ctypes.Structure):

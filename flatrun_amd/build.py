@@ -35,7 +35,7 @@ ROOT = PKG.parent
 BUILD = ROOT / "_build"
 LIB = PKG / "libfrq_hip.so"
 
-SOURCES = ["frq_dequant.hip", "frq_gemv.hip", "frq_gemv_mx.hip", "frq_gemv_sk.hip", "frq_gemv_mr.hip", "frq_gemm.hip", "frq_gemm_f32.hip",
+SOURCES = ["frq_dequant.hip", "frq_gemv.hip", "frq_gemv_mx.hip", "frq_gemv_sk.hip", "frq_gemv_mr.hip", "frq_gemv_mb.hip", "frq_gemm.hip", "frq_gemm_f32.hip",
            "frq_noalloc.hip", "frq_act.hip",
            "frq_api.cpp"]
 ARCH = os.environ.get("FRQ_OFFLOAD_ARCH", "gfx950")

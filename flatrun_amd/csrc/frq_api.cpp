@@ -16,7 +16,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/frq.h"
+#include "frq.h"
 #include "frq_kernels.h"
 
 namespace {
@@ -284,6 +284,19 @@ int64_t mr_rows_before_gemm(int qtype) {
     return qtype == FRQ_Q6_K ? 10 : 6;
 }
 
+// Q4_K batches the fp32 matrix-core kernel takes in one launch: four rows of
+// x (k <= 24576), or five to eight where k <= 8192. Two and three rows take
+// the small-M element-wise kernel, longer batches chunks of it or the GEMM.
+// Measured (us, graph-replayed): Q4_K 3584 x 18944, matrix cores 2 / 3 / 4
+// rows 24.7 / 26.2 / 27.6, element-wise small-M 17.1 / 20.4 / 34 (2 + 2),
+// 5 / 6 rows 35.5 / 39.6 (3 + 2, 3 + 3), GEMM 42.7 at 7; Q4_K 4096 x 4096,
+// matrix cores 4 / 5 / 6 rows 8.7 / 11.1 / 12.0, GEMM 18.3 at 7.
+bool mb_takes(int qtype, const uint8_t* w, const float* x, int64_t batch, int64_t n, int64_t k) {
+    frq::MbPlan p;
+    return qtype == FRQ_Q4_K && batch >= 4 && batch <= frq::kGemvMbMax && frq::gemv_mb_ok(w, x, k) &&
+           frq::plan_gemv_mb(n, k, (int)batch, &p);
+}
+
 // Up to this many rows of x, a matrix that the small-M kernel does not take
 // (its alignment, block count or k) runs one GEMV per row rather than the
 // GEMM: each GEMV reads the weights again, but at a few rows its time per
@@ -296,7 +309,9 @@ constexpr int64_t kRowsBeforeGemm = 3;
 // rows, else the GEMM where batched_gemm allows, else one GEMV per row.
 enum class BatchRoute { SmallM, Gemm, Rows };
 BatchRoute batch_route(int qtype, const uint8_t* w, const float* x, int64_t batch, int64_t n, int64_t k) {
-    if (batch >= 2 && batch <= mr_rows_before_gemm(qtype) && frq::gemv_mr_ok(qtype, w, x, k)) return BatchRoute::SmallM;
+    if (mb_takes(qtype, w, x, batch, n, k) ||
+        (batch >= 2 && batch <= mr_rows_before_gemm(qtype) && frq::gemv_mr_ok(qtype, w, x, k)))
+        return BatchRoute::SmallM;
     if (batch > kRowsBeforeGemm && batched_gemm(qtype, w, x, batch, n, k)) return BatchRoute::Gemm;
     return BatchRoute::Rows;
 }
@@ -306,6 +321,12 @@ BatchRoute batch_route(int qtype, const uint8_t* w, const float* x, int64_t batc
 int gemv_batched(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int64_t batch,
                  int64_t ldy, hipStream_t s, const frq::FixedScratch* fixed = nullptr) {
     const BatchRoute route = batch_route(qtype, w, x, batch, n, k);
+    if (route == BatchRoute::SmallM && mb_takes(qtype, w, x, batch, n, k)) {
+        frq::MbPlan p;
+        frq::plan_gemv_mb(n, k, (int)batch, &p);
+        FRQ_HIP(frq::launch_gemv_mb(w, x, y, n, k, (int)batch, ldy, p, s));
+        return FRQ_OK;
+    }
     if (route == BatchRoute::SmallM) {
         for (int64_t b = 0; b < batch;) {   // chunks of 2 or 3 rows: 4 = 2 + 2, 5 = 3 + 2, 7 = 3 + 2 + 2
             const int64_t rem = batch - b, m = rem == 4 ? 2 : (rem < 3 ? rem : 3);
@@ -648,8 +669,28 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
     hipStream_t s = static_cast<hipStream_t>(stream);
     const uint8_t* wp = static_cast<const uint8_t*>(w);
     if (cfg->kernel != FRQ_GEMV_AUTO && cfg->kernel != FRQ_GEMV_SPLITK && cfg->kernel != FRQ_GEMV_ROWS &&
-        cfg->kernel != FRQ_GEMV_MX)
+        cfg->kernel != FRQ_GEMV_MX && cfg->kernel != FRQ_GEMV_MB)
         return fail(FRQ_ERR_INVALID, "tuned gemv: unknown kernel %d", cfg->kernel);
+    if (cfg->kernel == FRQ_GEMV_MB) {
+        if (qtype != FRQ_Q4_K) return fail(FRQ_ERR_UNSUPPORTED, "the fp32 matrix-core GEMV takes Q4_K");
+        if (!frq::gemv_mb_ok(wp, x, k))
+            return fail(FRQ_ERR_ALIGN, "the fp32 matrix-core GEMV needs 16-byte aligned weights and x");
+        frq::MbPlan mp;
+        mp.rows = cfg->rows;
+        mp.nbp = cfg->unroll;
+        if (!frq::plan_gemv_mb(n, k, 1, &mp))
+            return fail(FRQ_ERR_UNSUPPORTED, "fp32 matrix-core GEMV: no plan for n=%lld k=%lld rows=%d pairs=%d",
+                        (long long)n, (long long)k, cfg->rows, cfg->unroll);
+        hipError_t e = frq::launch_gemv_mb(wp, x, y, n, k, 1, n, mp, s);
+        if (e != hipSuccess) return tuned_fail(e, "launch_gemv_mb");
+        cfg->cpl = 1;
+        cfg->rows = mp.rows;
+        cfg->unroll = mp.nbp;
+        cfg->slices = 1;
+        cfg->waves_per_wg = mp.waves;
+        cfg->items = mp.grid;
+        return FRQ_OK;
+    }
     if (cfg->kernel == FRQ_GEMV_MX || (cfg->kernel == FRQ_GEMV_AUTO && frq::gemv_mx_default(qtype, wp, x, n, k))) {
         if (qtype != FRQ_Q4_K) return fail(FRQ_ERR_UNSUPPORTED, "the matrix-core GEMV takes Q4_K");
         if ((reinterpret_cast<uintptr_t>(wp) | reinterpret_cast<uintptr_t>(x)) & 15)

@@ -140,6 +140,23 @@ __device__ __forceinline__ void nibbles8(uint32_t w, float (&f)[8], uint32_t mas
         : "v"(mask_a), "v"(mask_b), "v"(w));
 }
 
+// The value of the fp8 (e4m3) code 1: a power of two u such that a byte
+// holding q < 16 converts to q * u exactly (codes below 8 are subnormal,
+// 8 .. 15 have the smallest exponent; both read as q * u).
+__device__ __forceinline__ float fp8_unit() {
+    return __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
+}
+
+// The eight nibbles of w as q * fp8_unit(): f[0..3] the low nibbles of bytes
+// 0..3, f[4..7] the high ones. Seven VALU operations for eight values.
+__device__ __forceinline__ void nibbles8_fp8(uint32_t w, float (&f)[8]) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false), b = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
+    const auto c = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, false), e = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, true);
+    f[0] = a[0]; f[1] = a[1]; f[2] = b[0]; f[3] = b[1];
+    f[4] = c[0]; f[5] = c[1]; f[6] = e[0]; f[7] = e[1];
+}
+
 // Four 6-bit Q6_K codes q as the signed bytes 4 (q - 32), converted to float
 // exactly (one sign-extending byte-select convert each): lo holds the low
 // nibbles at bits 2..5 of each byte, hi2 the two high bits at bits 6, 7 with

@@ -104,6 +104,24 @@ bool gemv_mr_ok(int qtype, const uint8_t* w, const float* x, int64_t k);
 hipError_t launch_gemv_mr(int qtype, const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int m,
                           int64_t ldy, hipStream_t stream);
 
+// Q4_K matvec of m = 1 .. kGemvMbMax rows of x with fp32 products on the
+// matrix cores (frq_gemv_mb.hip): Y[r * ldy + i] = sum_j W[i, j] X[r * k + j],
+// W read once. Per-weight fp32 arithmetic (w = fma(s, q, -t), every product
+// fused into an fp32 sum); a row's bits depend on its own x only. Needs W and
+// x 16-byte aligned. The plan fills what is 0: nbp block pairs per wavefront
+// (waves = ceil(pairs / nbp) <= 16: k <= 24576 at m <= 4, k <= 8192 at m 5 .. 8),
+// rows per workgroup (<= 16).
+constexpr int kGemvMbMax = 8;
+struct MbPlan {
+    int nbp = 0, rows = 0;         // inputs (0: choose)
+    int cg = 1, waves = 0, groups = 0;
+    int64_t grid = 0;
+};
+bool plan_gemv_mb(int64_t n, int64_t k, int m, MbPlan* p);
+bool gemv_mb_ok(const uint8_t* w, const float* x, int64_t k);
+hipError_t launch_gemv_mb(const uint8_t* w, const float* x, float* y, int64_t n, int64_t k, int m, int64_t ldy,
+                          const MbPlan& p, hipStream_t stream);
+
 // Grouped GEMV: y_i[n_i] = W_i[n_i, k] . x[k] for up to kGemvGroupMax
 // matrices sharing x (q/k/v, gate/up), in ONE launch when every W_i is Q4_K
 // (16-byte aligned) or Q6_K (4-byte aligned, even block count) and 8 lanes

@@ -17,7 +17,7 @@
 
 #include <mutex>
 
-#include "../../include/frq.h"
+#include "frq.h"
 #include "frq_kernels.h"
 
 namespace {

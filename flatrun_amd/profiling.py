@@ -3,7 +3,9 @@
     python -m flatrun_amd.profiling trace  <results.db> [--match SUBSTR]
     python -m flatrun_amd.profiling counters <results.db> [--match SUBSTR]
     python -m flatrun_amd.profiling traffic --fetch <fetch.db> --write <write.db>
-            --match SUBSTR [--copy-bytes N]
+            [--match SUBSTR ...] [--copy-bytes N]
+
+Every command takes ``--by-grid``: one row per kernel and launch shape.
 
 ``trace`` reads a ``rocprofv3 --kernel-trace`` database and prints, per
 kernel, the dispatch count and the mean / median / min duration.
@@ -166,18 +168,25 @@ def _pick(table: dict, match) -> str:
 
 
 def traffic(fetch_db: str, write_db: str, match, copy_bytes: int, by_grid: bool = False) -> dict:
+    """HBM bytes per launch of the kernel that ``match`` names; with ``match``
+    empty, of every kernel present in both databases (one object per key)."""
     f, w = pmc_means(fetch_db, by_grid), pmc_means(write_db, by_grid)
-    k_f, k_w = _pick(f, match), _pick(w, match)
     c_f, c_w = _pick(f, COPY_KERNEL), _pick(w, COPY_KERNEL)
     scale_f = copy_bytes / (f[c_f]["FETCH_SIZE"] * 1024.0)
     scale_w = copy_bytes / (w[c_w]["WRITE_SIZE"] * 1024.0)
-    fetch_b = f[k_f]["FETCH_SIZE"] * 1024.0 * scale_f
-    write_b = w[k_w]["WRITE_SIZE"] * 1024.0 * scale_w
-    return {"kernel": k_f, "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
-            "traffic_bytes": round(fetch_b + write_b),
-            "raw_fetch_kib": f[k_f]["FETCH_SIZE"], "raw_write_kib": w[k_w]["WRITE_SIZE"],
-            "copy_bytes": copy_bytes, "copy_fetch_kib": f[c_f]["FETCH_SIZE"], "copy_write_kib": w[c_w]["WRITE_SIZE"],
-            "fetch_scale": scale_f, "write_scale": scale_w}
+
+    def one(k_f: str, k_w: str) -> dict:
+        fetch_b = f[k_f]["FETCH_SIZE"] * 1024.0 * scale_f
+        write_b = w[k_w]["WRITE_SIZE"] * 1024.0 * scale_w
+        return {"kernel": k_f, "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
+                "traffic_bytes": round(fetch_b + write_b),
+                "raw_fetch_kib": f[k_f]["FETCH_SIZE"], "raw_write_kib": w[k_w]["WRITE_SIZE"],
+                "copy_bytes": copy_bytes, "copy_fetch_kib": f[c_f]["FETCH_SIZE"],
+                "copy_write_kib": w[c_w]["WRITE_SIZE"], "fetch_scale": scale_f, "write_scale": scale_w}
+
+    if match:
+        return one(_pick(f, match), _pick(w, match))
+    return {k: one(k, k) for k in f if k in w and "FETCH_SIZE" in f[k] and "WRITE_SIZE" in w[k]}
 
 
 def main(argv=None) -> int:
@@ -192,8 +201,8 @@ def main(argv=None) -> int:
     tr = sub.add_parser("traffic")
     tr.add_argument("--fetch", required=True)
     tr.add_argument("--write", required=True)
-    tr.add_argument("--match", required=True, action="append",
-                    help="substring of the kernel's key; repeat to require several")
+    tr.add_argument("--match", action="append", default=[],
+                    help="substring of the kernel's key; repeat to require several; none: every kernel")
     tr.add_argument("--copy-bytes", type=int, default=256 << 20)
     for p in (t, cn, tr):
         p.add_argument("--by-grid", action="store_true",

@@ -220,9 +220,13 @@ int frq_dev_gemv_noalloc(int qtype, const void* w, size_t w_bytes, const float* 
  *                 workgroups per row (1: k <= 16384, or 2 halves of k),
  *                 `unroll` = load depth: 1 = each wavefront issues block
  *                 j + 1's weight loads before block j's products, >= its
- *                 blocks = all of them before its x split; 0 = choose).
- *                 AUTO takes the kernel frq_dev_gemv takes. Other values
- *                 are refused with FRQ_ERR_INVALID.
+ *                 blocks = all of them before its x split; 0 = choose)
+ *                 or FRQ_GEMV_MB (Q4_K, fp32 products on the matrix cores,
+ *                 the kernel batches of 2 .. 8 rows of x take: `rows` =
+ *                 rows per workgroup (<= 16), `unroll` = pairs of blocks
+ *                 per wavefront (1 .. 3, at most 16 wavefronts cover k);
+ *                 0 = choose). AUTO takes the kernel frq_dev_gemv takes.
+ *                 Other values are refused with FRQ_ERR_INVALID.
  *   cpl           work unit per lane (format specific); with ROWS and
  *                 Q1_0, 16 selects the matrix-core Q1_0 kernel (`rows` <=
  *                 16 per workgroup, `unroll` = 128-element blocks per
@@ -233,7 +237,7 @@ int frq_dev_gemv_noalloc(int qtype, const void* w, size_t w_bytes, const float* 
  *                 kernels (an input of 0 or 1; anything else is rejected)
  *   waves_per_wg  wavefronts per workgroup (output)
  *   items         work items / workgroups launched (output)              */
-enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2, FRQ_GEMV_MX = 4 };
+enum { FRQ_GEMV_AUTO = 0, FRQ_GEMV_SPLITK = 1, FRQ_GEMV_ROWS = 2, FRQ_GEMV_MX = 4, FRQ_GEMV_MB = 8 };
 typedef struct {
     int32_t kernel, cpl, rows, unroll, slices, waves_per_wg;
     int64_t items;

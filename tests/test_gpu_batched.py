@@ -186,11 +186,13 @@ def test_batched_noalloc_fewer_splits(frq):
 @pytest.mark.parametrize("n,k,seq", [(3584, 18944, 2), (3584, 18944, 3), (3584, 18944, 6), (3584, 18944, 7),
                                      (18944, 3584, 3), (4096, 4096, 2), (1536, 8960, 5)])
 def test_batched_q4k_few_rows(frq, n, k, seq):
-    """Two to six rows of x on a Q4_K matrix run the small-M kernel in
-    launches of two or three rows: each row has the bits it gets in a batch
-    of two (a row's result does not depend on its batch); from seven rows on,
-    the GEMM. Either way within the matvec bound, with an outlier of 2^24 in
-    the last row."""
+    """Two, three, and (where k > 8192) five or six rows of x on a Q4_K
+    matrix run the small-M element-wise kernel in launches of two or three
+    rows: each row has the bits it gets in a batch of two (a row's result
+    does not depend on its batch); from seven rows on, the GEMM. Either way
+    within the matvec bound, with an outlier of 2^24 in the last row. (Four
+    rows, and five to eight at k <= 8192, take the fp32 matrix-core kernel:
+    test_gpu_gemv_mb.py.)"""
     raw = synth.make_blocks("Q4_K", n, k, seed=n + seq)
     xs = synth.make_x(k, seed=seq + 80, batch=seq)
     xs[seq - 1, 5] = 2.0**24

@@ -54,7 +54,8 @@ def _case(q, n, k, batch, seed, stream):
     ("Q4_K", [(3584, 18944, 1), (2048, 18944, 1)]),     # element-wise, no scratch
     ("Q4_K", [(8192, 4096, 1), (4096, 4096, 1)]),       # matrix cores, whole rows: no scratch
     ("Q4_K", [(4096, 14336, 1), (1536, 8960, 2)]),      # then a batched call (small-M matvec)
-    ("Q4_K", [(512, 4096, 40), (128, 4096, 8)]),        # batched GEMM: K-split partials and row flags
+    ("Q4_K", [(512, 4096, 40), (128, 4096, 12)]),       # batched GEMM: K-split partials and row flags
+    ("Q4_K", [(1024, 4096, 8), (300, 14336, 4)]),       # fp32 matrix-core small batches: no scratch
     ("Q4_K", [(300, 33024, 1), (100, 33024, 1)]),       # k > 32768: split-K partials
     ("Q6_K", [(1024, 4096, 1), (512, 4096, 1)]),        # no scratch
     ("Q8_0", [(4864, 896, 1), (1000, 896, 1)]),
