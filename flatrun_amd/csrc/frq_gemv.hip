@@ -107,18 +107,17 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
     const int g = (CPL == 2) ? sub : (sub >> 1);
     const int hh = (CPL == 2) ? 0 : (sub & 1);
     const ScaleDecode dec(g);
-    // CPL = 1, plane ownership. The two lanes of group g (hh = 0, 1) are DPP
-    // neighbours and read the same 32 qs bytes' halves; lane hh "owns" scale
-    // pair 2g + hh: its nibble plane A is the low nibbles (hh = 0) or the high
-    // nibbles (hh = 1), with A's x loaded to match, and plane B is the other.
-    // Each lane decodes only its own pair (pre-divided by 16 for the high
-    // nibbles, which enter as 16 q), adds its neighbour's plane-B dot (which
-    // belongs to this lane's pair) with one DPP add, and applies its own
-    // scale. The row sum over all lanes is unchanged.
+    // CPL = 1, scale ownership. The two lanes of group g (hh = 0, 1) are DPP
+    // neighbours and read the two halves of the group's 32 qs bytes: plane A
+    // (low nibbles) belongs to sub-block 2g, plane B (high nibbles) to 2g + 1.
+    // Lane hh decodes only the (sc, m) pair of sub-block 2g + hh and takes
+    // the other one's (s, t) from its neighbour with one DPP move each.
     const PairDecode pdec(sub);
     const bool own_hi = CPL == 1 && hh;
-    const float hfac = own_hi ? 0.0625f : 1.0f;
-    const uint32_t mask_a = own_hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu, mask_b = ~mask_a;
+    // CPL = 1: codes enter as q * u, u = the value of the fp8 code 1 (a power
+    // of two): a nibble below 16 in a byte converts exactly, two per
+    // instruction; the scales carry 1 / u so that s' * (q u) = s q exactly.
+    const float u_inv = 1.0f / fp8_unit();
 
     const int64_t row0 = rb * R;
     const int nrows = (int)(n - row0 < R ? n - row0 : R);
@@ -142,8 +141,8 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
     float xl[NE], xh[NE];                                   // x of plane A, plane B
     {
         const float* xb = x + (int64_t)gblk * kQKElems + 64 * g + 16 * hh;
-        const float* xa = xb + (own_hi ? 32 : 0);
-        const float* xo = xb + (own_hi ? 0 : 32);
+        const float* xa = xb + ((CPL == 1) ? 0 : (own_hi ? 32 : 0));
+        const float* xo = xb + ((CPL == 1) ? 32 : (own_hi ? 0 : 32));
 #pragma unroll
         for (int i = 0; i < NE; i += 4) {
             const float4 a = *reinterpret_cast<const float4*>(xa + i);
@@ -173,10 +172,12 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
         if constexpr (CPL == 1) {
             uint32_t sc0, m0;
             pdec(t.hd.y, t.hd.z, t.hd.w, sc0, m0);          // this lane's pair 2g + hh
-            sa = (d * hfac) * (float)sc0;
-            ta = dm * (float)m0;
-            sb = dpp_mov<0xB1>(sa);                         // plane B is the neighbour's pair
-            tb = dpp_mov<0xB1>(ta);
+            const float so = (d * u_inv) * (float)sc0, to = dm * (float)m0;
+            const float sn = dpp_mov<0xB1>(so), tn = dpp_mov<0xB1>(to);   // the neighbour's pair
+            sa = own_hi ? sn : so;                          // plane A: low nibbles, sub-block 2g
+            ta = own_hi ? tn : to;
+            sb = own_hi ? so : sn;                          // plane B: high nibbles, 2g + 1
+            tb = own_hi ? to : tn;
         } else {
             uint32_t sc0, m0, sc1, m1;
             dec(t.hd.y, t.hd.z, t.hd.w, sc0, m0, sc1, m1);
@@ -192,7 +193,8 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
 #pragma unroll
             for (int wd = 0; wd < 4; ++wd) {
                 float f[8];                                       // plane A, plane B
-                nibbles8(qw[wd], f, mask_a, mask_b);
+                if constexpr (CPL == 1) nibbles8_fp8(qw[wd], f);
+                else nibbles8(qw[wd], f);
                 const int e = 16 * c + 4 * wd;
                 a0 = __builtin_fmaf(__builtin_fmaf(sa, f[0], -ta), xl[e + 0], a0);
                 a1 = __builtin_fmaf(__builtin_fmaf(sa, f[1], -ta), xl[e + 1], a1);

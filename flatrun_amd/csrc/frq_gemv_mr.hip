@@ -32,37 +32,34 @@ namespace {
 
 // Q4_K lane: part p = 0..7 holds qs bytes 16p .. 16p+15 of its block, i.e.
 // group g = p / 2 (bytes 32g .. 32g+31: sub-block 2g in the low, 2g + 1 in
-// the high nibbles) and its half hf = p % 2, so low nibbles are elements
-// 64g + 16hf + t and high nibbles 64g + 32 + 16hf + t (t < 16).
-// Plane ownership: lane hf owns scale pair 2g + hf, whose weights are its
-// plane A (low nibbles for hf = 0, high for hf = 1, as 16 q with the scale
-// pre-divided by 16); plane B is the other nibble plane, whose pair the DPP
-// neighbour (lane ^ 1) owns. Each lane decodes one pair and reads the
-// neighbour's (s, t) with one DPP move each.
+// the high nibbles) and its half hf = p % 2, so low nibbles (plane A) are
+// elements 64g + 16hf + t and high nibbles (plane B) 64g + 32 + 16hf + t
+// (t < 16). Lane hf decodes the (sc, m) pair of sub-block 2g + hf only and
+// reads the other one's (s, t) from its DPP neighbour (lane ^ 1). Codes
+// enter as q * u (fp8 conversion, two per instruction; the scale carries
+// 1 / u), as in the single-row element-wise kernel.
 struct Q4KMrLane {
     static constexpr int kLanes = 8, kBytes = kQ4KBytes, kElems = kQKElems;
     using X = float[2][16];                             // x of plane A, plane B
     struct Row {
         uint4 hd, qv;
     };
-    uint32_t off_h, off_q, mask_a, mask_b;
-    float hfac;
+    uint32_t off_h, off_q;
+    float u_inv;
     int g, hf;
     PairDecode pdec;
 
     __device__ __forceinline__ Q4KMrLane(int blk, int p) : pdec(p) {
         g = p >> 1;
         hf = p & 1;
-        hfac = hf ? 0.0625f : 1.0f;
-        mask_a = hf ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-        mask_b = ~mask_a;
+        u_inv = 1.0f / fp8_unit();
         off_h = (uint32_t)blk * kQ4KBytes;
         off_q = off_h + 16 + 32 * g + 16 * hf;
     }
     __device__ __forceinline__ void load_x(const float* __restrict__ xrow, int blk, X& xv) const {
         const float* xb = xrow + (int64_t)blk * kQKElems + 64 * g + 16 * hf;
-        const float* xa = xb + (hf ? 32 : 0);
-        const float* xo = xb + (hf ? 0 : 32);
+        const float* xa = xb;
+        const float* xo = xb + 32;
 #pragma unroll
         for (int i = 0; i < 16; i += 4) {
             const float4 a = *reinterpret_cast<const float4*>(xa + i);
@@ -80,8 +77,10 @@ struct Q4KMrLane {
         uint32_t sc0, m0;
         pdec(t.hd.y, t.hd.z, t.hd.w, sc0, m0);
         const float d = f16_bits_to_f32(t.hd.x), dm = f16_bits_to_f32(t.hd.x >> 16);
-        const float sa = (d * hfac) * (float)sc0, ta = dm * (float)m0;    // exact
-        const float sb = dpp_mov<0xB1>(sa), tb = dpp_mov<0xB1>(ta);     // quad_perm [1,0,3,2]
+        const float so = (d * u_inv) * (float)sc0, to = dm * (float)m0;  // exact
+        const float sn = dpp_mov<0xB1>(so), tn = dpp_mov<0xB1>(to);     // quad_perm [1,0,3,2]
+        const float sa = hf ? sn : so, ta = hf ? tn : to;               // plane A: sub-block 2g
+        const float sb = hf ? so : sn, tb = hf ? to : tn;               // plane B: 2g + 1
         float a[M], b[M];
 #pragma unroll
         for (int r = 0; r < M; ++r) a[r] = b[r] = 0.0f;
@@ -89,7 +88,7 @@ struct Q4KMrLane {
 #pragma unroll
         for (int wd = 0; wd < 4; ++wd) {
             float f[8];
-            nibbles8(qw[wd], f, mask_a, mask_b);        // f[0..3] plane A, f[4..7] plane B
+            nibbles8_fp8(qw[wd], f);                    // f[0..3] plane A, f[4..7] plane B
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const float wl = __builtin_fmaf(sa, f[c], -ta);

@@ -108,14 +108,16 @@ def test_ragged_shapes(frq, q, n, k):
 
 def test_q4k_row_bits_independent_of_batch(frq):
     """A Q4_K row's bits depend only on the row: the same x row gives the
-    same output in a batch of 2, 3, 4, 5 or 6 (launches of two and of three
-    rows) at any position."""
+    same output in a batch of 2, 3, 5 or 6 (launches of two and of three rows
+    of this kernel) at any position. (Four rows take the fp32 matrix-core
+    kernel, whose rows are position- and content-independent within their
+    batch size: test_gpu_gemv_mb.py.)"""
     n, k = 3584, 18944
     raw = synth.make_blocks("Q4_K", n, k, seed=5)
     pool = synth.make_x(k, seed=6, batch=6)
     probe = pool[2].copy()
     ref = None
-    for seq in (2, 3, 4, 5, 6):
+    for seq in (2, 3, 5, 6):
         for pos in sorted({0, seq - 1, seq // 2}):
             xs = pool[:seq].copy()
             xs[pos] = probe
