@@ -172,11 +172,15 @@ int frq_dev_dequant_f16(int qtype, const void* w, size_t w_bytes, int64_t n_elem
  * x with any value outside that range (tiny, subnormal, huge, inf, NaN) is
  * computed again weight by weight in fp64 (one rounding; inf and NaN as
  * IEEE arithmetic has them) by a second kernel. A few
- * rows (Q4_K, Q8_0: up to 6; Q6_K: up to 10) run the small-M matvec instead
- * when W and k suit it (one launch per two or three rows, W read once per
- * launch; Q4_K with per-weight fp32 arithmetic as one row, a row's bits
- * independent of its batch; Q6_K and Q8_0 with the bits of a batch-1 call);
- * up to 3 rows that it does not take run one GEMV per row. Few output
+ * rows run a small-M matvec instead, W read once per launch: Q4_K with 4
+ * rows (k <= 24576), or 5 to 8 rows where k <= 8192, in one launch of the
+ * fp32 matrix-core matvec (per-weight dequant, each product fused into an
+ * fp32 sum by v_mfma_f32_4x4x1_16b_f32; a row's bits independent of the
+ * other rows and of its position); otherwise (Q4_K, Q8_0: up to 6 rows;
+ * Q6_K: up to 10) the element-wise small-M matvec, one launch per two or
+ * three rows (Q4_K with per-weight fp32 arithmetic as one row, a row's bits
+ * the same in any batch this kernel takes; Q6_K and Q8_0 with the bits of a
+ * batch-1 call); up to 3 rows that neither takes run one GEMV per row. Few output
  * tiles split k over workgroups whose fp32 partials a second kernel adds in
  * a fixed order (scratch of the stream). Q5_K and Q1_0 run one matvec per
  * row. */
@@ -194,9 +198,8 @@ int frq_dev_gemv(int qtype, const void* w, size_t w_bytes, const float* x, float
  * rows so today) and 3 MiB of split-K partials (n x slices x 4 bytes, rows
  * longer than one workgroup). A batch-1 shape that needs more is refused
  * with FRQ_ERR_UNSUPPORTED before anything is launched. A batch that takes
- * the small-M matvec (2 to 6 rows of Q4_K or Q8_0, 2 to 10 of Q6_K, on
- * matrices it accepts) needs no scratch; a batch that takes the batched
- * GEMM (4 or more rows of Q4_K, Q6_K, Q8_0) keeps one flag word per row of x
+ * a small-M matvec (see frq_dev_gemv) needs no scratch; a batch that takes
+ * the batched GEMM (more rows of Q4_K, Q6_K, Q8_0) keeps one flag word per row of x
  * in the 3 MiB and splits k only as far as its partials (splits x batch x n
  * x 4 bytes) fit beside them, so neither is refused (up to 786432 rows); where the GEMM splits less than
  * frq_dev_gemv would, the bits differ from frq_dev_gemv's within the same
