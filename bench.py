@@ -907,7 +907,7 @@ def decode_sweep_resident(stream, steps: int, layers: int = 32, cpu_baseline_on:
                    for parts, k in groups[0] if len(parts) > 1)
     ycat.free()
     # the forwarder's chain with resident activations (flatrun_amd.layer):
-    # q|k|v -> o (on the q part) -> gate|up -> SiLU.mul -> down, per layer
+    # q|k|v -> o (on the q part) -> gate|up and SiLU.mul -> down, per layer
     from flatrun_amd.layer import DecoderProjections
 
     drivers = [DecoderProjections({nm: (spec[nm][0], dev[L][nm], spec[nm][1], kk, host[nm].nbytes)
@@ -919,6 +919,9 @@ def decode_sweep_resident(stream, steps: int, layers: int = 32, cpu_baseline_on:
             qkv = dp.qkv_proj(x)
             dp.mlp(dp.o_proj(qkv))          # seq 1: the q part leads each qkv row
 
+    k_gate = {nm: kk for nm, _, _, kk in LLAMA_LAYER}["gate"]
+    mlp_fused = all(device.gemv_swiglu_fusable((spec["gate"][0], dev[L]["gate"]), (spec["up"][0], dev[L]["up"]),
+                                               k_gate) for L in range(layers))
     with device.Graph.capture(stream) as capd:
         step_driver()
     ms_d = timed(lambda: capd.launch(stream))
@@ -936,11 +939,12 @@ def decode_sweep_resident(stream, steps: int, layers: int = 32, cpu_baseline_on:
             "fused_shared_x": {"ms_per_step": round(ms_f, 4), "launches_per_step": layers * 4,
                                "gbs": round(total / (ms_f / 1e3) / 1e9, 1), "groups_fused": fused_ok,
                                "note": "q|k|v and gate|up as one grouped launch each"},
-            "decoder_chain_resident": {"ms_per_step": round(ms_d, 4), "launches_per_step": layers * 5,
-                                       "gbs": round(total / (ms_d / 1e3) / 1e9, 1),
+            "decoder_chain_resident": {"ms_per_step": round(ms_d, 4),
+                                       "launches_per_step": layers * (4 if mlp_fused else 5),
+                                       "gbs": round(total / (ms_d / 1e3) / 1e9, 1), "mlp_fused": mlp_fused,
                                        "note": "DecoderProjections per layer: q|k|v grouped, o on the q part, "
-                                               "gate|up grouped, SiLU.mul, down; activations resident, "
-                                               "one graph per step"}}
+                                               "gate|up and SiLU.mul in one launch (frq_dev_gemv_swiglu), "
+                                               "down; activations resident, one graph per step"}}
 
 
 def main() -> int:

@@ -113,6 +113,8 @@ SIGNATURES: dict[str, list] = {
     "frq_dev_copy": [_vp, _vp, _sz, _vp],
     "frq_dev_read_xor": [_vp, _sz, _vp, _vp],
     "frq_dev_silu_mul": [_vp, _i64, _vp, _i64, _i64, _i64, _vp],
+    "frq_dev_gemv_swiglu": [_i32, _vp, _sz, _i32, _vp, _sz, _i64, _vp, _i64, _vp, _vp, _i64, _vp],
+    "frq_gemv_swiglu_fusable": [_i32, _vp, _i32, _vp, _i64],
     "frq_set_device": [_i32],
     "frq_malloc": [_c.POINTER(_vp), _sz],
     "frq_free": [_vp],

@@ -14,14 +14,6 @@
 namespace frq {
 namespace {
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    float e = expf(-g);
-    e = e + 1.0f;
-    e = 1.0f / e;
-    e = e * g;
-    return e * u;
-}
-
 __global__ void __launch_bounds__(256) silu_mul_kernel(const float* __restrict__ gateup, int64_t ld_in,
                                                        float* __restrict__ out, int64_t ld_out, int64_t rows,
                                                        int64_t inter) {

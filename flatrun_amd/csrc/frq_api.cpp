@@ -867,6 +867,40 @@ int frq_dev_silu_mul(const float* gateup, int64_t ld_in, float* out, int64_t ld_
     return FRQ_OK;
 }
 
+int frq_dev_gemv_swiglu(int qtype_gate, const void* w_gate, size_t gate_bytes, int qtype_up, const void* w_up,
+                        size_t up_bytes, int64_t inter, const float* x, int64_t k, float* gateup, float* act,
+                        int64_t batch, void* stream) {
+    if (inter < 0) return fail(FRQ_ERR_SHAPE, "gemv swiglu: negative inter");
+    if (!act) return fail(FRQ_ERR_INVALID, "gemv swiglu: null act");
+    if (reinterpret_cast<uintptr_t>(act) & 3) return fail(FRQ_ERR_ALIGN, "gemv swiglu: act must be 4-byte aligned");
+    Fmt f;
+    if (int rc = dev_gemv_checks(qtype_gate, w_gate, gate_bytes, x, gateup, inter, k, batch, &f)) return rc;
+    if (int rc = dev_gemv_checks(qtype_up, w_up, up_bytes, x, gateup, inter, k, batch, &f)) return rc;
+    if (inter == 0 || batch == 0) return FRQ_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t* wg = static_cast<const uint8_t*>(w_gate);
+    const uint8_t* wu = static_cast<const uint8_t*>(w_up);
+    if (batch == 1 && frq::gemv_swiglu_fusable(qtype_gate, wg, qtype_up, wu, k)) {
+        FRQ_HIP(frq::launch_gemv_swiglu(wg, wu, x, gateup, act, inter, k, s));
+        return FRQ_OK;
+    }
+    const int qt[2] = {qtype_gate, qtype_up};
+    const void* wp[2] = {w_gate, w_up};
+    const size_t wb[2] = {gate_bytes, up_bytes};
+    const int64_t nn[2] = {inter, inter};
+    float* yy[2] = {gateup, gateup + inter};
+    if (int rc = frq_dev_gemv_group(2, qt, wp, wb, nn, x, k, yy, batch, 2 * inter, stream)) return rc;
+    FRQ_HIP(frq::launch_silu_mul(gateup, 2 * inter, act, inter, batch, inter, s));
+    return FRQ_OK;
+}
+
+int frq_gemv_swiglu_fusable(int qtype_gate, const void* w_gate, int qtype_up, const void* w_up, int64_t k) {
+    return frq::gemv_swiglu_fusable(qtype_gate, static_cast<const uint8_t*>(w_gate), qtype_up,
+                                    static_cast<const uint8_t*>(w_up), k)
+               ? 1
+               : 0;
+}
+
 int frq_set_device(int device) { FRQ_HIP(hipSetDevice(device)); return FRQ_OK; }
 int frq_malloc(void** ptr, size_t bytes) {
     if (!ptr) return fail(FRQ_ERR_INVALID, "null ptr");

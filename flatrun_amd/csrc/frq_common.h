@@ -140,6 +140,17 @@ __device__ __forceinline__ void nibbles8(uint32_t w, float (&f)[8], uint32_t mas
         : "v"(mask_a), "v"(mask_b), "v"(w));
 }
 
+// SwiGLU's silu(g) * u with the forwarder's operations and roundings
+// (model/qwen2.py:1703-1740): e = exp(-g); e = e + 1; e = 1 / e; e = e * g;
+// e * u -- each rounded, no FMA, the reciprocal a correctly rounded division.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    float e = expf(-g);
+    e = e + 1.0f;
+    e = 1.0f / e;
+    e = e * g;
+    return e * u;
+}
+
 // The value of the fp8 (e4m3) code 1: a power of two u such that a byte
 // holding q < 16 converts to q * u exactly (codes below 8 are subnormal,
 // 8 .. 15 have the smallest exponent; both read as q * u).

@@ -94,7 +94,8 @@ __device__ __forceinline__ void finish_rows(int64_t row0, int64_t row_end, float
 // kernel below passes the index inside its segment).
 template <int CPL, int U, int R>
 __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                               float* __restrict__ y, int64_t n, int nb, int64_t wg) {
+                                               float* __restrict__ y, int64_t n, int nb, int64_t wg,
+                                               float* keep = nullptr) {
     static_assert(U <= R, "ring deeper than the row count");
     __shared__ float red[R * 64];                           // [row][wave][DPP row]
     constexpr int LPB = 8 / CPL;
@@ -218,6 +219,7 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
         float s = 0.0f;
         for (int w2 = 0; w2 < 4 * nwaves; ++w2) s += red[r * 4 * nwaves + w2];
         y[row0 + r] = s;
+        if (keep) keep[r] = s;                              // the caller's LDS copy (fused epilogues)
     }
 }
 
@@ -490,6 +492,27 @@ __global__ void __launch_bounds__(1024) gemv_group_kernel(GemvGroup g, const flo
         gemv_q4_k_body<1, (R < 3 ? R : 3), R>(g.w[i], x, g.y[i], g.n[i], nb, wg);
     else
         gemv_q6_k_ring_body<(R < 4 ? R : 4), R>(g.w[i], x, g.y[i], g.n[i], nb, wg);
+}
+
+// Gate and up of a SwiGLU block in one launch, with the activation: workgroup
+// w runs the Q4_K row body on rows [w R, w R + R) of W_gate, then on the same
+// rows of W_up (x reread from cache), writing both to gateup as the grouped
+// launch does (bit-identical rows), and the threads that wrote row r of
+// each apply act[r] = silu(gate[r]) * up[r] with silu_mul's operations.
+template <int R>
+__global__ void __launch_bounds__(1024) gemv_swiglu_kernel(const uint8_t* __restrict__ wgate,
+                                                          const uint8_t* __restrict__ wup,
+                                                          const float* __restrict__ x, float* __restrict__ gateup,
+                                                          float* __restrict__ act, int64_t inter, int nb) {
+    __shared__ float kg[R], ku[R];
+    const int64_t b = blockIdx.x;
+    gemv_q4_k_body<1, (R < 3 ? R : 3), R>(wgate, x, gateup, inter, nb, b, kg);
+    __syncthreads();                                        // the body's reduction array is reused
+    gemv_q4_k_body<1, (R < 3 ? R : 3), R>(wup, x, gateup + inter, inter, nb, b, ku);
+    const int64_t row0 = b * R;
+    const int nrows = (int)(inter - row0 < R ? inter - row0 : R);
+    for (int r = threadIdx.x; r < nrows; r += blockDim.x)   // the same thread wrote kg[r] and ku[r]
+        act[row0 + r] = silu_mul(kg[r], ku[r]);
 }
 
 // ------------------------------------------------------------------ Q8_0
@@ -1164,6 +1187,43 @@ hipError_t launch_gemv(int qtype, const uint8_t* w, const float* x, float* y, in
     if (p.unroll == 8)
         return launch_u<8>(qtype, p.cpl, w, x, y, n, (int)nb, p.rows_per_wg, p.waves, p.grid, stream);
     return launch_u<4>(qtype, p.cpl, w, x, y, n, (int)nb, p.rows_per_wg, p.waves, p.grid, stream);
+}
+
+bool gemv_swiglu_fusable(int qtype_gate, const uint8_t* wgate, int qtype_up, const uint8_t* wup, int64_t k) {
+    return qtype_gate == kTypeQ4K && qtype_up == kTypeQ4K && k > 0 && k % kQKElems == 0 &&
+           (k / kQKElems) * 8 <= 1024 && !(reinterpret_cast<uintptr_t>(wgate) & 15) &&
+           !(reinterpret_cast<uintptr_t>(wup) & 15);
+}
+
+template <int R>
+static void swiglu_go(int64_t grid, int waves, const uint8_t* wgate, const uint8_t* wup, const float* x,
+                      float* gateup, float* act, int64_t inter, int nb, hipStream_t s) {
+    gemv_swiglu_kernel<R><<<dim3((unsigned)grid), dim3((unsigned)(64 * waves)), 0, s>>>(wgate, wup, x, gateup, act,
+                                                                                         inter, nb);
+}
+
+hipError_t launch_gemv_swiglu(const uint8_t* wgate, const uint8_t* wup, const float* x, float* gateup, float* act,
+                              int64_t inter, int64_t k, hipStream_t s) {
+    if (inter <= 0) return hipSuccess;
+    if (!gemv_swiglu_fusable(kTypeQ4K, wgate, kTypeQ4K, wup, k)) return hipErrorInvalidValue;
+    const int64_t nb = k / kQKElems;
+    const int waves = (int)((nb * 8 + 63) / 64);
+    // rows per workgroup: half of what the grouped launch gives the 2 inter
+    // rows, so that a workgroup runs the same row count
+    int R = pick_rows_q4k(2 * inter, waves) / 2;
+    if (R < 1) R = 1;
+    if (R == 3) R = 2;
+    const int64_t grid = (inter + R - 1) / R;
+    if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    switch (R) {
+        case 1: swiglu_go<1>(grid, waves, wgate, wup, x, gateup, act, inter, (int)nb, s); break;
+        case 2: swiglu_go<2>(grid, waves, wgate, wup, x, gateup, act, inter, (int)nb, s); break;
+        case 4: swiglu_go<4>(grid, waves, wgate, wup, x, gateup, act, inter, (int)nb, s); break;
+        case 7: swiglu_go<7>(grid, waves, wgate, wup, x, gateup, act, inter, (int)nb, s); break;
+        case 8: swiglu_go<8>(grid, waves, wgate, wup, x, gateup, act, inter, (int)nb, s); break;
+        default: return hipErrorInvalidConfiguration;
+    }
+    return hipGetLastError();
 }
 
 bool gemv_group_fusable(int count, const int* qtypes, const uint8_t* const* w, int64_t k) {

@@ -205,6 +205,14 @@ hipError_t launch_gemm_f32(int qtype, const uint8_t* w, const float* x, float* y
 
 // out[r, i] = silu(gateup[r, i]) * gateup[r, inter + i] for r < rows, rows of
 // gateup ld_in floats apart and of out ld_out apart (frq_act.hip).
+// Gate and up of a SwiGLU block and its activation in one launch (batch 1,
+// both Q4_K, 16-byte aligned, k a multiple of 256 with 8 lanes per block
+// covering it): gateup[0, 2 inter) = [W_gate x | W_up x] with the grouped
+// launch's bits, act[i] = silu(gate[i]) * up[i] with silu_mul's.
+bool gemv_swiglu_fusable(int qtype_gate, const uint8_t* wgate, int qtype_up, const uint8_t* wup, int64_t k);
+hipError_t launch_gemv_swiglu(const uint8_t* wgate, const uint8_t* wup, const float* x, float* gateup, float* act,
+                              int64_t inter, int64_t k, hipStream_t s);
+
 hipError_t launch_silu_mul(const float* gateup, int64_t ld_in, float* out, int64_t ld_out, int64_t rows,
                            int64_t inter, hipStream_t stream);
 

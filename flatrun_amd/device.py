@@ -349,6 +349,28 @@ def dequant_f16(qtype, w, y, n_elems: int, stream=None, w_bytes: int | None = No
     check(lib().frq_dev_dequant_f16(q, _addr(w), wb, int(n_elems), _addr(y), _stream(stream)))
 
 
+def gemv_swiglu(gate, up, x, k: int, gateup, act, batch: int = 1, stream=None) -> None:
+    """gateup[r] = [W_gate x_r | W_up x_r] and act[r] = silu(gate) * up for
+    `batch` rows of x, enqueued (frq_dev_gemv_swiglu: one launch for a Q4_K
+    pair at batch 1, else the grouped launch and frq_dev_silu_mul, same
+    bits). ``gate`` / ``up``: ``(qtype, w, inter[, w_bytes])``."""
+    qg, wg, inter = gate[0], gate[1], int(gate[2])
+    qu, wu = up[0], up[1]
+    gb = int(gate[3]) if len(gate) > 3 else _nbytes(wg)
+    ub = int(up[3]) if len(up) > 3 else _nbytes(wu)
+    if int(up[2]) != inter:
+        raise ValueError(f"gate and up need the same output size, got {inter} and {up[2]}")
+    check(lib().frq_dev_gemv_swiglu(qtype_id(qg), _addr(wg), gb, qtype_id(qu), _addr(wu), ub, inter, _addr(x),
+                                    int(k), _addr(gateup), _addr(act), int(batch), _stream(stream)))
+
+
+def gemv_swiglu_fusable(gate, up, k: int) -> bool:
+    """True if gemv_swiglu runs ``gate`` and ``up`` ((qtype, w, ...)) and the
+    activation as one launch at batch 1."""
+    return bool(lib().frq_gemv_swiglu_fusable(qtype_id(gate[0]), _addr(gate[1]), qtype_id(up[0]), _addr(up[1]),
+                                              int(k)))
+
+
 def silu_mul(gateup, out, rows: int, inter: int, ld_in: int = 0, ld_out: int = 0, stream=None) -> None:
     """out[r, :inter] = silu(gate) * up for the grouped gate|up rows of
     gateup (gate first; rows ld_in floats apart, default 2 inter; out rows

@@ -13,7 +13,9 @@ keeps every activation of that chain in device buffers:
     xn ─▶ [gate|up] grouped ─▶ gateup ─▶ SiLU·mul ─▶ act ─▶ down ─▶ mlp_out
 
 The projections are frq_dev_gemv_group / frq_dev_gemv launches (fp32
-contract, 1e-5 of fp64), SiLU·mul is frq_dev_silu_mul, all on one stream.
+contract, 1e-5 of fp64); gate, up and SiLU·mul are frq_dev_gemv_swiglu (one
+launch for a Q4_K pair at batch 1, the grouped launch and frq_dev_silu_mul
+otherwise, same bits); all on one stream.
 Attention, RoPE, norms and residuals are not quantized matvecs; the caller
 supplies them as functions on device buffers (or does them itself between
 :meth:`qkv`, :meth:`o` and :meth:`mlp`).
@@ -121,11 +123,8 @@ class DecoderProjections:
         """mlp_out = W_down (silu(W_gate xn) * W_up xn); returns mlp_out."""
         seq = self._check_seq(seq)
         g, u = self.p["gate"], self.p["up"]
-        base = self.gateup.ptr
-        device.gemv_group([(g.qtype, g.weight, g.n, base, g.nbytes),
-                           (u.qtype, u.weight, u.n, base + 4 * g.n, u.nbytes)],
-                          xn, self.hidden, batch=seq, y_stride=2 * self.inter, stream=self.stream)
-        device.silu_mul(self.gateup, self.act, seq, self.inter, stream=self.stream)
+        device.gemv_swiglu((g.qtype, g.weight, g.n, g.nbytes), (u.qtype, u.weight, u.n, u.nbytes), xn,
+                           self.hidden, self.gateup, self.act, batch=seq, stream=self.stream)
         self._gemv("down", self.act, self.mlp_out, seq)
         return self.mlp_out
 

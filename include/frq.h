@@ -321,6 +321,25 @@ int frq_dev_read_xor(const void* src, size_t bytes, uint32_t* out, void* stream)
 int frq_dev_silu_mul(const float* gateup, int64_t ld_in, float* out, int64_t ld_out, int64_t rows, int64_t inter,
                      void* stream);
 
+/* A decoder block's gate and up projections and their SwiGLU activation
+ * (replaces the forwarder's gate and up matmuls, their np.concatenate and
+ * the in-place SwiGLU chain, model/qwen2.py:1690-1740): for each of `batch`
+ * rows of x (k floats apart), gateup[r * 2 inter + [0, inter)] = W_gate x_r,
+ * gateup[r * 2 inter + [inter, 2 inter)] = W_up x_r and
+ * act[r * inter + i] = silu(gate_i) * up_i, with W_gate and W_up
+ * [inter x k] blocks of qtype_gate / qtype_up. The results are bit for bit
+ * those of frq_dev_gemv_group over the two matrices (y_stride 2 inter)
+ * followed by frq_dev_silu_mul. With batch 1, both matrices Q4_K (16-byte
+ * aligned) and 8 lanes per block covering k (k <= 32768), it is one launch:
+ * each workgroup computes the same rows of both matrices and applies the
+ * activation; otherwise those two calls. Status codes as frq_dev_gemv. */
+int frq_dev_gemv_swiglu(int qtype_gate, const void* w_gate, size_t gate_bytes, int qtype_up, const void* w_up,
+                        size_t up_bytes, int64_t inter, const float* x, int64_t k, float* gateup, float* act,
+                        int64_t batch, void* stream);
+/* 1 if frq_dev_gemv_swiglu runs these two matrices and the activation as one
+ * launch at batch 1, else 0. */
+int frq_gemv_swiglu_fusable(int qtype_gate, const void* w_gate, int qtype_up, const void* w_up, int64_t k);
+
 /* ------------------------------------------- memory, streams and events
  * Thin wrappers so a ctypes caller needs no other HIP binding. Streams are
  * created at the default priority.                                         */

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 from conftest import assert_matvec_close
-from flatrun_amd import device, synth
+from flatrun_amd import _lib, device, synth
 from flatrun_amd.layer import DecoderProjections
 from oracle import gguf_np as G
 
@@ -161,3 +161,85 @@ def test_silu_mul_rejects(frq):
         assert _lib.lib().frq_dev_silu_mul(b.ptr, 12, b.ptr, 6, 0, 6, None) == 0     # no rows: nothing to do
     finally:
         b.free()
+
+
+def _swiglu_pair(gq, uq, inter, k, batch, seed):
+    g_raw = synth.make_blocks(gq, inter, k, seed=seed)
+    u_raw = synth.make_blocks(uq, inter, k, seed=seed + 1)
+    xs = synth.make_x(k, seed=seed + 2, batch=batch if batch > 1 else None).reshape(batch, k)
+    bufs = [device.DeviceBuffer.from_host(g_raw), device.DeviceBuffer.from_host(u_raw),
+            device.DeviceBuffer.from_host(xs)]
+    out = [device.DeviceBuffer(4 * batch * 2 * inter) for _ in range(2)] + \
+          [device.DeviceBuffer(4 * batch * inter) for _ in range(2)]
+    try:
+        wg, wu, x = bufs
+        gu_f, gu_r, act_f, act_r = out
+        nan = np.full(batch * 2 * inter, np.nan, np.float32)
+        for b in (gu_f, gu_r):
+            _lib.check(_lib.lib().frq_memcpy_h2d(b.ptr, nan.ctypes.data, nan.nbytes))
+        device.gemv_swiglu((gq, wg, inter, g_raw.nbytes), (uq, wu, inter, u_raw.nbytes), x, k, gu_f, act_f,
+                           batch=batch)
+        device.gemv_group([(gq, wg, inter, gu_r.ptr, g_raw.nbytes), (uq, wu, inter, gu_r.ptr + 4 * inter, u_raw.nbytes)],
+                          x, k, batch=batch, y_stride=2 * inter)
+        device.silu_mul(gu_r, act_r, batch, inter)
+        device.synchronize()
+        return [b.to_host(np.float32) for b in out], (g_raw, u_raw, xs)
+    finally:
+        for b in bufs + out:
+            b.free()
+
+
+@pytest.mark.parametrize("gq,uq,inter,k,batch", [
+    ("Q4_K", "Q4_K", 14336, 4096, 1), ("Q4_K", "Q4_K", 1000, 4096, 1), ("Q4_K", "Q4_K", 37, 2048, 1),
+    ("Q4_K", "Q4_K", 18944, 3584, 1), ("Q4_K", "Q4_K", 300, 4096, 3), ("Q6_K", "Q4_K", 512, 4096, 1),
+    ("Q4_K", "Q4_K", 5, 40960, 1),
+])
+def test_gemv_swiglu_matches_group_and_silu(frq, gq, uq, inter, k, batch):
+    """frq_dev_gemv_swiglu gives the bits of the grouped gate|up launch plus
+    frq_dev_silu_mul: fused (a Q4_K pair at batch 1, k covered by one
+    workgroup, ragged last workgroup) and through those two calls (batch 3,
+    a Q6_K gate, k beyond one workgroup); gate and up within the matvec
+    contract."""
+    (gu_f, gu_r, act_f, act_r), (g_raw, u_raw, xs) = _swiglu_pair(gq, uq, inter, k, batch, seed=inter + k)
+    assert np.array_equal(gu_f.view(np.uint32), gu_r.view(np.uint32))
+    assert np.array_equal(act_f.view(np.uint32), act_r.view(np.uint32))
+    gu = gu_f.reshape(batch, 2 * inter)
+    for name, raw, cols in (("gate", g_raw, slice(0, inter)), ("up", u_raw, slice(inter, 2 * inter))):
+        q = gq if name == "gate" else uq
+        y64 = G.matmul_f64(q, xs, raw, inter, k)
+        a64 = G.abs_matmul_f64(q, xs, raw, inter, k)
+        for r in range(batch):
+            assert_matvec_close(gu[r, cols], y64[r], a64[r], what=f"{name} row {r}")
+
+
+def test_gemv_swiglu_rejects(frq):
+    raw = synth.make_blocks("Q4_K", 8, 256, seed=1)
+    w = device.DeviceBuffer.from_host(raw)
+    x = device.DeviceBuffer.from_host(synth.make_x(256, seed=2))
+    y = device.DeviceBuffer(4 * 16)
+    try:
+        with pytest.raises(ValueError):         # up of another size
+            device.gemv_swiglu(("Q4_K", w, 8, raw.nbytes), ("Q4_K", w, 4, raw.nbytes), x, 256, y, y)
+        with pytest.raises(RuntimeError):       # weight byte size mismatch
+            device.gemv_swiglu(("Q4_K", w, 8, raw.nbytes - 1), ("Q4_K", w, 8, raw.nbytes), x, 256, y, y)
+        with pytest.raises(RuntimeError):       # null act
+            device.gemv_swiglu(("Q4_K", w, 8, raw.nbytes), ("Q4_K", w, 8, raw.nbytes), x, 256, y, 0)
+    finally:
+        w.free()
+        x.free()
+        y.free()
+
+
+def test_gemv_swiglu_fusable(frq):
+    """The one-launch condition: a Q4_K pair, 16-byte aligned, k covered by
+    one workgroup (8 lanes per block, k <= 32768)."""
+    raw = synth.make_blocks("Q4_K", 4, 4096, seed=3)
+    w = device.DeviceBuffer.from_host(raw)
+    try:
+        assert device.gemv_swiglu_fusable(("Q4_K", w), ("Q4_K", w), 4096)
+        assert device.gemv_swiglu_fusable(("Q4_K", w), ("Q4_K", w), 32768)
+        assert not device.gemv_swiglu_fusable(("Q4_K", w), ("Q4_K", w), 32768 + 256)
+        assert not device.gemv_swiglu_fusable(("Q6_K", w), ("Q4_K", w), 4096)
+        assert not device.gemv_swiglu_fusable(("Q4_K", w), ("Q4_K", w.ptr + 8), 4096)
+    finally:
+        w.free()
