@@ -35,9 +35,10 @@
 // (the next pair's x is in flight meanwhile), then for each row group the
 // two 16-byte loads per lane (block header, the lane's qs bytes) that a ring
 // of two slots keeps one step ahead. Accumulators persist per row group over
-// the pairs; at the end each row group's 16 k slots are summed across lanes
-// (DPP within 16-lane rows, then across rows) and the waves' partials meet in
-// LDS, added in a fixed order. A row's result depends on its own x only: not
+// the pairs; at the end each row group's four k slots per 16-lane row are
+// summed with DPP, and the four rows' partials of every wave meet in LDS,
+// added in a fixed order. The last wavefront skips the pairs past the row's
+// end (a wave-uniform branch). A row's result depends on its own x only: not
 // on m, on the other rows of x, or on which column it takes.
 #include "frq_common.h"
 #include "frq_kernels.h"
@@ -74,13 +75,12 @@ __device__ __forceinline__ void mb_load_x(__amdgpu_buffer_rsrc_t xs, int64_t k, 
     }
 }
 
-// Sum over the 16 k slots of a 4-register accumulator: lane 4 kb + j ends
-// with the sum over kb for every register (the same order for every j).
-__device__ __forceinline__ float mb_slot_sum(float v) {
+// Sum over the four k slots of a 16-lane row (lanes 4 kb + j, kb in
+// 4q .. 4q + 3): lane 16q + j (j < 4) ends with it, the same order for
+// every j.
+__device__ __forceinline__ float mb_row_sum(float v) {
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false));
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
     return v;
 }
 
@@ -88,7 +88,7 @@ template <int NBP, int G, int CG>
 __global__ void __launch_bounds__(1024) gemv_q4_k_mb_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                            float* __restrict__ y, int64_t n, int nb, int m, int R,
                                                            int64_t ldy) {
-    extern __shared__ float red[];                      // [4 G rows][4 CG x rows][waves]
+    extern __shared__ float red[];                      // [4 G rows][4 CG x rows][waves][4 DPP rows]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
     const int c = lane & 3, kb = lane >> 2, p = kb >> 3, h = kb & 7, g = h >> 1, hh = h & 1;
     const int64_t k = (int64_t)nb * kQKElems;
@@ -101,9 +101,11 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mb_kernel(const uint8_t* __res
     const float u_inv = 1.0f / fp8_unit();
     const ScaleDecode dec(g);
 
-    // block of pair jp for this lane; invalid past the row's end (x = 0, s = t = 0)
+    // block of pair jp for this lane; invalid past the row's end (x = 0, s = t = 0).
+    // The last wavefront may own fewer pairs: it skips the others (uniform).
     auto blk_of = [&](int jp) { return 2 * (wave * NBP + jp) + p; };
     auto valid_of = [&](int jp) { return wave * NBP + jp < npairs && blk_of(jp) < nb; };
+    const int own = npairs - wave * NBP < NBP ? npairs - wave * NBP : NBP;   // >= 1
 
     struct Slot {
         uint4 hd, qv;
@@ -128,14 +130,17 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mb_kernel(const uint8_t* __res
     mb_load_x<CG>(xs, k, c, valid_of(0), blk_of(0), g, hh, xb[0]);
     __builtin_amdgcn_sched_barrier(0);
     load(0, ring[0]);
-    if constexpr (NBP * G > 1) load(1, ring[1]);
+    if constexpr (NBP * G > 1) {
+        if ((1 / G) < own) load(1, ring[1]);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     static_for<0, NBP * G>([&](auto sc) {
         constexpr int step = decltype(sc)::value;
         constexpr int jp = step / G, rg = step % G;
+        if (jp >= own) return;                          // wave-uniform: a pair past the row's end
         if constexpr (rg == 0 && jp + 1 < NBP) {       // next pair's x, in flight behind this pair's loads
-            mb_load_x<CG>(xs, k, c, valid_of(jp + 1), blk_of(jp + 1), g, hh, xb[(jp + 1) & 1]);
+            if (jp + 1 < own) mb_load_x<CG>(xs, k, c, valid_of(jp + 1), blk_of(jp + 1), g, hh, xb[(jp + 1) & 1]);
         }
         const MbX<CG>& xv = xb[jp & 1];
         Slot& t = ring[step & 1];
@@ -151,7 +156,7 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mb_kernel(const uint8_t* __res
             // everything this step reads from the slot is in registers now:
             // refill it with the step two ahead before the products
             __builtin_amdgcn_sched_barrier(0);
-            load(step + 2, t);
+            if ((step + 2) / G < own) load(step + 2, t);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
@@ -182,15 +187,16 @@ __global__ void __launch_bounds__(1024) gemv_q4_k_mb_kernel(const uint8_t* __res
         for (int rg = 0; rg < G; ++rg)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float v = mb_slot_sum(acc[cg][rg][i]);
-                if (lane < 4) red[((4 * rg + i) * 4 * CG + 4 * cg + lane) * nw + wave] = v;
+                const float v = mb_row_sum(acc[cg][rg][i]);
+                if ((lane & 15) < 4)
+                    red[(((4 * rg + i) * 4 * CG + 4 * cg + (lane & 3)) * nw + wave) * 4 + (lane >> 4)] = v;
             }
     __syncthreads();
     for (int idx = tid; idx < nrows * m; idx += blockDim.x) {
         const int row = idx / m, r = idx - row * m;
-        const float* rp = red + (row * 4 * CG + r) * nw;
+        const float* rp = red + (row * 4 * CG + r) * nw * 4;
         float s = 0.0f;
-        for (int w2 = 0; w2 < nw; ++w2) s += rp[w2];
+        for (int w2 = 0; w2 < 4 * nw; ++w2) s += rp[w2];
         y[r * ldy + row0 + row] = s;
     }
 }
@@ -246,7 +252,7 @@ hipError_t launch_gemv_mb(const uint8_t* w, const float* x, float* y, int64_t n,
     const int nb = (int)(k / kQKElems);
     if ((int64_t)p.waves * p.nbp * 2 < nb || p.groups * 4 < p.rows) return hipErrorInvalidValue;
     const dim3 gd((unsigned)p.grid), bd((unsigned)(64 * p.waves));
-    const size_t lds = sizeof(float) * 16 * 4 * p.cg * p.waves;
+    const size_t lds = sizeof(float) * 16 * 4 * p.cg * p.waves * 4;
     if (p.cg == 2) {
         if (p.nbp != 1) return hipErrorInvalidValue;
         return mb_go<1, 2>(p.groups, gd, bd, lds, stream, w, x, y, n, nb, m, p.rows, ldy);
