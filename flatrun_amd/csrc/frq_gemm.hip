@@ -75,7 +75,7 @@ struct WFmt<kTypeQ4K> {
         r.h = *reinterpret_cast<const u32x4*>(bp);
         r.q = *reinterpret_cast<const u32x2*>(bp + 16 + 32 * ((kb >> 6) & 3) + 8 * wq);
     }
-    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq) {
+    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq, float u_inv) {
         const int g = (kb >> 6) & 3;
         // scale/min pairs 2g, 2g+1 (get_scale_min_k4, gguf.py:135-163) without a
         // branch, so the K-step stays one block the scheduler can interleave:
@@ -89,15 +89,22 @@ struct WFmt<kTypeQ4K> {
         const uint32_t scm = ((P & 0x3F3F3F3Fu) & lowsel) |
                              ((lo4 | ((P >> 2) & 0x30303030u)) & ~lowsel);
         const float d = f16_bits_to_f32(r.h[0]), dmin = f16_bits_to_f32(r.h[0] >> 16);
-        const float s0 = d * byte_f(scm, 0), t0 = dmin * byte_f(scm, 2);
-        const float s1 = d * byte_f(scm, 1), t1 = dmin * byte_f(scm, 3);
+        // codes enter as q * u (fp8 pair conversion of the nibble bytes, u a
+        // power of two) and the scale as d * sc / u, so fma(s, q u, -t) is
+        // fl(d*sc*q - dmin*m): d*sc*q is exact, one rounding, the dequant's bits
+        const float du = d * u_inv;
+        const float s0 = du * byte_f(scm, 0), t0 = dmin * byte_f(scm, 2);
+        const float s1 = du * byte_f(scm, 1), t1 = dmin * byte_f(scm, 3);
         const uint32_t qw[2] = {r.q[0], r.q[1]};
         uint32_t lo[4], hi[4];
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const uint32_t v = qw[p >> 1] >> (16 * (p & 1));   // bytes 2p, 2p+1 of the quarter
-            lo[p] = pack_bf16(s0 * (float)(v & 15u) - t0, s0 * (float)((v >> 8) & 15u) - t0);
-            hi[p] = pack_bf16(s1 * (float)((v >> 4) & 15u) - t1, s1 * (float)((v >> 12) & 15u) - t1);
+        for (int h = 0; h < 2; ++h) {                          // bytes 4h .. 4h+3 of the quarter
+            float f[8];
+            nibbles8_fp8(qw[h], f);                            // f[0..3] low nibbles, f[4..7] high
+            lo[2 * h] = pack_bf16(__builtin_fmaf(s0, f[0], -t0), __builtin_fmaf(s0, f[1], -t0));
+            lo[2 * h + 1] = pack_bf16(__builtin_fmaf(s0, f[2], -t0), __builtin_fmaf(s0, f[3], -t0));
+            hi[2 * h] = pack_bf16(__builtin_fmaf(s1, f[4], -t1), __builtin_fmaf(s1, f[5], -t1));
+            hi[2 * h + 1] = pack_bf16(__builtin_fmaf(s1, f[6], -t1), __builtin_fmaf(s1, f[7], -t1));
         }
         *reinterpret_cast<u32x4*>(dst + 8 * wq) = u32x4{lo[0], lo[1], lo[2], lo[3]};
         *reinterpret_cast<u32x4*>(dst + 32 + 8 * wq) = u32x4{hi[0], hi[1], hi[2], hi[3]};
@@ -119,7 +126,7 @@ struct WFmt<kTypeQ80> {
 #pragma unroll
         for (int i = 0; i < 4; ++i) r.q[i] = ld_u32_a2(bp + 2 + 16 * (wq & 1) + 4 * i);
     }
-    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq) {
+    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq, float) {
         (void)kb;
         const float d = f16_bits_to_f32(r.d);
         uint32_t o[8];
@@ -167,7 +174,7 @@ struct WFmt<kTypeQ6K> {
         r.sc = bp[192 + 8 * h + (wq & 1) + 2 * ks];
         r.d = ld_u16(bp + 208);
     }
-    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq) {
+    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq, float) {
         const int kt4 = (kb & 255) >> 6, ks = 2 * (kt4 & 1) + (wq >> 1);
         const float s = f16_bits_to_f32(r.d) * (float)(int)(int8_t)(r.sc & 0xFFu);
         const float m = -32.0f * s;                         // exact: a power-of-two multiple
@@ -220,6 +227,7 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
     // W staging: thread owns quarter wq (8 bytes) of the group's 32 qs bytes of W row wr.
     const int wr = tid >> 2, wq = tid & 3;
     const uint8_t* wrow = w + (int64_t)(n0 + wr < N ? n0 + wr : N - 1) * row_bytes;
+    const float u_inv = 1.0f / fp8_unit();
 
     struct Stage {
         u32x4 x[4];
@@ -240,7 +248,7 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
             constexpr int j = decltype(jc)::value;
             *reinterpret_cast<u32x4*>(&xs[buf][(xr + 64 * j) * kLds + 8 * xc]) = sg.x[j];
         });
-        F::store(sg.w, &ws[buf][wr * kLds], (kbase + kt) * kBK, wq);
+        F::store(sg.w, &ws[buf][wr * kLds], (kbase + kt) * kBK, wq, u_inv);
     };
 
     f32x16 acc[2][2];
