@@ -227,6 +227,21 @@ __device__ __forceinline__ float wave_sum_lane63(float v) {
     return v;
 }
 
+// Issue priority by row progress, for the row-ring GEMV bodies. A SIMD's
+// instruction arbiter serves its oldest ready wavefront first, vector memory
+// instructions included, so without priorities the wavefronts dispatched
+// last in a workgroup receive their first rows only when the older ones have
+// finished theirs, and the workgroup ends with a few wavefronts running
+// alone, each limited by its own issue chain (clock stamps per row at
+// 3584 x 18944: the last two of ten wavefronts finished 11k cycles after the
+// first four). A wavefront at row j of R runs at priority 3 - 4j/R, so the
+// ones behind issue and load first and the workgroup's wavefronts advance
+// together. s_setprio changes only this wavefront's arbitration priority.
+template <bool ON, int R, int J>
+__device__ __forceinline__ void row_priority() {
+    if constexpr (ON) __builtin_amdgcn_s_setprio(3 - (4 * J) / R);
+}
+
 // The four in-row DPP steps of wave_sum_lane63: every lane ends with the sum
 // of its 16-lane DPP row. Callers park the four row sums (lanes 15, 31, 47,
 // 63) in LDS and add them with the other waves' in a fixed order, which

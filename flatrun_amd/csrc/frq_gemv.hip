@@ -91,8 +91,9 @@ __device__ __forceinline__ void finish_rows(int64_t row0, int64_t row_end, float
 // written once at the end.
 //
 // Body of one workgroup; `wg` plays the role of blockIdx.x (the grouped
-// kernel below passes the index inside its segment).
-template <int CPL, int U, int R>
+// kernel below passes the index inside its segment). PRIO: row_priority per
+// row (wavefronts that are behind issue first).
+template <int CPL, int U, int R, bool PRIO = false>
 __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                float* __restrict__ y, int64_t n, int nb, int64_t wg,
                                                float* keep = nullptr) {
@@ -119,6 +120,7 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
     // of two): a nibble below 16 in a byte converts exactly, two per
     // instruction; the scales carry 1 / u so that s' * (q u) = s q exactly.
     const float u_inv = 1.0f / fp8_unit();
+    row_priority<PRIO, R, 0>();                             // x and the first rows load at the top priority
 
     const int64_t row0 = rb * R;
     const int nrows = (int)(n - row0 < R ? n - row0 : R);
@@ -165,6 +167,7 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
     static_for<0, R>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         Q4KRow<CPL>& t = ring[j % U];
+        row_priority<PRIO, R, j>();
         // everything read from the slot is read before the slot is refilled
         const float d = f16_bits_to_f32(t.hd.x), dm = f16_bits_to_f32(t.hd.x >> 16);
         // (s, t) of plane A and plane B: w = fma(s, f, -t) per weight (f = q,
@@ -223,10 +226,14 @@ __device__ __forceinline__ void gemv_q4_k_body(const uint8_t* __restrict__ w, co
     }
 }
 
+// Row priorities pay from 14 rows per workgroup (3584 x 18944: 12.6 -> 11.9
+// us; 28672 x 4096: 16.4 -> 15.8; 4096 x 14336: 10.65 -> 10.2) and cost at
+// fewer rows with many workgroups per CU (18944 x 3584 at 8 rows: 12.0 ->
+// 12.3; 1024 x 4096 at 4 rows: 3.52 -> 3.58), same process.
 template <int CPL, int U, int R>
 __global__ void __launch_bounds__(CPL == 1 ? 1024 : 512) __attribute__((amdgpu_waves_per_eu((CPL == 1 && U <= 3) ? 5 : 1)))
 gemv_q4_k_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, int64_t n, int nb) {
-    gemv_q4_k_body<CPL, U, R>(w, x, y, n, nb, blockIdx.x);
+    gemv_q4_k_body<CPL, U, R, (R >= 14)>(w, x, y, n, nb, blockIdx.x);
 }
 
 // ------------------------------------------------------------------ Q5_K
@@ -419,7 +426,7 @@ __global__ void __launch_bounds__(512) gemv_q6_k_kernel(const uint8_t* __restric
 // Q6RingLane's (frq_ringrow.h). Rows stream through a ring of U register
 // slots, the row loop is unrolled over R rows without guards (as in the Q4_K
 // ring kernel), and partials are reduced with DPP into LDS.
-template <int U, int R>
+template <int U, int R, bool PRIO = false>
 __device__ __forceinline__ void gemv_q6_k_ring_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                     float* __restrict__ y, int64_t n, int nb, int64_t wg) {
     static_assert(U <= R, "ring deeper than the row count");
@@ -440,6 +447,7 @@ __device__ __forceinline__ void gemv_q6_k_ring_body(const uint8_t* __restrict__ 
     };
 
     float xv[1][4][8];
+    row_priority<PRIO, R, 0>();
     ln.load_x(x, blk, xv[0]);
     __builtin_amdgcn_sched_barrier(0);
     Q6RingRow ring[U];
@@ -450,6 +458,7 @@ __device__ __forceinline__ void gemv_q6_k_ring_body(const uint8_t* __restrict__ 
     static_for<0, R>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         Q6RingRow& t = ring[j % U];
+        row_priority<PRIO, R, j>();
         float pu[1];
         ln.dot<1>(t, xv, pu);
         if constexpr (j + U < R) load1(t, j + U);
@@ -465,11 +474,14 @@ __device__ __forceinline__ void gemv_q6_k_ring_body(const uint8_t* __restrict__ 
     }
 }
 
-template <int U, int R>
+// PRIO: row priorities, for workgroups of four or more wavefronts (4096 x
+// 14336: 13.36 -> 12.83 us); with two-wavefront workgroups, many per CU, they
+// cost (lm_head 152064 x 3584: 86.1 -> 93.4 us).
+template <int U, int R, bool PRIO>
 __global__ void __launch_bounds__(1024) gemv_q6_k_ring_kernel(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, int64_t n, int nb) {
-    gemv_q6_k_ring_body<U, R>(w, x, y, n, nb, blockIdx.x);
+    gemv_q6_k_ring_body<U, R, PRIO>(w, x, y, n, nb, blockIdx.x);
 }
 
 // ------------------------------------------------------------------ grouped
@@ -479,7 +491,8 @@ __global__ void __launch_bounds__(1024) gemv_q6_k_ring_kernel(const uint8_t* __r
 // workgroup shape (8 lanes per block, all of k) serves both row bodies; the
 // segment's format picks the body with a wave-uniform branch. Workgroups of
 // a segment do exactly what the single-matrix kernel's workgroups do, so the
-// outputs are bit-identical to separate launches.
+// outputs are bit-identical to separate launches (row priorities change the
+// order of issue, not the arithmetic).
 template <int R>
 __global__ void __launch_bounds__(1024) gemv_group_kernel(GemvGroup g, const float* __restrict__ x, int nb) {
     const int64_t b = blockIdx.x;
@@ -489,9 +502,9 @@ __global__ void __launch_bounds__(1024) gemv_group_kernel(GemvGroup g, const flo
         if (t < g.count && b >= g.wg_begin[t]) i = t;
     const int64_t wg = b - g.wg_begin[i];
     if (g.qtype[i] == kTypeQ4K)
-        gemv_q4_k_body<1, (R < 3 ? R : 3), R>(g.w[i], x, g.y[i], g.n[i], nb, wg);
+        gemv_q4_k_body<1, (R < 3 ? R : 3), R, true>(g.w[i], x, g.y[i], g.n[i], nb, wg);
     else
-        gemv_q6_k_ring_body<(R < 4 ? R : 4), R>(g.w[i], x, g.y[i], g.n[i], nb, wg);
+        gemv_q6_k_ring_body<(R < 4 ? R : 4), R, true>(g.w[i], x, g.y[i], g.n[i], nb, wg);
 }
 
 // Gate and up of a SwiGLU block in one launch, with the activation: workgroup
@@ -506,9 +519,9 @@ __global__ void __launch_bounds__(1024) gemv_swiglu_kernel(const uint8_t* __rest
                                                           float* __restrict__ act, int64_t inter, int nb) {
     __shared__ float kg[R], ku[R];
     const int64_t b = blockIdx.x;
-    gemv_q4_k_body<1, (R < 3 ? R : 3), R>(wgate, x, gateup, inter, nb, b, kg);
+    gemv_q4_k_body<1, (R < 3 ? R : 3), R, (R >= 14)>(wgate, x, gateup, inter, nb, b, kg);
     __syncthreads();                                        // the body's reduction array is reused
-    gemv_q4_k_body<1, (R < 3 ? R : 3), R>(wup, x, gateup + inter, inter, nb, b, ku);
+    gemv_q4_k_body<1, (R < 3 ? R : 3), R, (R >= 14)>(wup, x, gateup + inter, inter, nb, b, ku);
     const int64_t row0 = b * R;
     const int nrows = (int)(inter - row0 < R ? inter - row0 : R);
     for (int r = threadIdx.x; r < nrows; r += blockDim.x)   // the same thread wrote kg[r] and ku[r]
@@ -983,22 +996,22 @@ int pick_rows_q6k(int64_t n, int waves) {
     return best;
 }
 
-template <int U, int R>
+template <int U, int R, bool P>
 void q6k_go(dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n, int nb) {
-    gemv_q6_k_ring_kernel<(U < R ? U : R), R><<<gd, bd, 0, s>>>(w, x, y, n, nb);
+    gemv_q6_k_ring_kernel<(U < R ? U : R), R, P><<<gd, bd, 0, s>>>(w, x, y, n, nb);
 }
 
-template <int U>
+template <int U, bool P>
 bool q6k_rows(int rows, dim3 gd, dim3 bd, hipStream_t s, const uint8_t* w, const float* x, float* y, int64_t n,
               int nb) {
     switch (rows) {
-        case 1: q6k_go<U, 1>(gd, bd, s, w, x, y, n, nb); return true;
-        case 2: q6k_go<U, 2>(gd, bd, s, w, x, y, n, nb); return true;
-        case 4: q6k_go<U, 4>(gd, bd, s, w, x, y, n, nb); return true;
-        case 7: q6k_go<U, 7>(gd, bd, s, w, x, y, n, nb); return true;
-        case 8: q6k_go<U, 8>(gd, bd, s, w, x, y, n, nb); return true;
-        case 14: q6k_go<U, 14>(gd, bd, s, w, x, y, n, nb); return true;
-        case 16: q6k_go<U, 16>(gd, bd, s, w, x, y, n, nb); return true;
+        case 1: q6k_go<U, 1, P>(gd, bd, s, w, x, y, n, nb); return true;
+        case 2: q6k_go<U, 2, P>(gd, bd, s, w, x, y, n, nb); return true;
+        case 4: q6k_go<U, 4, P>(gd, bd, s, w, x, y, n, nb); return true;
+        case 7: q6k_go<U, 7, P>(gd, bd, s, w, x, y, n, nb); return true;
+        case 8: q6k_go<U, 8, P>(gd, bd, s, w, x, y, n, nb); return true;
+        case 14: q6k_go<U, 14, P>(gd, bd, s, w, x, y, n, nb); return true;
+        case 16: q6k_go<U, 16, P>(gd, bd, s, w, x, y, n, nb); return true;
         default: return false;
     }
 }
@@ -1072,7 +1085,9 @@ hipError_t launch_q6k_ring(int ring, int rows, int waves, int64_t grid, const ui
                            int64_t n, int nb, hipStream_t s) {
     const dim3 gd((unsigned)grid), bd((unsigned)(64 * waves));
     (void)ring;
-    if (!q6k_rows<4>(rows, gd, bd, s, w, x, y, n, nb)) return hipErrorInvalidConfiguration;
+    const bool ok = waves >= 4 ? q6k_rows<4, true>(rows, gd, bd, s, w, x, y, n, nb)
+                               : q6k_rows<4, false>(rows, gd, bd, s, w, x, y, n, nb);
+    if (!ok) return hipErrorInvalidConfiguration;
     return hipGetLastError();
 }
 
