@@ -4,7 +4,8 @@ Contract: laid out as the forwarder's np.concatenate of the projections
 (model/qwen2.py:1510-1519, 1690-1702). Fused into one launch for Q4_K / Q6_K
 matrices, whose outputs are bit for bit those of separate launches of the
 element-wise kernels (frq_dev_gemv_tuned with FRQ_GEMV_ROWS: same per-row
-arithmetic); one frq_dev_gemv launch per matrix otherwise, with its bits.
+arithmetic; two Q4_K matrices of one shape share one row ring per workgroup,
+same bits); one frq_dev_gemv launch per matrix otherwise, with its bits.
 Values are checked against the fp64 oracle as well (1e-5 normwise and
 componentwise, fp32 accumulation).
 """
@@ -84,6 +85,12 @@ def test_llama_groups_fused_and_exact(frq, spec):
     ([("Q6_K", 300), ("Q4_K", 0), ("Q6_K", 7)], 2048),      # empty middle segment
     ([("Q4_K", 700), ("Q4_K", 300)], 18944),                # 10-wave workgroups
     ([("Q4_K", 3000), ("Q6_K", 2000)], 3584),
+    # two Q4_K matrices of one shape: one ring over the same rows of both
+    ([("Q4_K", 5), ("Q4_K", 5)], 256),                      # 2 rows of each, ragged last workgroup
+    ([("Q4_K", 1001), ("Q4_K", 1001)], 4096),
+    ([("Q4_K", 777), ("Q4_K", 777)], 18944),                # 10-wave workgroups
+    ([("Q4_K", 9000), ("Q4_K", 9000)], 512),                # 4 rows of each
+    ([("Q4_K", 0), ("Q4_K", 300), ("Q4_K", 300)], 1024),    # an empty segment, then a pair
 ])
 def test_group_shapes_bit_identical(frq, spec, k):
     y, ysep, *_, fusable = run_group(spec, k, seed=len(spec) + k)
