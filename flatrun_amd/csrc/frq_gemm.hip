@@ -16,15 +16,20 @@
 // Tiling: a workgroup (8 waves, two per SIMD) owns a 256 (M) x 128 (N) tile of
 // Y and walks K in steps of 64 (one Q4_K group: 32 qs bytes per row). Wave
 // (wm, wn) owns the 64 x 64 sub-tile at (64 wm, 64 wn): 2 x 2 MFMA tiles of
-// 32 x 32, 64 fp32 accumulators per lane; while one wave of a SIMD dequantizes
-// or waits on LDS the other issues MFMAs. Each K-step:
-//   * X tile [256][64] bf16 and the W tile [128][64] (dequantized by the
-//     workgroup, 16 weights of one row per thread) go to LDS, double
-//     buffered; global loads run two steps ahead (two register staging
-//     sets), and each step's dequant + LDS writes for step t+1 follow its
-//     MFMAs, so the arithmetic runs while the matrix cores work.
-//   * LDS rows are padded to 72 bf16 (144 B) so a fragment read by 32 lanes
-//     of consecutive rows spreads over the banks.
+// 32 x 32, 64 fp32 accumulators per lane. Per K-step the X tile [256][64]
+// bf16 and the W tile [128][64] (dequantized, 16 weights of one row per
+// thread) pass through LDS, double buffered; LDS rows are padded to 72 bf16
+// (144 B) so a fragment read by 32 lanes of consecutive rows spreads over
+// the banks.
+// Schedule (ping-pong): the two waves of a SIMD (w and w + 4) sit in
+// different groups, group g = the waves with wn = g, and the groups take turns
+// between workgroup barriers. In one phase a wave issues its K-step's 16
+// MFMAs from registers (with the global loads for a later tile and the
+// dequant arithmetic between them); in the next it reads its next K-step's
+// fragments from LDS and writes its group's half of a later tile (X rows
+// 128 g .. 128 g + 127, W rows 64 g .. 64 g + 63). So one wave's MFMAs run
+// while its SIMD partner waits on LDS, instead of both waves of a SIMD
+// reaching the LDS round trip together.
 // MFMA operand layouts (32x32x16, 8 bf16 per lane): A lane l holds row l%32,
 // k = 8*(l/32) .. +7; B lane l holds column l%32, same k; D register r of lane
 // l is row 8*(r/4) + 4*(l/32) + r%4, column l%32.
@@ -45,7 +50,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBM = 256, kBN = 128, kBK = 64;
-constexpr int kGemmValuPerMfma = 5;   // dequant VALU ops placed after each MFMA of a K-step
 constexpr int kLds = kBK + 8;   // bf16 per LDS row
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
@@ -55,8 +59,9 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 
 // W staging per format. A K-step is 64 consecutive k of 128 rows; thread
 // (row wr, quarter wq) stages 16 weights of row wr. load() issues the global
-// reads for step `kb` (first k of the step), store() dequantizes them (same
-// rounding sequence as the format's dequant kernel) into bf16 LDS row `dst`.
+// reads for step `kb` (first k of the step), convert() dequantizes them (same
+// rounding sequence as the format's dequant kernel) into 16 bf16 in two
+// registers of four words, and put() writes those into bf16 LDS row `dst`.
 template <int QT>
 struct WFmt;
 
@@ -70,17 +75,23 @@ struct WFmt<kTypeQ4K> {
         u32x4 h;
         u32x2 q;
     };
-    __device__ static void load(Raw& r, const uint8_t* wrow, int kb, int wq) {
-        const uint8_t* bp = wrow + (int64_t)(kb >> 8) * kQ4KBytes;
-        r.h = *reinterpret_cast<const u32x4*>(bp);
-        r.q = *reinterpret_cast<const u32x2*>(bp + 16 + 32 * ((kb >> 6) & 3) + 8 * wq);
+    // rs covers the workgroup's W rows; voff = the row's byte offset, the
+    // K-step's block and group offsets go in as scalars
+    __device__ static void load(Raw& r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, int kb, int wq) {
+        const int sblk = (kb >> 8) * kQ4KBytes;
+        r.h = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff, sblk, 0));
+        r.q = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(voff + 16 + 8 * wq),
+                                                                            sblk + 32 * ((kb >> 6) & 3), 0));
     }
-    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq, float u_inv) {
+    // scale/min pairs 2g, 2g+1 (get_scale_min_k4, gguf.py:135-163) as
+    // (s0, t0, s1, t1), without a branch: bytes o, o+1 of scales[0..3] and
+    // [4..7] (g < 2), or the nibbles of scales[8 + o], [9 + o] with their high
+    // bits (g >= 2), o = 2 (g % 2). Codes enter as q * u (fp8 pair conversion
+    // of the nibble bytes, u a power of two) and the scale as d * sc / u, so
+    // fma(s, q u, -t) is fl(d*sc*q - dmin*m): d*sc*q is exact, one rounding,
+    // the dequant's bits.
+    __device__ static f32x4 scales(const Raw& r, int kb, float u_inv) {
         const int g = (kb >> 6) & 3;
-        // scale/min pairs 2g, 2g+1 (get_scale_min_k4, gguf.py:135-163) without a
-        // branch, so the K-step stays one block the scheduler can interleave:
-        // bytes o, o+1 of scales[0..3] and [4..7] (g < 2), or the nibbles of
-        // scales[8 + o], [9 + o] with their high bits (g >= 2), o = 2 (g % 2)
         const uint32_t o = 2u * (uint32_t)(g & 1);
         const uint32_t P = __builtin_amdgcn_perm(r.h[2], r.h[1], o | ((o + 1) << 8) | ((o + 4) << 16) | ((o + 5) << 24));
         const uint32_t Q = __builtin_amdgcn_perm(r.h[3], r.h[3], o | ((o + 1) << 8) | (o << 16) | ((o + 1) << 24));
@@ -89,12 +100,12 @@ struct WFmt<kTypeQ4K> {
         const uint32_t scm = ((P & 0x3F3F3F3Fu) & lowsel) |
                              ((lo4 | ((P >> 2) & 0x30303030u)) & ~lowsel);
         const float d = f16_bits_to_f32(r.h[0]), dmin = f16_bits_to_f32(r.h[0] >> 16);
-        // codes enter as q * u (fp8 pair conversion of the nibble bytes, u a
-        // power of two) and the scale as d * sc / u, so fma(s, q u, -t) is
-        // fl(d*sc*q - dmin*m): d*sc*q is exact, one rounding, the dequant's bits
         const float du = d * u_inv;
-        const float s0 = du * byte_f(scm, 0), t0 = dmin * byte_f(scm, 2);
-        const float s1 = du * byte_f(scm, 1), t1 = dmin * byte_f(scm, 3);
+        return f32x4{du * byte_f(scm, 0), dmin * byte_f(scm, 2), du * byte_f(scm, 1), dmin * byte_f(scm, 3)};
+    }
+    // the 16 weights as bf16: a = k 8wq .. +7 (low nibbles), b = k 32 + 8wq .. +7
+    __device__ static void weights(const Raw& r, const f32x4& sc, u32x4& a, u32x4& b) {
+        const float s0 = sc[0], t0 = sc[1], s1 = sc[2], t1 = sc[3];
         const uint32_t qw[2] = {r.q[0], r.q[1]};
         uint32_t lo[4], hi[4];
 #pragma unroll
@@ -106,8 +117,15 @@ struct WFmt<kTypeQ4K> {
             hi[2 * h] = pack_bf16(__builtin_fmaf(s1, f[4], -t1), __builtin_fmaf(s1, f[5], -t1));
             hi[2 * h + 1] = pack_bf16(__builtin_fmaf(s1, f[6], -t1), __builtin_fmaf(s1, f[7], -t1));
         }
-        *reinterpret_cast<u32x4*>(dst + 8 * wq) = u32x4{lo[0], lo[1], lo[2], lo[3]};
-        *reinterpret_cast<u32x4*>(dst + 32 + 8 * wq) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+        a = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        b = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    }
+    __device__ static void convert(const Raw& r, int kb, int, float u_inv, u32x4& a, u32x4& b) {
+        weights(r, scales(r, kb, u_inv), a, b);
+    }
+    __device__ static void put(uint16_t* dst, int wq, const u32x4& a, const u32x4& b) {
+        *reinterpret_cast<u32x4*>(dst + 8 * wq) = a;
+        *reinterpret_cast<u32x4*>(dst + 32 + 8 * wq) = b;
     }
 };
 
@@ -126,8 +144,7 @@ struct WFmt<kTypeQ80> {
 #pragma unroll
         for (int i = 0; i < 4; ++i) r.q[i] = ld_u32_a2(bp + 2 + 16 * (wq & 1) + 4 * i);
     }
-    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq, float) {
-        (void)kb;
+    __device__ static void convert(const Raw& r, int, int, float, u32x4& a, u32x4& b) {
         const float d = f16_bits_to_f32(r.d);
         uint32_t o[8];
 #pragma unroll
@@ -135,8 +152,12 @@ struct WFmt<kTypeQ80> {
             const uint32_t v = r.q[p >> 1] >> (16 * (p & 1));
             o[p] = pack_bf16((float)(int)(int8_t)(v & 0xFFu) * d, (float)(int)(int8_t)((v >> 8) & 0xFFu) * d);
         }
-        *reinterpret_cast<u32x4*>(dst + 16 * wq) = u32x4{o[0], o[1], o[2], o[3]};
-        *reinterpret_cast<u32x4*>(dst + 16 * wq + 8) = u32x4{o[4], o[5], o[6], o[7]};
+        a = u32x4{o[0], o[1], o[2], o[3]};
+        b = u32x4{o[4], o[5], o[6], o[7]};
+    }
+    __device__ static void put(uint16_t* dst, int wq, const u32x4& a, const u32x4& b) {
+        *reinterpret_cast<u32x4*>(dst + 16 * wq) = a;
+        *reinterpret_cast<u32x4*>(dst + 16 * wq + 8) = b;
     }
 };
 
@@ -174,7 +195,7 @@ struct WFmt<kTypeQ6K> {
         r.sc = bp[192 + 8 * h + (wq & 1) + 2 * ks];
         r.d = ld_u16(bp + 208);
     }
-    __device__ static void store(const Raw& r, uint16_t* dst, int kb, int wq, float) {
+    __device__ static void convert(const Raw& r, int kb, int wq, float, u32x4& a, u32x4& b) {
         const int kt4 = (kb & 255) >> 6, ks = 2 * (kt4 & 1) + (wq >> 1);
         const float s = f16_bits_to_f32(r.d) * (float)(int)(int8_t)(r.sc & 0xFFu);
         const float m = -32.0f * s;                         // exact: a power-of-two multiple
@@ -192,8 +213,12 @@ struct WFmt<kTypeQ6K> {
             o[2 * c] = pack_bf16(__builtin_fmaf(byte_f(q, 0), s, m), __builtin_fmaf(byte_f(q, 1), s, m));
             o[2 * c + 1] = pack_bf16(__builtin_fmaf(byte_f(q, 2), s, m), __builtin_fmaf(byte_f(q, 3), s, m));
         }
-        *reinterpret_cast<u32x4*>(dst + 16 * wq) = u32x4{o[0], o[1], o[2], o[3]};
-        *reinterpret_cast<u32x4*>(dst + 16 * wq + 8) = u32x4{o[4], o[5], o[6], o[7]};
+        a = u32x4{o[0], o[1], o[2], o[3]};
+        b = u32x4{o[4], o[5], o[6], o[7]};
+    }
+    __device__ static void put(uint16_t* dst, int wq, const u32x4& a, const u32x4& b) {
+        *reinterpret_cast<u32x4*>(dst + 16 * wq) = a;
+        *reinterpret_cast<u32x4*>(dst + 16 * wq + 8) = b;
     }
 };
 
@@ -201,10 +226,17 @@ struct WFmt<kTypeQ6K> {
 // and writes its fp32 partial tile to plane s of `part`; a second, small
 // kernel adds the planes in split order (deterministic, and the kernel
 // boundary makes every partial visible whichever XCD wrote it).
-// AHEAD: K-steps between a tile's global loads and its MFMAs (2, or 3 when
-// the K-step count per split is a multiple of four: 77.7 -> 76.6 us at
-// 512 x 14336 x 4096, bit-identical).
-template <int QT, int AHEAD>
+// L: K-steps between a tile's global loads and the phase that dequantizes it
+// (1, or 2 when the K-step count per split is a multiple of four).
+//
+// Phases (group 0's numbering; group 1 runs the same sequence one phase
+// later): phase 2t issues the MFMAs of step t, phase 2t + 1 reads the
+// fragments of tile t + 1 and writes the group's half of tile t + 2. Tile u
+// lives in LDS buffer u % 2: group 0 writes its half in global phase 2u - 3,
+// group 1 in 2u - 2; group 0 reads it in 2u - 1, group 1 in 2u; the buffer is
+// rewritten from phase 2u + 1 on. Every access is separated from a
+// conflicting one by at least one barrier.
+template <int QT, int L>
 __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restrict__ w,
                                                              const uint16_t* __restrict__ x,
                                                              float* __restrict__ y, int M, int N, int K, int S,
@@ -213,6 +245,7 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
     __shared__ __attribute__((aligned(16))) uint16_t ws[2][kBN * kLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 3, wn = wave >> 2;
+    const int grp = __builtin_amdgcn_readfirstlane(wn);
     // 1-D grid, M-tile fastest: workgroups are dealt to the 8 XCDs round-robin,
     // so with 2 (or 4, 8) M-tiles each XCD only ever needs its own M-tile of X
     // (2 MB at M-tile 256, K 4096), which then stays in that XCD's L2.
@@ -222,38 +255,55 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
     const int n0 = nt * kBN, m0 = mt * kBM;
     using F = WFmt<QT>;
     const int64_t row_bytes = (int64_t)(K / F::kElems) * F::kBytes;
-    const int ksteps = K / kBK / S;                    // even (chosen by the host)
+    const int ksteps = K / kBK / S;                    // a multiple of NS (chosen by the host)
     const int kbase = split * ksteps;
 
-    // X staging: 8 threads per row (16 B each), rows xr + 64 j.
-    const int xc = tid & 7, xr = tid >> 3;
-    // W staging: thread owns quarter wq (8 bytes) of the group's 32 qs bytes of W row wr.
-    const int wr = tid >> 2, wq = tid & 3;
-    const uint8_t* wrow = w + (int64_t)(n0 + wr < N ? n0 + wr : N - 1) * row_bytes;
+    // The group's half of a tile: X rows 128 grp + xr + 32 j (8 threads of 16 B
+    // per row), W row 64 grp + wr, quarter wq.
+    const int gt = tid & 255;
+    const int xc = gt & 7, xr = 128 * grp + (gt >> 3);
+    const int wr = 64 * grp + (gt >> 2), wq = gt & 3;
     const float u_inv = 1.0f / fp8_unit();
+    // X (and Q4_K W) through buffer resources over the tile's rows: per-thread
+    // offsets are constants and the K-step's offset a scalar, so a load needs
+    // no address arithmetic. Rows past M or N read as zeros (their outputs
+    // are not stored); the host keeps the offsets below 2^31.
+    const int mrows = M - m0 < kBM ? M - m0 : kBM;
+    const auto xrs = buffer_rsrc(x + (int64_t)m0 * K, (uint32_t)((int64_t)mrows * K * 2));
+    uint32_t xoff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xoff[j] = (uint32_t)(((int64_t)(xr + 32 * j) * K + 8 * xc) * 2);
+    const int nrows = N - n0 < kBN ? N - n0 : kBN;
+    const auto wrs = buffer_rsrc(w + (int64_t)n0 * row_bytes, (uint32_t)((int64_t)nrows * row_bytes));
+    const uint32_t wvoff = (uint32_t)((int64_t)wr * row_bytes);
+    const uint8_t* wrow = w + (int64_t)(n0 + wr < N ? n0 + wr : N - 1) * row_bytes;
 
     struct Stage {
         u32x4 x[4];
         typename F::Raw w;
     };
-    constexpr int NS = AHEAD == 3 ? 4 : 2;              // staging sets, a power of two
-    static_assert(AHEAD == 2 || AHEAD == 3, "loads two or three K-steps ahead");
+    constexpr int NS = L == 2 ? 4 : 2;                 // staging sets, a power of two
+    static_assert(L == 1 || L == 2, "loads one or two K-steps ahead");
     Stage st[NS];
-    auto load_tile = [&](Stage& sg, int kt) __attribute__((always_inline)) {
-        const int kb = (kbase + kt) * kBK;
+    const int last = ksteps - 1;
+    // Tiles past the last one repeat it (into an LDS buffer nothing reads
+    // again), so loads and LDS writes stay unconditional and the compiler's
+    // wait before an LDS write covers one staging set only.
+    auto kb_of = [&](int u) __attribute__((always_inline)) { return (kbase + (u < last ? u : last)) * kBK; };
+    auto load_half = [&](Stage& sg, int u) __attribute__((always_inline)) {
+        const int kb = kb_of(u);
         static_for<0, 4>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
-            const int r = m0 + xr + 64 * j;
-            sg.x[j] = *reinterpret_cast<const u32x4*>(x + (int64_t)(r < M ? r : M - 1) * K + kb + 8 * xc);
+            sg.x[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)xoff[j], kb * 2, 0));
         });
-        F::load(sg.w, wrow, kb, wq);
+        if constexpr (QT == kTypeQ4K) F::load(sg.w, wrs, wvoff, kb, wq);
+        else F::load(sg.w, wrow, kb, wq);
     };
-    auto store_tile = [&](const Stage& sg, int buf, int kt) __attribute__((always_inline)) {
+    auto put_x = [&](const Stage& sg, int buf) __attribute__((always_inline)) {
         static_for<0, 4>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
-            *reinterpret_cast<u32x4*>(&xs[buf][(xr + 64 * j) * kLds + 8 * xc]) = sg.x[j];
+            *reinterpret_cast<u32x4*>(&xs[buf][(xr + 32 * j) * kLds + 8 * xc]) = sg.x[j];
         });
-        F::store(sg.w, &ws[buf][wr * kLds], (kbase + kt) * kBK, wq, u_inv);
     };
 
     f32x16 acc[2][2];
@@ -264,70 +314,87 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.0f;
 
-    auto compute = [&](int buf) __attribute__((always_inline)) {
+    bf16x8 fa[kBK / 16][2], fb[kBK / 16][2];           // one K-step's fragments
+    u32x4 wa, wb;                                      // the next W half, as bf16
+    // Q4_K with loads two steps ahead: the memory phase decodes the scales of
+    // the tile the next MFMA phase dequantizes, after its own LDS traffic, so
+    // the MFMA phase only applies them (70.5 -> 70.0 us at 512 x 14336 x 4096).
+    constexpr bool kPipe = QT == kTypeQ4K && L == 2;
+    f32x4 sc_next = {0.f, 0.f, 0.f, 0.f};
+
+    // MFMA phase of step t: the global loads for tile uld = t + 2 + L, the
+    // dequant of tile udq = t + 2's W half into wa, wb, and the step's MFMAs.
+    auto mfma_phase = [&](Stage& sld, int uld, const Stage& sdq, int udq) __attribute__((always_inline)) {
+        load_half(sld, uld);
+        if constexpr (kPipe) F::weights(sdq.w, sc_next, wa, wb);
+        else F::convert(sdq.w, kb_of(udq), wq, u_inv, wa, wb);
 #pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            const int kof = 16 * kk + 8 * (lane >> 5);
-            bf16x8 a[2], b[2];
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
-                a[mi] = *reinterpret_cast<const bf16x8*>(&xs[buf][(64 * wm + 32 * mi + (lane & 31)) * kLds + kof]);
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
-                b[ni] = *reinterpret_cast<const bf16x8*>(&ws[buf][(64 * wn + 32 * ni + (lane & 31)) * kLds + kof]);
+        for (int kk = 0; kk < kBK / 16; ++kk)
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk][mi], fb[kk][ni], acc[mi][ni], 0, 0, 0);
+    };
+    // Memory phase: the fragments of buffer rbuf, then the group's half of
+    // the tile in staging set sst (X) and wa, wb (W) into buffer wbuf; then
+    // (Q4_K, L = 2) the scales of tile unx from set snx.
+    auto mem_phase = [&](int rbuf, const Stage& sst, int wbuf, const Stage& snx, int unx) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kk = 0; kk < kBK / 16; ++kk) {
+            const int kof = 16 * kk + 8 * (lane >> 5);
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+                fa[kk][mi] = *reinterpret_cast<const bf16x8*>(&xs[rbuf][(64 * wm + 32 * mi + (lane & 31)) * kLds + kof]);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+                fb[kk][ni] = *reinterpret_cast<const bf16x8*>(&ws[rbuf][(64 * wn + 32 * ni + (lane & 31)) * kLds + kof]);
+        }
+        put_x(sst, wbuf);
+        F::put(&ws[wbuf][wr * kLds], wq, wa, wb);
+        if constexpr (kPipe) {
+            __builtin_amdgcn_sched_barrier(0);
+            sc_next = F::scales(snx.w, kb_of(unx), u_inv);
+        } else {
+            (void)snx;
+            (void)unx;
         }
     };
+    // A phase ends at a workgroup barrier; sched_barrier(0) keeps the
+    // scheduler from moving MFMAs or memory operations across it.
+    auto phase_end = []() __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    };
 
-    // Global loads run AHEAD K-steps ahead of the MFMAs: the loads for step
-    // t + AHEAD are issued at step t (staging set (t + AHEAD) % NS) and reach
-    // LDS at the end of step t + AHEAD - 1. The loop is unrolled by NS so the
-    // staging set of every step is a compile-time choice (the step count is a
-    // multiple of NS), and loads and LDS writes are unconditional -- past the
-    // last step they repeat it into the buffer nothing reads again -- so the
-    // compiler's wait before each LDS write covers one staging set only.
-    const int last = ksteps - 1;
-    static_for<0, AHEAD>([&](auto ic) {
+    // Prologue: tiles 0 .. L loaded, tile 0 whole in LDS (both groups), the W
+    // half of tile 1 converted, the loads for tile 1 + L issued.
+    static_for<0, L + 1>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
-        load_tile(st[i], i < last ? i : last);
+        load_half(st[i], i);
     });
-    store_tile(st[0], 0, 0);
+    put_x(st[0], 0);
+    F::convert(st[0].w, kb_of(0), wq, u_inv, wa, wb);
+    F::put(&ws[0][wr * kLds], wq, wa, wb);
+    F::convert(st[1].w, kb_of(1), wq, u_inv, wa, wb);
+    load_half(st[(1 + L) % NS], 1 + L);
     __syncthreads();
-    for (int kt0 = 0; kt0 < ksteps; kt0 += NS) {
+    // group 1 lags one phase: one barrier before the sequence, group 0 one after
+    if (grp == 1) phase_end();
+    mem_phase(0, st[1], 1, st[2 % NS], 2);
+    phase_end();
+    for (int t0 = 0; t0 < ksteps; t0 += NS) {
         static_for<0, NS>([&](auto jc) {
-            constexpr int j = decltype(jc)::value;      // kt % NS: staging set; kt % 2: LDS buffer
-            const int kt = kt0 + j;
-            load_tile(st[(j + AHEAD) % NS], kt + AHEAD < last ? kt + AHEAD : last);
-            compute(j & 1);
-            store_tile(st[(j + 1) % NS], (j + 1) & 1, kt + 1 < last ? kt + 1 : last);
-            // Order for the scheduler: the loads for t + AHEAD first, then this
-            // step's 16 MFMAs with the next step's dequant arithmetic between
-            // them (the wave's other SIMD partner is in the same phase, so
-            // only this interleave keeps the matrix core and the VALU both
-            // busy), the fragment reads of each 16-k slice ahead of its
-            // MFMAs, and the LDS writes of step t + 1 last.
-            __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);   // global loads
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // fragments of k-slice 0
-            static_for<0, kBK / 16>([&](auto kc) {
-                constexpr int kk = decltype(kc)::value;
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, kGemmValuPerMfma, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, kGemmValuPerMfma, 0);
-                if constexpr (kk + 1 < kBK / 16) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, kGemmValuPerMfma, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, kGemmValuPerMfma, 0);
-            });
-            __builtin_amdgcn_sched_group_barrier(0x200, 6, 0);   // LDS writes for t + 1
-            __syncthreads();
+            constexpr int j = decltype(jc)::value;      // t % NS: staging sets; t % 2: LDS buffers
+            const int t = t0 + j;
+            mfma_phase(st[(j + 2 + L) % NS], t + 2 + L, st[(j + 2) % NS], t + 2);
+            phase_end();
+            mem_phase((j + 1) & 1, st[(j + 2) % NS], j & 1, st[(j + 3) % NS], t + 3);
+            phase_end();
         });
     }
+    if (grp == 0) phase_end();
 
     // S > 1: this split's partial tile goes to plane `split` of the scratch;
     // gemm_split_reduce_kernel adds the planes after the kernel.
@@ -372,10 +439,11 @@ __global__ void __launch_bounds__(256) gemm_split_reduce_strided_kernel(const fl
 }  // namespace
 
 bool gemm_bf16_supported(int qtype, int64_t m, int64_t n, int64_t k) {
-    // K-steps of 64 must come in pairs (the pipeline is unrolled by two)
+    // K-steps of 64 come in pairs (the loop is unrolled by two or four); k <=
+    // 2^22 keeps the X and W buffer offsets of a tile below 2^31
     const int64_t kq = qtype == kTypeQ80 ? 128 : (qtype == kTypeQ4K || qtype == kTypeQ6K) ? kQKElems : 0;
     return kq > 0 && m > 0 && n > 0 && k > 0 && k % kq == 0 && m <= 0x7FFFFFFF && n <= 0x7FFFFFFF &&
-           k <= 0x7FFFFFFF && ((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM) <= 0x7FFFFFFF;
+           k <= (int64_t)1 << 22 && ((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM) <= 0x7FFFFFFF;
 }
 
 // K-splits for a GEMM shape: the largest S in {1, 2, 4, 8} that keeps the grid
@@ -423,19 +491,20 @@ hipError_t launch_gemm_bf16(int qtype, const uint8_t* w, const uint16_t* x, floa
     const int64_t tiles = ((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM);
     if (tiles * sp > 0x7FFFFFFF) return hipErrorInvalidValue;
     const dim3 grid((unsigned)(tiles * sp)), block(512);
-    const bool ahead3 = (k / kBK / sp) % 4 == 0;
+    // loads two K-steps ahead where the step count per split is a multiple of four
+    const bool ahead2 = (k / kBK / sp) % 4 == 0;
     switch (qtype) {
         case kTypeQ4K:
-            if (ahead3) gemm_bf16_kernel<kTypeQ4K, 3><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
-            else gemm_bf16_kernel<kTypeQ4K, 2><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
+            if (ahead2) gemm_bf16_kernel<kTypeQ4K, 2><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
+            else gemm_bf16_kernel<kTypeQ4K, 1><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
             break;
         case kTypeQ6K:
-            if (ahead3) gemm_bf16_kernel<kTypeQ6K, 3><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
-            else gemm_bf16_kernel<kTypeQ6K, 2><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
+            if (ahead2) gemm_bf16_kernel<kTypeQ6K, 2><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
+            else gemm_bf16_kernel<kTypeQ6K, 1><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
             break;
         case kTypeQ80:
-            if (ahead3) gemm_bf16_kernel<kTypeQ80, 3><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
-            else gemm_bf16_kernel<kTypeQ80, 2><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
+            if (ahead2) gemm_bf16_kernel<kTypeQ80, 2><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
+            else gemm_bf16_kernel<kTypeQ80, 1><<<grid, block, 0, stream>>>(w, x, y, (int)m, (int)n, (int)k, sp, part);
             break;
         default: return hipErrorInvalidValue;
     }
