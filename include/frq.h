@@ -278,14 +278,15 @@ int frq_dev_gemv_tuned(int qtype, const void* w, size_t w_bytes, const float* x,
  * to bf16 (nearest even); products and sums are fp32. Replaces, for
  * activations already in bf16, the per-token loop of matmul_q4_k_batched
  * (_C.cpp:154-197), which re-dequantizes W for every row of x. Device
- * pointers (w, x 16-byte aligned); k a multiple of 256. */
+ * pointers (w, x 16-byte aligned); k a multiple of 256, at most 4194304. */
 int frq_dev_gemm_q4_k_bf16(const void* w, size_t w_bytes, const uint16_t* x_bf16, float* y, int64_t m, int64_t n,
                            int64_t k, void* stream);
 /* Same with host buffers (copied to the device and back on every call). */
 int frq_gemm_q4_k_bf16(const uint16_t* x_bf16, const uint8_t* w, size_t w_bytes, int64_t m, int64_t n, int64_t k,
                        float* y);
 /* The same GEMM for any of Q4_K, Q6_K, Q8_0 (qtype); k a multiple of 256
- * (Q4_K, Q6_K) or 128 (Q8_0); w 16-byte aligned (Q4_K) or 2-byte aligned.
+ * (Q4_K, Q6_K) or 128 (Q8_0) and at most 4194304 (FRQ_ERR_UNSUPPORTED
+ * beyond); w 16-byte aligned (Q4_K) or 2-byte aligned.
  * Replaces, for bf16 activations, matmul_q6_k_batched (_C.cpp:244-283) and
  * matmul_q8_0_batched (_C.cpp:199-242) as well. Shapes with too few output
  * tiles to fill the GPU (e.g. n = 1024 or 4096 at m = 512) split K over

@@ -138,3 +138,16 @@ def test_facade_value_errors(method, x):
     b.available = True                                  # force past the availability gate
     with pytest.raises(ValueError):
         getattr(b, method)(x, _W16, 2, 512)
+
+
+def test_gemm_k_limit():
+    """The prefill GEMM takes k up to 2^22 (its buffer offsets stay below
+    2^31): one Q4_K block past it is refused as unsupported before any pointer
+    or device is touched; at the limit the checks pass and the null buffers
+    are what is refused."""
+    lib = _lib.lib()
+    n = 1
+    for k, code in (((1 << 22) + 256, _lib.ERR_UNSUPPORTED), (1 << 22, _lib.ERR_INVALID)):
+        w_bytes = n * (k // 256) * 144
+        rc = lib.frq_dev_gemm_bf16(_lib.QTYPES["Q4_K"], None, w_bytes, None, None, 4, n, k, None)
+        assert rc == code, (k, rc)
