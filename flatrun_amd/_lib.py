@@ -138,6 +138,7 @@ SIGNATURES: dict[str, list] = {
     "frq_dev_gemm_q4_k_bf16": [_vp, _sz, _vp, _vp, _i64, _i64, _i64, _vp],
     "frq_gemm_q4_k_bf16": [_vp, _vp, _sz, _i64, _i64, _i64, _vp],
     "frq_dev_gemm_bf16": [_i32, _vp, _sz, _vp, _vp, _i64, _i64, _i64, _vp],
+    "frq_dev_gemm_bf16_group": [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp],
     "frq_gemm_bf16": [_i32, _vp, _vp, _sz, _i64, _i64, _i64, _vp],
     "frq_stream_begin_capture": [_vp],
     "frq_stream_end_capture": [_vp, _c.POINTER(_vp)],

@@ -798,6 +798,60 @@ int frq_dev_gemm_bf16(int qtype, const void* w, size_t w_bytes, const uint16_t* 
     return FRQ_OK;
 }
 
+int frq_dev_gemm_bf16_group(int count, const int* qtypes, const void* const* w, const size_t* w_bytes,
+                            const int64_t* n, const uint16_t* x, int64_t m, int64_t k, float* const* y,
+                            int64_t y_stride, void* stream) {
+    if (count < 1 || count > frq::kGemmGroupMax)
+        return fail(FRQ_ERR_INVALID, "gemm group: count %d outside [1, %d]", count, frq::kGemmGroupMax);
+    if (!qtypes || !w || !w_bytes || !n || !y) return fail(FRQ_ERR_INVALID, "gemm group: null argument array");
+    if (y_stride < 0 || y_stride > 0x7FFFFFFF) return fail(FRQ_ERR_SHAPE, "gemm group: y_stride outside [0, 2^31)");
+    Fmt f;
+    int64_t total = 0;
+    for (int i = 0; i < count; ++i) {
+        if (int rc = gemm_checks(qtypes[i], w_bytes[i], m, n[i], k, &f)) return rc;
+        if (y_stride && y_stride < n[i]) return fail(FRQ_ERR_SHAPE, "gemm group: y_stride below a matrix's rows");
+        total += n[i];
+    }
+    if (m == 0 || total == 0) return FRQ_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < count; ++i)
+        if (n[i] && !y[i]) return fail(FRQ_ERR_INVALID, "null buffer");
+    if (k == 0) {
+        for (int i = 0; i < count; ++i)
+            for (int64_t r = 0; n[i] && r < m; ++r)
+                FRQ_HIP(frq::launch_fill(y[i] + r * (y_stride ? y_stride : n[i]), 0.0f, n[i], s));
+        return FRQ_OK;
+    }
+    if (!x || (reinterpret_cast<uintptr_t>(x) & 15)) return fail(FRQ_ERR_ALIGN, "gemm group: x null or misaligned");
+    // segments with rows: one launch for all of them (or a single matrix's own GEMM)
+    int qt[frq::kGemmGroupMax], c = 0;
+    const uint8_t* wp[frq::kGemmGroupMax];
+    int64_t nn[frq::kGemmGroupMax], ld[frq::kGemmGroupMax];
+    size_t wb[frq::kGemmGroupMax];
+    float* yy[frq::kGemmGroupMax];
+    for (int i = 0; i < count; ++i) {
+        if (!n[i]) continue;
+        const uintptr_t wa = reinterpret_cast<uintptr_t>(w[i]);
+        if (!w[i] || (qtypes[i] == FRQ_Q4_K ? (wa & 15) : (wa & 1)))
+            return fail(FRQ_ERR_ALIGN, "gemm group: weight %d null or misaligned", i);
+        if (reinterpret_cast<uintptr_t>(y[i]) & 3) return fail(FRQ_ERR_ALIGN, "y must be 4-byte aligned");
+        qt[c] = qtypes[i];
+        wp[c] = static_cast<const uint8_t*>(w[i]);
+        wb[c] = w_bytes[i];
+        nn[c] = n[i];
+        ld[c] = y_stride ? y_stride : n[i];
+        yy[c] = y[i];
+        ++c;
+    }
+    if (c == 1 && ld[0] == nn[0]) return frq_dev_gemm_bf16(qt[0], wp[0], wb[0], x, yy[0], m, nn[0], k, stream);
+    float* part = nullptr;
+    uint32_t* cnt = nullptr;
+    std::lock_guard<std::mutex> lk(g_sk_mu);
+    if (int rc = sk_scratch_locked(s, frq::gemm_bf16_group_scratch(c, nn, m, k), 0, &part, &cnt)) return rc;
+    FRQ_HIP(frq::launch_gemm_bf16_group(c, qt, wp, nn, yy, ld, x, m, k, s, part));
+    return FRQ_OK;
+}
+
 int frq_gemm_bf16(int qtype, const uint16_t* x, const uint8_t* w, size_t w_bytes, int64_t m, int64_t n, int64_t k,
                   float* y) {
     Fmt f;

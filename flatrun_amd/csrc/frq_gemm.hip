@@ -261,22 +261,23 @@ struct WFmt<kTypeQ6K> {
 // group 1 in 2u - 2; group 0 reads it in 2u - 1, group 1 in 2u; the buffer is
 // rewritten from phase 2u + 1 on. Every access is separated from a
 // conflicting one by at least one barrier.
+typedef uint16_t XTile[kBM * kLds];
+typedef uint16_t WTile[kBN * kLds];
+// The workgroup's LDS tiles, named directly in the tile body (a pointer
+// passed in would be a generic address: 64-bit arithmetic and spills).
+__shared__ __attribute__((aligned(16))) XTile xs[2];
+__shared__ __attribute__((aligned(16))) WTile ws[2];
+
+// One workgroup's output tile (M-tile mt, N-tile nt, K-split `split` of S):
+// y[m * ldy + n] for its rows and columns, or with S > 1 plane `split` of
+// `part` (M x N, dense).
 template <int QT, int L>
-__global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restrict__ w,
-                                                             const uint16_t* __restrict__ x,
-                                                             float* __restrict__ y, int M, int N, int K, int S,
-                                                             float* __restrict__ part) {
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2][kBM * kLds];
-    __shared__ __attribute__((aligned(16))) uint16_t ws[2][kBN * kLds];
+__device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ w, const uint16_t* __restrict__ x,
+                                          float* __restrict__ y, int ldy, float* __restrict__ part, int M, int N,
+                                          int K, int S, int mt, int nt, int split) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 3, wn = wave >> 2;
     const int grp = __builtin_amdgcn_readfirstlane(wn);
-    // 1-D grid, M-tile fastest: workgroups are dealt to the 8 XCDs round-robin,
-    // so with 2 (or 4, 8) M-tiles each XCD only ever needs its own M-tile of X
-    // (2 MB at M-tile 256, K 4096), which then stays in that XCD's L2.
-    const int mtiles = (M + kBM - 1) / kBM;
-    const int mt = (int)(blockIdx.x % mtiles), rest = (int)(blockIdx.x / mtiles);
-    const int split = rest % S, nt = rest / S;
     const int n0 = nt * kBN, m0 = mt * kBM;
     using F = WFmt<QT>;
     const int64_t row_bytes = (int64_t)(K / F::kElems) * F::kBytes;
@@ -433,9 +434,8 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
     }
     if (grp == 0) phase_end();
 
-    // S > 1: this split's partial tile goes to plane `split` of the scratch;
-    // gemm_split_reduce_kernel adds the planes after the kernel.
     float* out = S == 1 ? y : part + (int64_t)split * M * N;
+    const int ldo = S == 1 ? ldy : N;
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -444,9 +444,50 @@ __global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restric
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + 64 * wm + 32 * mi + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < M && n < N) out[(int64_t)m * N + n] = acc[mi][ni][r];
+                if (m < M && n < N) out[(int64_t)m * ldo + n] = acc[mi][ni][r];
             }
         }
+}
+
+// 1-D grid, M-tile fastest: workgroups are dealt to the 8 XCDs round-robin,
+// so with 2 (or 4, 8) M-tiles each XCD only ever needs its own M-tile of X
+// (2 MB at M-tile 256, K 4096), which then stays in that XCD's L2. S > 1:
+// a split's partial tile goes to plane `split` of `part`, and
+// gemm_split_reduce_kernel adds the planes after the kernel.
+template <int QT, int L>
+__global__ void __launch_bounds__(512) gemm_bf16_kernel(const uint8_t* __restrict__ w,
+                                                             const uint16_t* __restrict__ x,
+                                                             float* __restrict__ y, int M, int N, int K, int S,
+                                                             float* __restrict__ part) {
+    const int mtiles = (M + kBM - 1) / kBM;
+    const int mt = (int)(blockIdx.x % mtiles), rest = (int)(blockIdx.x / mtiles);
+    const int split = rest % S, nt = rest / S;
+    gemm_tile<QT, L>(w, x, y, N, part, M, N, K, S, mt, nt, split);
+}
+
+// Up to four matrices that multiply the same x in one launch (a fused q|k|v
+// projection): segment i owns workgroups [wg_begin_i, wg_begin_{i+1}), laid
+// out as the single-matrix kernel's grid, and its format picks the tile
+// body with a wave-uniform branch (the bodies share the LDS).
+template <int L>
+__global__ void __launch_bounds__(512) gemm_bf16_group_kernel(GemmGroup g, const uint16_t* __restrict__ x, int M,
+                                                                   int K, int S) {
+    const int64_t b = blockIdx.x;
+    int i = 0;
+#pragma unroll
+    for (int t = 1; t < kGemmGroupMax; ++t)
+        if (t < g.count && b >= g.wg_begin[t]) i = t;
+    const int N = (int)g.n[i];
+    const int mtiles = (M + kBM - 1) / kBM;
+    const int local = (int)(b - g.wg_begin[i]);
+    const int mt = local % mtiles, rest = local / mtiles;
+    const int split = rest % S, nt = rest / S;
+    const int ldy = (int)g.ldy[i];
+    switch (g.qtype[i]) {
+        case kTypeQ4K: gemm_tile<kTypeQ4K, L>(g.w[i], x, g.y[i], ldy, g.part[i], M, N, K, S, mt, nt, split); break;
+        case kTypeQ6K: gemm_tile<kTypeQ6K, L>(g.w[i], x, g.y[i], ldy, g.part[i], M, N, K, S, mt, nt, split); break;
+        default: gemm_tile<kTypeQ80, L>(g.w[i], x, g.y[i], ldy, g.part[i], M, N, K, S, mt, nt, split); break;
+    }
 }
 
 // y[i] = part[0][i] + part[1][i] + ... + part[S-1][i], in that order (the
@@ -473,6 +514,20 @@ __global__ void __launch_bounds__(256) gemm_split_reduce_strided_kernel(const fl
     y[(i / cols) * ldy + i % cols] = sum_planes<float>([&](int q) { return part[q * count + i]; }, S);
 }
 
+// The split sums of a group: element e of segment i (e - e_begin_i = r n_i + c)
+// goes to y_i[r ldy_i + c], the planes added in split order.
+__global__ void __launch_bounds__(256) gemm_split_reduce_group_kernel(GemmGroup g, int64_t M, int S, int64_t total) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= total) return;
+    int i = 0;
+#pragma unroll
+    for (int t = 1; t < kGemmGroupMax; ++t)
+        if (t < g.count && e >= g.e_begin[t]) i = t;
+    const int64_t local = e - g.e_begin[i], n = g.n[i], count = M * n;
+    const float* p = g.part[i] + local;
+    g.y[i][(local / n) * g.ldy[i] + local % n] = sum_planes<float>([&](int q) { return p[q * count]; }, S);
+}
+
 }  // namespace
 
 bool gemm_bf16_supported(int qtype, int64_t m, int64_t n, int64_t k) {
@@ -488,9 +543,8 @@ bool gemm_bf16_supported(int qtype, int64_t m, int64_t n, int64_t k) {
 // split at an even count of at least 4 K-steps. Shapes that fill the GPU are
 // not split: that would only trade tail balance for partial-sum traffic.
 // 512 x 14336 x 4096: 1; 512 x 4096 x 14336: 4; 512 x 1024 x 4096: 8.
-int gemm_bf16_splits(int64_t m, int64_t n, int64_t k) {
+static int splits_for_tiles(int64_t tiles, int64_t k) {
     const int64_t kCUs = 256;
-    const int64_t tiles = ((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM);
     const int64_t ksteps = k / kBK;
     int best = 1;
     for (int sp = 2; sp <= 8; sp *= 2) {
@@ -498,6 +552,26 @@ int gemm_bf16_splits(int64_t m, int64_t n, int64_t k) {
         best = sp;
     }
     return best;
+}
+
+int gemm_bf16_splits(int64_t m, int64_t n, int64_t k) {
+    return splits_for_tiles(((n + kBN - 1) / kBN) * ((m + kBM - 1) / kBM), k);
+}
+
+// A group splits K for its total tile count (q|k|v of Llama-3-8B at m = 512:
+// 96 tiles, 2 splits, where q alone takes 4 and k or v alone 8).
+int gemm_bf16_group_splits(int count, const int64_t* n, int64_t m, int64_t k) {
+    int64_t tiles = 0;
+    for (int i = 0; i < count; ++i) tiles += ((n[i] + kBN - 1) / kBN) * ((m + kBM - 1) / kBM);
+    return splits_for_tiles(tiles, k);
+}
+
+size_t gemm_bf16_group_scratch(int count, const int64_t* n, int64_t m, int64_t k) {
+    const int sp = gemm_bf16_group_splits(count, n, m, k);
+    if (sp == 1) return 0;
+    size_t cols = 0;
+    for (int i = 0; i < count; ++i) cols += (size_t)n[i];
+    return (size_t)sp * (size_t)m * cols * sizeof(float);
 }
 
 size_t gemm_bf16_scratch(int64_t m, int64_t n, int64_t k) {
@@ -549,6 +623,42 @@ hipError_t launch_gemm_bf16(int qtype, const uint8_t* w, const uint16_t* x, floa
         const int64_t count = m * n, threads = (count + 3) / 4;
         gemm_split_reduce_kernel<<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream>>>(part, y, sp, count);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_bf16_group(int count, const int* qtypes, const uint8_t* const* w, const int64_t* n,
+                                  float* const* y, const int64_t* ldy, const uint16_t* x, int64_t m, int64_t k,
+                                  hipStream_t stream, float* part) {
+    if (count < 1 || count > kGemmGroupMax) return hipErrorInvalidValue;
+    for (int i = 0; i < count; ++i)
+        if (!gemm_bf16_supported(qtypes[i], m, n[i], k) || ldy[i] < n[i] || ldy[i] > 0x7FFFFFFF)
+            return hipErrorInvalidValue;
+    int sp = gemm_bf16_group_splits(count, n, m, k);
+    if (sp > 1 && !part) sp = 1;                           // no scratch: one split
+    GemmGroup g{};
+    g.count = count;
+    const int64_t mtiles = (m + kBM - 1) / kBM;
+    int64_t wg = 0, e = 0;
+    float* pp = part;
+    for (int i = 0; i < count; ++i) {
+        g.w[i] = w[i];
+        g.y[i] = y[i];
+        g.n[i] = n[i];
+        g.ldy[i] = ldy[i];
+        g.qtype[i] = qtypes[i];
+        g.wg_begin[i] = wg;
+        g.e_begin[i] = e;
+        g.part[i] = sp > 1 ? pp : nullptr;
+        wg += ((n[i] + kBN - 1) / kBN) * mtiles * sp;
+        e += m * n[i];
+        if (sp > 1) pp += (int64_t)sp * m * n[i];
+    }
+    if (wg > 0x7FFFFFFF) return hipErrorInvalidValue;
+    const bool ahead2 = (k / kBK / sp) % 4 == 0;
+    if (ahead2) gemm_bf16_group_kernel<2><<<dim3((unsigned)wg), dim3(512), 0, stream>>>(g, x, (int)m, (int)k, sp);
+    else gemm_bf16_group_kernel<1><<<dim3((unsigned)wg), dim3(512), 0, stream>>>(g, x, (int)m, (int)k, sp);
+    if (sp > 1)
+        gemm_split_reduce_group_kernel<<<dim3((unsigned)((e + 255) / 256)), dim3(256), 0, stream>>>(g, m, sp, e);
     return hipGetLastError();
 }
 

@@ -179,6 +179,29 @@ size_t gemm_bf16_scratch(int64_t m, int64_t n, int64_t k);
 hipError_t launch_gemm_bf16(int qtype, const uint8_t* w, const uint16_t* x, float* y, int64_t m, int64_t n, int64_t k,
                             hipStream_t stream, float* part = nullptr);
 
+// The same GEMM for up to kGemmGroupMax matrices W_i[n_i, k] that multiply
+// the same x, in one launch (and one split-adding launch when K is split):
+// y_i[r * ldy_i + c]. The K-split is chosen for the group's total tile count
+// (gemm_bf16_group_splits); with the same split a matrix's outputs are those
+// of its own launch bit for bit. Every segment passes gemm_bf16_supported.
+constexpr int kGemmGroupMax = 4;
+struct GemmGroup {
+    const uint8_t* w[kGemmGroupMax];
+    float* y[kGemmGroupMax];
+    float* part[kGemmGroupMax];        // segment i's partial planes (split > 1)
+    int64_t n[kGemmGroupMax];
+    int64_t ldy[kGemmGroupMax];
+    int64_t wg_begin[kGemmGroupMax];   // first workgroup of each segment
+    int64_t e_begin[kGemmGroupMax];    // first element of each segment in the split-adding kernel
+    int qtype[kGemmGroupMax];
+    int count;
+};
+int gemm_bf16_group_splits(int count, const int64_t* n, int64_t m, int64_t k);
+size_t gemm_bf16_group_scratch(int count, const int64_t* n, int64_t m, int64_t k);
+hipError_t launch_gemm_bf16_group(int count, const int* qtypes, const uint8_t* const* w, const int64_t* n,
+                                  float* const* y, const int64_t* ldy, const uint16_t* x, int64_t m, int64_t k,
+                                  hipStream_t stream, float* part);
+
 // y[r * ldy + c] = part[0][i] + ... + part[splits-1][i], i = r * cols + c, for
 // the rows x cols elements of the partial planes, in split order.
 hipError_t launch_split_reduce(const float* part, float* y, int splits, int64_t rows, int64_t cols, int64_t ldy,

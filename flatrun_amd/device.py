@@ -260,7 +260,7 @@ GROUP_MAX = 4
 
 def _group_arrays(parts):
     if not 1 <= len(parts) <= GROUP_MAX:
-        raise ValueError(f"a GEMV group holds 1..{GROUP_MAX} matrices, got {len(parts)}")
+        raise ValueError(f"a group holds 1..{GROUP_MAX} matrices, got {len(parts)}")
     qt = (ctypes.c_int * len(parts))(*[qtype_id(p[0]) for p in parts])
     wp = (ctypes.c_void_p * len(parts))(*[_addr(p[1]) for p in parts])
     return qt, wp
@@ -307,6 +307,21 @@ def gemm_bf16(qtype, w, x_bf16, y, m: int, n: int, k: int, stream=None, w_bytes:
     wb = _nbytes(w) if w_bytes is None else int(w_bytes)
     check(lib().frq_dev_gemm_bf16(qtype_id(qtype), _addr(w), wb, _addr(x_bf16), _addr(y), int(m), int(n), int(k),
                                   _stream(stream)))
+
+
+def gemm_bf16_group(parts, x_bf16, m: int, k: int, y_stride: int = 0, stream=None) -> None:
+    """Matrices sharing x in one GEMM launch (frq_dev_gemm_bf16_group).
+    ``parts``: up to 4 tuples ``(qtype, w, n, y[, w_bytes])``; ``y`` is the
+    device output (an int address is accepted, e.g. an offset into one
+    concatenated buffer); row r of matrix i goes to ``y_i + r * (y_stride or n_i)``
+    floats."""
+    qt, wp = _group_arrays(parts)
+    c = len(parts)
+    wb = (ctypes.c_size_t * c)(*[int(p[4]) if len(p) > 4 else _nbytes(p[1]) for p in parts])
+    nn = (ctypes.c_int64 * c)(*[int(p[2]) for p in parts])
+    yy = (ctypes.c_void_p * c)(*[_addr(p[3]) for p in parts])
+    check(lib().frq_dev_gemm_bf16_group(c, qt, wp, wb, nn, _addr(x_bf16), int(m), int(k), yy, int(y_stride),
+                                        _stream(stream)))
 
 
 def gemm_q4k_bf16(w, x_bf16, y, m: int, n: int, k: int, stream=None, w_bytes: int | None = None) -> None:

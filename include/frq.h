@@ -296,6 +296,24 @@ int frq_dev_gemm_bf16(int qtype, const void* w, size_t w_bytes, const uint16_t* 
                       int64_t n, int64_t k, void* stream);
 int frq_gemm_bf16(int qtype, const uint16_t* x_bf16, const uint8_t* w, size_t w_bytes, int64_t m, int64_t n,
                   int64_t k, float* y);
+/* Up to 4 matrices that multiply the same x (a fused q|k|v projection at
+ * prefill) in one GEMM launch, plus one launch adding the K-split partials
+ * where the group splits K. No reference counterpart: the reference's
+ * forwarder calls one batched matmul per projection (model/qwen2.py:1510-1519);
+ * this is those calls with x read by one launch.
+ *   count      1 .. 4; qtypes[i], w[i], w_bytes[i], n[i] as for
+ *              frq_dev_gemm_bf16, all sharing m, k and x (m rows of k bf16)
+ *   y[i]       output of matrix i: row r at y[i] + r * (y_stride ? y_stride : n[i])
+ *              floats, so y[i] = out + (n[0] + .. + n[i-1]) with y_stride the sum
+ *              of n gives the concatenation [X W_0^T | X W_1^T | ...]
+ * The K-split is chosen for the group's total tile count; with the split a
+ * matrix would get alone, its outputs are those of frq_dev_gemm_bf16 bit for
+ * bit, else they agree to the fp32 accumulation tolerance. A group with one
+ * matrix and a dense output is frq_dev_gemm_bf16. Status codes as
+ * frq_dev_gemm_bf16. */
+int frq_dev_gemm_bf16_group(int count, const int* qtypes, const void* const* w, const size_t* w_bytes,
+                            const int64_t* n, const uint16_t* x_bf16, int64_t m, int64_t k, float* const* y,
+                            int64_t y_stride, void* stream);
 
 /* dst = src on the device with a plain 16-byte-per-lane streaming kernel:
  * the reference point for calibrating HBM traffic counters (bytes a

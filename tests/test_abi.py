@@ -151,3 +151,23 @@ def test_gemm_k_limit():
         w_bytes = n * (k // 256) * 144
         rc = lib.frq_dev_gemm_bf16(_lib.QTYPES["Q4_K"], None, w_bytes, None, None, 4, n, k, None)
         assert rc == code, (k, rc)
+
+
+def test_gemm_group_validation():
+    """frq_dev_gemm_bf16_group refuses bad groups before touching a device:
+    a count outside 1..4, a weight size that does not match, a y_stride below
+    a matrix's rows; an empty group (m = 0) is a no-op."""
+    import ctypes
+
+    lib = _lib.lib()
+    q = (ctypes.c_int * 2)(_lib.QTYPES["Q4_K"], _lib.QTYPES["Q6_K"])
+    w = (ctypes.c_void_p * 2)(None, None)
+    n = (ctypes.c_int64 * 2)(256, 128)
+    wb = (ctypes.c_size_t * 2)(256 * 2 * 144, 128 * 2 * 210)
+    y = (ctypes.c_void_p * 2)(None, None)
+    assert lib.frq_dev_gemm_bf16_group(0, q, w, wb, n, None, 4, 512, y, 0, None) == _lib.ERR_INVALID
+    assert lib.frq_dev_gemm_bf16_group(5, q, w, wb, n, None, 4, 512, y, 0, None) == _lib.ERR_INVALID
+    bad = (ctypes.c_size_t * 2)(256 * 2 * 144, 128 * 2 * 210 - 1)
+    assert lib.frq_dev_gemm_bf16_group(2, q, w, bad, n, None, 4, 512, y, 0, None) == _lib.ERR_SIZE
+    assert lib.frq_dev_gemm_bf16_group(2, q, w, wb, n, None, 4, 512, y, 200, None) == _lib.ERR_SHAPE
+    assert lib.frq_dev_gemm_bf16_group(2, q, w, wb, n, None, 0, 512, y, 0, None) == _lib.OK
