@@ -699,9 +699,10 @@ def prefill_layer(stream, m: int = 512, reps: int = 20) -> dict:
     """One Llama-3-8B decoder layer's projections at prefill, Y = X . W^T for
     the Q4_K_M mix (q, k, o, gate, up Q4_K; v, down Q6_K), X [512 x in] bf16:
     seven bf16-MFMA GEMMs (shapes with few output tiles split K), captured as
-    one graph and replayed. `grouped_qkv`: the same seven products with q|k|v
-    as one frq_dev_gemm_bf16_group launch into a concatenated [512 x 6144]
-    output (the K-split chosen for the three together), five GEMM launches."""
+    one graph and replayed. `grouped`: the same seven products with q|k|v and
+    gate|up as frq_dev_gemm_bf16_group launches into concatenated outputs
+    ([512 x 6144], [512 x 28672]; K split for each group's tile count), four
+    GEMM launches."""
     from flatrun_amd import _C
 
     host = {name: synth.make_blocks(q, n, k, seed=40 + i) for i, (name, q, n, k) in enumerate(LLAMA_LAYER)}
@@ -710,20 +711,25 @@ def prefill_layer(stream, m: int = 512, reps: int = 20) -> dict:
     nmax = max(n for _, _, n, _ in LLAMA_LAYER)
     x = _C.to_bf16_bits(np.random.default_rng(41).standard_normal((m, kmax)).astype(np.float32))
     xd = device.DeviceBuffer.from_host(x)
-    yd = device.DeviceBuffer(4 * m * nmax)
-    qkv = [(q, dev[name], n, host[name].nbytes) for name, q, n, _ in LLAMA_LAYER[:3]]
-    nqkv = sum(n for _, _, n, _ in qkv)
+    yd = device.DeviceBuffer(4 * m * 2 * nmax)
+    groups = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]
+    shape = {name: (q, n, k) for name, q, n, k in LLAMA_LAYER}
 
     def layer():
         for name, q, n, k in LLAMA_LAYER:
             device.gemm_bf16(q, dev[name], xd, yd, m, n, k, stream=stream, w_bytes=host[name].nbytes)
 
     def layer_grouped():
-        offs = np.concatenate([[0], np.cumsum([n for _, _, n, _ in qkv])[:-1]])
-        device.gemm_bf16_group([(q, w, n, yd.ptr + 4 * int(o), nb) for (q, w, n, nb), o in zip(qkv, offs)],
-                               xd, m, LLAMA_LAYER[0][3], y_stride=nqkv, stream=stream)
-        for name, q, n, k in LLAMA_LAYER[3:]:
-            device.gemm_bf16(q, dev[name], xd, yd, m, n, k, stream=stream, w_bytes=host[name].nbytes)
+        for names in groups:
+            if len(names) == 1:
+                q, n, k = shape[names[0]]
+                device.gemm_bf16(q, dev[names[0]], xd, yd, m, n, k, stream=stream, w_bytes=host[names[0]].nbytes)
+                continue
+            ns = [shape[nm][1] for nm in names]
+            offs = np.concatenate([[0], np.cumsum(ns)[:-1]])
+            device.gemm_bf16_group([(shape[nm][0], dev[nm], shape[nm][1], yd.ptr + 4 * int(o), host[nm].nbytes)
+                                    for nm, o in zip(names, offs)], xd, m, shape[names[0]][2], y_stride=sum(ns),
+                                   stream=stream)
 
     def timed(fn):
         fn()                                  # split-K scratch exists before capture
@@ -750,7 +756,7 @@ def prefill_layer(stream, m: int = 512, reps: int = 20) -> dict:
     flop = sum(2 * m * n * k for _, _, n, k in LLAMA_LAYER)
     return {"us_per_layer": round(us, 1), "tflops": round(flop / us / 1e6, 1), "flop": flop, "gemms": len(LLAMA_LAYER),
             "frac_bf16_peak": round(flop / us / 1e6 / BF16_PEAK_TFLOPS, 4),
-            "grouped_qkv": {"us_per_layer": round(us_g, 1), "tflops": round(flop / us_g / 1e6, 1), "gemm_launches": 5,
+            "grouped": {"us_per_layer": round(us_g, 1), "tflops": round(flop / us_g / 1e6, 1), "gemm_launches": 4,
                             "frac_bf16_peak": round(flop / us_g / 1e6 / BF16_PEAK_TFLOPS, 4)},
             "note": "X 512 tokens (bf16); W resident raw blocks; the reference re-dequantizes W per token"}
 
