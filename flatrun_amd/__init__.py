@@ -396,6 +396,52 @@ class NativeBackend:
         """As matmul_q4k_bf16 for Q8_0 weights (fp32 path: ``matmul_q8_0``)."""
         return self._gemm_bf16("Q8_0", x, weight, n, k)
 
+    def matmul_fused_bf16(self, x, parts, k: int):
+        """matmul_fused for the prefill GEMM: ``parts`` = [(quant, weight, n),
+        ...] (1..4 entries; Q4_K, Q6_K or Q8_0; weight raw bytes or a
+        DeviceWeight), x (seq, k) or (k,) rounded to bf16 ->
+        ``np.concatenate([x W_0^T, x W_1^T, ...], axis=-1)`` in one GEMM launch
+        (frq_dev_gemm_bf16_group)."""
+        self._require()
+        from . import device
+        xb = _C.to_bf16_bits(x)
+        x2 = xb.reshape(1, -1) if xb.ndim == 1 else xb
+        if x2.ndim != 2 or x2.shape[1] != k:
+            raise ValueError(f"x must be ({k},) or (seq, {k}), got {np.shape(x)}")
+        if not 1 <= len(parts) <= device.GROUP_MAX:
+            raise ValueError(f"matmul_fused_bf16 takes 1..{device.GROUP_MAX} parts, got {len(parts)}")
+        seq, ns = x2.shape[0], [int(n) for _, _, n in parts]
+        total = sum(ns)
+        out = np.empty((seq, total), dtype=np.float32)
+        with self._lock:
+            temps, ws = [], []
+            xd = device.DeviceBuffer.from_host(x2)
+            yd = device.DeviceBuffer(max(1, seq * total * 4))
+            try:
+                for _, wgt, _ in parts:
+                    if isinstance(wgt, DeviceWeight):
+                        ws.append(wgt)
+                    else:
+                        raw = _raw_bytes(wgt).reshape(-1)
+                        dw = DeviceWeight(raw) if raw.size else None
+                        temps.append(dw)
+                        ws.append(dw)
+                if seq and total:
+                    grp, off = [], 0
+                    for (q, _, n), w in zip(parts, ws):
+                        grp.append((q, w if w is not None else 0, n, yd.ptr + 4 * off, w.nbytes if w is not None else 0))
+                        off += int(n)
+                    device.gemm_bf16_group(grp, xd, seq, k, y_stride=total)
+                    device.synchronize()
+                    out[:] = yd.to_host(np.float32, seq * total).reshape(seq, total)
+            finally:
+                for t in temps:
+                    if t is not None:
+                        t.buffer.free()
+                xd.free()
+                yd.free()
+        return out[0] if xb.ndim == 1 else out
+
     # ------------------------------------------------------------ dequant
     def dequant_q4k(self, weight, shape: tuple[int, int]):
         """Pure Q4_K dequant to f32 (out, in) (python/__init__.py:211-227)."""

@@ -138,3 +138,22 @@ def test_group_repeat_and_graph_replay(frq):
         for b in bufs + [xd, yd]:
             b.free()
         s.destroy()
+
+
+def test_facade_matmul_fused_bf16(frq):
+    """NativeBackend.matmul_fused_bf16: the concatenation of the per-matrix
+    prefill GEMMs, from raw bytes or resident weights, 2-D and 1-D x."""
+    from flatrun_amd import NativeBackend
+
+    nb = NativeBackend()
+    m, k = 24, 512
+    xb = make_case(m, 1, k, seed=80)[1]
+    parts = [("Q4_K", synth.make_blocks("Q4_K", 96, k, seed=81), 96),
+             ("Q6_K", synth.make_blocks("Q6_K", 40, k, seed=82), 40)]
+    y = nb.matmul_fused_bf16(xb, parts, k)
+    assert y.shape == (m, 136)
+    check(y[:, :96], parts[0][1], xb, 96, k)
+    check(y[:, 96:], parts[1][1], xb, 40, k, q="Q6_K")
+    dev = [(q, nb.upload(raw), n) for q, raw, n in parts]
+    assert bits_equal(nb.matmul_fused_bf16(xb, dev, k), y)
+    assert bits_equal(nb.matmul_fused_bf16(xb[3], parts, k), y[3])
