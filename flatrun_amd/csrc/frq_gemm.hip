@@ -528,6 +528,22 @@ __global__ void __launch_bounds__(256) gemm_split_reduce_group_kernel(GemmGroup 
     g.y[i][(local / n) * g.ldy[i] + local % n] = sum_planes<float>([&](int q) { return p[q * count]; }, S);
 }
 
+// The same with four consecutive elements per thread, where every n_i and
+// ldy_i is a multiple of 4 and every y_i 16-byte aligned (then no group of
+// four crosses a row, and every load and store is one 16-byte access).
+__global__ void __launch_bounds__(256) gemm_split_reduce_group4_kernel(GemmGroup g, int64_t M, int S, int64_t total) {
+    const int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (e >= total) return;
+    int i = 0;
+#pragma unroll
+    for (int t = 1; t < kGemmGroupMax; ++t)
+        if (t < g.count && e >= g.e_begin[t]) i = t;
+    const int64_t local = e - g.e_begin[i], n = g.n[i], count = M * n;
+    const float* p = g.part[i] + local;
+    const f32x4 v = sum_planes<f32x4>([&](int q) { return *reinterpret_cast<const f32x4*>(p + q * count); }, S);
+    *reinterpret_cast<f32x4*>(g.y[i] + (local / n) * g.ldy[i] + local % n) = v;
+}
+
 }  // namespace
 
 bool gemm_bf16_supported(int qtype, int64_t m, int64_t n, int64_t k) {
@@ -657,8 +673,15 @@ hipError_t launch_gemm_bf16_group(int count, const int* qtypes, const uint8_t* c
     const bool ahead2 = (k / kBK / sp) % 4 == 0;
     if (ahead2) gemm_bf16_group_kernel<2><<<dim3((unsigned)wg), dim3(512), 0, stream>>>(g, x, (int)m, (int)k, sp);
     else gemm_bf16_group_kernel<1><<<dim3((unsigned)wg), dim3(512), 0, stream>>>(g, x, (int)m, (int)k, sp);
-    if (sp > 1)
-        gemm_split_reduce_group_kernel<<<dim3((unsigned)((e + 255) / 256)), dim3(256), 0, stream>>>(g, m, sp, e);
+    if (sp > 1) {
+        bool vec4 = true;
+        for (int i = 0; i < count; ++i)
+            vec4 = vec4 && n[i] % 4 == 0 && ldy[i] % 4 == 0 && (reinterpret_cast<uintptr_t>(y[i]) & 15) == 0;
+        if (vec4)
+            gemm_split_reduce_group4_kernel<<<dim3((unsigned)((e / 4 + 255) / 256)), dim3(256), 0, stream>>>(g, m, sp, e);
+        else
+            gemm_split_reduce_group_kernel<<<dim3((unsigned)((e + 255) / 256)), dim3(256), 0, stream>>>(g, m, sp, e);
+    }
     return hipGetLastError();
 }
 
