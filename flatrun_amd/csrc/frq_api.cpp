@@ -816,10 +816,15 @@ int frq_dev_gemm_bf16_group(int count, const int* qtypes, const void* const* w, 
     hipStream_t s = static_cast<hipStream_t>(stream);
     for (int i = 0; i < count; ++i)
         if (n[i] && !y[i]) return fail(FRQ_ERR_INVALID, "null buffer");
-    if (k == 0) {
-        for (int i = 0; i < count; ++i)
-            for (int64_t r = 0; n[i] && r < m; ++r)
-                FRQ_HIP(frq::launch_fill(y[i] + r * (y_stride ? y_stride : n[i]), 0.0f, n[i], s));
+    if (k == 0) {   // empty dot products are 0 (kernel fills: graph-capturable)
+        for (int i = 0; i < count; ++i) {
+            if (!n[i]) continue;
+            if (!y_stride || y_stride == n[i]) {
+                FRQ_HIP(frq::launch_fill(y[i], 0.0f, m * n[i], s));
+            } else {
+                for (int64_t r = 0; r < m; ++r) FRQ_HIP(frq::launch_fill(y[i] + r * y_stride, 0.0f, n[i], s));
+            }
+        }
         return FRQ_OK;
     }
     if (!x || (reinterpret_cast<uintptr_t>(x) & 15)) return fail(FRQ_ERR_ALIGN, "gemm group: x null or misaligned");

@@ -157,3 +157,23 @@ def test_facade_matmul_fused_bf16(frq):
     dev = [(q, nb.upload(raw), n) for q, raw, n in parts]
     assert bits_equal(nb.matmul_fused_bf16(xb, dev, k), y)
     assert bits_equal(nb.matmul_fused_bf16(xb[3], parts, k), y[3])
+
+
+def test_group_k_zero_fills(frq):
+    """k = 0: every output is 0, dense or strided."""
+    m = 5
+    s = device.Stream()
+    yd = device.DeviceBuffer(4 * m * 12)
+    try:
+        _lib.check(_lib.lib().frq_memcpy_h2d(yd.ptr, np.full(m * 12, np.nan, np.float32).ctypes.data, m * 12 * 4))
+        device.gemm_bf16_group([("Q4_K", 0, 4, yd.ptr, 0), ("Q6_K", 0, 8, yd.ptr + 16, 0)], 0, m, 0, y_stride=12,
+                               stream=s)
+        s.synchronize()
+        assert np.array_equal(yd.to_host(np.float32, m * 12), np.zeros(m * 12, np.float32))
+        _lib.check(_lib.lib().frq_memcpy_h2d(yd.ptr, np.full(m * 12, np.nan, np.float32).ctypes.data, m * 12 * 4))
+        device.gemm_bf16_group([("Q4_K", 0, 12, yd.ptr, 0)], 0, m, 0, stream=s)
+        s.synchronize()
+        assert np.array_equal(yd.to_host(np.float32, m * 12), np.zeros(m * 12, np.float32))
+    finally:
+        yd.free()
+        s.destroy()
