@@ -34,10 +34,18 @@
 
 namespace frq {
 
+// Output stores are non-temporal (`nt`): a dequantized matrix is written
+// once and not read again by this kernel, and streaming it past the caches
+// moves it at a far higher rate than ordinary write-allocating stores
+// (Q4_K 18944 x 3584 to fp32: 69-71 -> 40-41 us; fp16 40.5 -> 25-28 us).
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ void store4(float* __restrict__ y, int64_t e0, int64_t n, float v0, float v1,
                                        float v2, float v3) {
     if (e0 + 3 < n && ((reinterpret_cast<uintptr_t>(y + e0) & 15) == 0)) {
-        *reinterpret_cast<float4*>(y + e0) = make_float4(v0, v1, v2, v3);
+        __builtin_nontemporal_store(f32x4v{v0, v1, v2, v3}, reinterpret_cast<f32x4v*>(y + e0));
     } else {
         if (e0 + 0 < n) y[e0 + 0] = v0;
         if (e0 + 1 < n) y[e0 + 1] = v1;
@@ -60,7 +68,7 @@ __device__ __forceinline__ void store4(uint16_t* __restrict__ y, int64_t e0, int
                                        float v2, float v3) {
     const uint32_t h0 = f16_bits(v0), h1 = f16_bits(v1), h2 = f16_bits(v2), h3 = f16_bits(v3);
     if (e0 + 3 < n && ((reinterpret_cast<uintptr_t>(y + e0) & 7) == 0)) {
-        *reinterpret_cast<uint2*>(y + e0) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+        __builtin_nontemporal_store(u32x2v{h0 | (h1 << 16), h2 | (h3 << 16)}, reinterpret_cast<u32x2v*>(y + e0));
     } else {
         if (e0 + 0 < n) y[e0 + 0] = (uint16_t)h0;
         if (e0 + 1 < n) y[e0 + 1] = (uint16_t)h1;
@@ -79,8 +87,9 @@ __device__ __forceinline__ void store8(uint16_t* __restrict__ y, int64_t e0, int
 #pragma unroll
     for (int c = 0; c < 8; ++c) h[c] = f16_bits(v[c]);
     if (e0 + 7 < n && ((reinterpret_cast<uintptr_t>(y + e0) & 15) == 0)) {
-        *reinterpret_cast<uint4*>(y + e0) =
-            make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+        __builtin_nontemporal_store(
+            u32x4v{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)},
+            reinterpret_cast<u32x4v*>(y + e0));
     } else {
 #pragma unroll
         for (int c = 0; c < 8; ++c)
