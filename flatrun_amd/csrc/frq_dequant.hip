@@ -36,8 +36,11 @@ namespace frq {
 
 // Output stores are non-temporal (`nt`): a dequantized matrix is written
 // once and not read again by this kernel, and streaming it past the caches
-// moves it at a far higher rate than ordinary write-allocating stores
-// (Q4_K 18944 x 3584 to fp32: 69-71 -> 40-41 us; fp16 40.5 -> 25-28 us).
+// saves 4-9 % against ordinary write-allocating stores, with weights and
+// outputs both cold (Q4_K 18944 x 3584 to fp32: 64.4 -> 61.3 us; Q6_K
+// 152064 x 3584: 521-524 -> 491-494 us; fp16 Q6_K 304 -> 290 us). The
+// stores also leave the last-level cache to the weights, so a weight that
+// is read again soon after (a few hundred MB of them) stays cached.
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
